@@ -1,0 +1,754 @@
+/*
+ * apus_backend.hip — C-ABI host side of the MI355X backend (include/apus_hip.h).
+ *
+ * Mirrors the structure of apus's Metal backend (c/backend_metal.mm:660-746):
+ * lazy device init, a hook table filled by enable, weight caches for the
+ * dense linears keyed by host pointer, per-op fail-soft (nonzero return =
+ * caller runs its CPU kernel). Differences that follow from MI355X:
+ *  - weights are copied once into HBM (discrete memory, no zero-copy);
+ *  - routed experts are cached by (layer, expert id) in an HBM-resident
+ *    store instead of by pointer, so evicted/reused host slabs never alias;
+ *  - everything runs on one HIP stream; host-pointer entry points stage
+ *    through device scratch and synchronise before returning.
+ */
+#include <hip/hip_runtime.h>
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/apus_hip.h"
+#include "apus_internal.h"
+#include "apus_numerics.h"
+
+/* ------------------------------------------------------------------ state */
+
+namespace {
+
+thread_local char g_err[512];
+
+void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+struct DevBuf {
+    void *p = nullptr;
+    size_t n = 0;
+};
+
+struct DenseW {        /* one cached dense weight (codes/packed + scales) */
+    const void *host_scales;
+    uint8_t *w, *ws;
+    size_t wbytes, sbytes;
+    uint64_t fp;
+};
+
+struct ExpertW {       /* one cached routed expert, six tensors */
+    uint8_t *p[6];
+    size_t bytes;
+};
+
+struct State {
+    bool enabled = false;
+    bool inited = false;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    std::unordered_map<const void *, DenseW> dense;
+    std::unordered_map<uint64_t, ExpertW> experts;
+    DevBuf scratch[8];
+    uint64_t bytes_uploaded = 0, bytes_resident = 0, dispatches = 0;
+    size_t dense_budget = 0;
+    ApusHipHooks hooks{};
+};
+
+State g;
+std::mutex g_mu;
+
+bool ok(hipError_t e, const char *what) {
+    if (e == hipSuccess) return true;
+    set_err("%s: %s", what, hipGetErrorString(e));
+    return false;
+}
+
+bool ensure_init() {
+    if (g.inited) return true;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        set_err("no HIP device visible");
+        return false;
+    }
+    hipDeviceProp_t prop;
+    if (!ok(hipGetDeviceProperties(&prop, 0), "hipGetDeviceProperties")) return false;
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        set_err("device 0 is %s, this backend is built for gfx950 only", prop.gcnArchName);
+        return false;
+    }
+    if (!ok(hipSetDevice(0), "hipSetDevice")) return false;
+    if (!ok(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking), "hipStreamCreate")) return false;
+    if (!ok(hipEventCreate(&g.ev0), "hipEventCreate")) return false;
+    if (!ok(hipEventCreate(&g.ev1), "hipEventCreate")) return false;
+    const char *mb = getenv("APUS_HIP_DENSE_MB");
+    g.dense_budget = (size_t)(mb ? strtoull(mb, nullptr, 10) : 131072ull) << 20;
+    g.inited = true;
+    return true;
+}
+
+/* grow-only device scratch slot i of at least n bytes */
+void *scratch(int i, size_t n) {
+    DevBuf &b = g.scratch[i];
+    if (b.n >= n && b.p) return b.p;
+    if (b.p) { hipStreamSynchronize(g.stream); hipFree(b.p); b.p = nullptr; b.n = 0; }
+    size_t want = n < 4096 ? 4096 : n;
+    if (!ok(hipMalloc(&b.p, want), "hipMalloc scratch")) return nullptr;
+    b.n = want;
+    return b.p;
+}
+
+bool upload(void *dst, const void *src, size_t n) {
+    return ok(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g.stream), "H2D");
+}
+
+bool download(void *dst, const void *src, size_t n) {
+    return ok(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g.stream), "D2H");
+}
+
+bool finish() { return ok(hipStreamSynchronize(g.stream), "hipStreamSynchronize"); }
+
+bool launched(hipError_t e, const char *what) {
+    g.dispatches++;
+    return ok(e, what);
+}
+
+/* 64-bit fingerprint of 16 words sampled across a host buffer (cheap; makes a
+ * freed-and-reused host address with new contents re-upload instead of
+ * silently reading the stale device copy) */
+uint64_t fingerprint(const uint8_t *p, size_t n) {
+    uint64_t h = 0xcbf29ce484222325ull ^ n;
+    for (int i = 0; i < 16; i++) {
+        uint64_t v = 0;
+        const size_t off = (n > 8) ? (size_t)((n - 8) * (uint64_t)i / 15) : 0;
+        memcpy(&v, p + off, n >= 8 ? 8 : n);
+        h = (h ^ v) * 0x100000001b3ull;
+    }
+    return h;
+}
+
+/* dense weight cache lookup/insert, keyed by the host weight pointer (the
+ * engine's weight pointers are stable, c/backend_metal.h:38-43); a hit whose
+ * shape, scale pointer or sampled contents changed is re-uploaded */
+const DenseW *dense_weight(const uint8_t *w, const uint8_t *ws, size_t wbytes,
+                           size_t sbytes) {
+    const uint64_t fp = fingerprint(w, wbytes) ^ (fingerprint(ws, sbytes) * 31);
+    auto it = g.dense.find(w);
+    if (it != g.dense.end()) {
+        DenseW &d = it->second;
+        if (d.host_scales == ws && d.wbytes == wbytes && d.sbytes == sbytes && d.fp == fp)
+            return &d;
+        (void)hipStreamSynchronize(g.stream);
+        (void)hipFree(d.w);
+        (void)hipFree(d.ws);
+        g.bytes_resident -= d.wbytes + d.sbytes;
+        g.dense.erase(it);
+    }
+    if (g.bytes_resident + wbytes + sbytes > g.dense_budget) {
+        set_err("dense weight budget exhausted (APUS_HIP_DENSE_MB)");
+        return nullptr;
+    }
+    DenseW d{ws, nullptr, nullptr, wbytes, sbytes, fp};
+    if (!ok(hipMalloc(&d.w, wbytes), "hipMalloc weight")) return nullptr;
+    if (!ok(hipMalloc(&d.ws, sbytes), "hipMalloc scales")) { hipFree(d.w); return nullptr; }
+    if (!upload(d.w, w, wbytes) || !upload(d.ws, ws, sbytes)) return nullptr;
+    g.bytes_uploaded += wbytes + sbytes;
+    g.bytes_resident += wbytes + sbytes;
+    return &(g.dense[w] = d);
+}
+
+bool shape_ok(int M, int K, int O) {
+    if (M <= 0 || O <= 0 || K <= 0 || (K % 128) != 0) {
+        set_err("unsupported shape M=%d K=%d O=%d (needs K %% 128 == 0)", M, K, O);
+        return false;
+    }
+    return true;
+}
+
+int gemm_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
+             const float *as, float *out, int M, int O, int K, int round_out) {
+    ApusGemmArgs a{};
+    a.acodes = acodes; a.ascale = as; a.ents = nullptr;
+    a.ent0.w = w; a.ent0.ws = ws; a.ent0.out = out;
+    a.ent0.arows = nullptr; a.ent0.orows = nullptr;
+    a.ent0.a0 = 0; a.ent0.o0 = 0; a.ent0.M = M;
+    a.O = O; a.K = K; a.ldo = O; a.round_out = round_out;
+    return launched(apus_launch_gemm(wfmt, &a, 1, g.stream), "gemm") ? 0 : 1;
+}
+
+/* host-pointer linear: stage x, quantise, GEMM, BF16 out, copy back */
+int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
+                float *out, int M, int K, int O) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init() || !shape_ok(M, K, O)) return 1;
+    const size_t wbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 2 : (size_t)O * K;
+    const size_t sbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 32
+                                             : (size_t)((O + 127) / 128) * (K / 128);
+    const DenseW *d = dense_weight(w, ws, wbytes, sbytes);
+    if (!d) return 1;
+    const size_t nab = K / 128;
+    float *dx = (float *)scratch(0, (size_t)M * K * 4);
+    uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
+    float *dsc = (float *)scratch(2, (size_t)M * nab * 4);
+    float *dout = (float *)scratch(3, (size_t)M * O * 4);
+    if (!dx || !dc || !dsc || !dout) return 1;
+    if (!upload(dx, x, (size_t)M * K * 4)) return 1;
+    if (!launched(apus_launch_act_quant(dx, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
+    if (gemm_dev(wfmt, d->w, d->ws, dc, dsc, dout, M, O, K, 1)) return 1;
+    if (!download(out, dout, (size_t)M * O * 4) || !finish()) return 1;
+    return 0;
+}
+
+int gemm_host(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
+              const float *as, float *out, int M, int O, int K) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init() || !shape_ok(M, K, O)) return 1;
+    const size_t wbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 2 : (size_t)O * K;
+    const size_t sbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 32
+                                             : (size_t)((O + 127) / 128) * (K / 128);
+    const size_t nab = K / 128;
+    uint8_t *dw = (uint8_t *)scratch(4, wbytes);
+    uint8_t *dws = (uint8_t *)scratch(5, sbytes);
+    uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
+    float *dsc = (float *)scratch(2, (size_t)M * nab * 4);
+    float *dout = (float *)scratch(3, (size_t)M * O * 4);
+    if (!dw || !dws || !dc || !dsc || !dout) return 1;
+    if (!upload(dw, w, wbytes) || !upload(dws, ws, sbytes) ||
+        !upload(dc, acodes, (size_t)M * K) || !upload(dsc, as, (size_t)M * nab * 4))
+        return 1;
+    if (gemm_dev(wfmt, dw, dws, dc, dsc, dout, M, O, K, 0)) return 1;
+    if (!download(out, dout, (size_t)M * O * 4) || !finish()) return 1;
+    return 0;
+}
+
+/* workspace carve-up for the routed dispatch */
+struct MoeWs {
+    uint8_t *xc; float *xs;
+    int32_t *pair, *tok;
+    ApusGemmEnt *e13, *e2;
+    float *gm, *um; uint8_t *hc; float *hs; float *eo;
+    uint8_t **tab;
+    size_t total;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
+    MoeWs w{};
+    const size_t nj = (size_t)s * topk;
+    size_t off = 0;
+    auto take = [&](size_t n) { size_t o = off; off += align256(n); return o; };
+    size_t o_xc = take((size_t)s * dim), o_xs = take((size_t)s * (dim / 128) * 4);
+    size_t o_pair = take(nj * 4), o_tok = take(nj * 4);
+    size_t o_e13 = take(2 * (size_t)E * sizeof(ApusGemmEnt)), o_e2 = take((size_t)E * sizeof(ApusGemmEnt));
+    size_t o_g = take(nj * inter * 4), o_u = take(nj * inter * 4);
+    size_t o_hc = take(nj * inter), o_hs = take(nj * (inter / 128) * 4);
+    size_t o_eo = take(nj * dim * 4);
+    size_t o_tab = take(6 * (size_t)E * sizeof(void *));
+    w.total = off;
+    if (base) {
+        uint8_t *b = (uint8_t *)base;
+        w.xc = b + o_xc; w.xs = (float *)(b + o_xs);
+        w.pair = (int32_t *)(b + o_pair); w.tok = (int32_t *)(b + o_tok);
+        w.e13 = (ApusGemmEnt *)(b + o_e13); w.e2 = (ApusGemmEnt *)(b + o_e2);
+        w.gm = (float *)(b + o_g); w.um = (float *)(b + o_u);
+        w.hc = b + o_hc; w.hs = (float *)(b + o_hs); w.eo = (float *)(b + o_eo);
+        w.tab = (uint8_t **)(b + o_tab);
+    }
+    return w;
+}
+
+/* the routed-dispatch pipeline on device data; tab = 6 device arrays of E
+ * pointers (w1, w1s, w2, w2s, w3, w3s) */
+int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
+                 const float *x, const int32_t *idx, const float *wgt, int s,
+                 int topk, float *y, const MoeWs &w) {
+    const int nj = s * topk;
+    ApusExpertTable t;
+    t.w1 = tab; t.w1s = tab + E; t.w2 = tab + 2 * E; t.w2s = tab + 3 * E;
+    t.w3 = tab + 4 * E; t.w3s = tab + 5 * E;
+    if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, w.xc, w.xs, g.stream), "act_quant"))
+        return 1;
+    if (!launched(apus_launch_moe_route(idx, nj, topk, E, t, w.gm, w.um, w.eo, inter, dim,
+                                        w.pair, w.tok, w.e13, w.e2, g.stream), "moe_route"))
+        return 1;
+    ApusGemmArgs a{};
+    a.acodes = w.xc; a.ascale = w.xs; a.ents = w.e13;
+    a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
+    if (!launched(apus_launch_gemm(APUS_W_FP4, &a, 2 * E, g.stream), "gemm w1/w3")) return 1;
+    if (!launched(apus_launch_swiglu_quant(w.gm, w.um, nj, inter, limit, w.hc, w.hs, g.stream),
+                  "swiglu_quant"))
+        return 1;
+    ApusGemmArgs b{};
+    b.acodes = w.hc; b.ascale = w.hs; b.ents = w.e2;
+    b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
+    if (!launched(apus_launch_gemm(APUS_W_FP4, &b, E, g.stream), "gemm w2")) return 1;
+    if (!launched(apus_launch_moe_accum(w.eo, wgt, s, topk, dim, y, g.stream), "moe_accum"))
+        return 1;
+    return 0;
+}
+
+}  // namespace
+
+/* ---------------------------------------------------------- store type */
+
+struct ApusHipStore {
+    int L, E, dim, inter;
+    size_t sz[6];          /* bytes of w1, w1s, w2, w2s, w3, w3s */
+    size_t expert_bytes;   /* 256-aligned slab per expert */
+    std::vector<uint8_t *> layer_base;   /* one allocation per layer */
+    std::vector<uint8_t **> layer_tab;   /* device pointer tables, 6*E each */
+};
+
+/* ============================================================== C ABI */
+
+extern "C" {
+
+int apus_hip_enable(char *err, size_t errcap) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init()) {
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        return -1;
+    }
+    g.hooks.fp8_linear = apus_hip_fp8_linear;
+    g.hooks.f32_linear = nullptr;
+    g.hooks.head_gemv = nullptr;
+    g.hooks.fp4_linear = apus_hip_fp4_linear;
+    g.hooks.fp4_gemm_grouped = apus_hip_fp4_gemm_grouped;
+    g.hooks.moe_routed = apus_hip_moe_routed;
+    g.enabled = true;
+    return 0;
+}
+
+void apus_hip_disable(void) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g.inited) return;
+    hipStreamSynchronize(g.stream);
+    for (auto &kv : g.dense) { hipFree(kv.second.w); hipFree(kv.second.ws); }
+    g.dense.clear();
+    for (auto &kv : g.experts) hipFree(kv.second.p[0]);
+    g.experts.clear();
+    for (auto &b : g.scratch) { if (b.p) hipFree(b.p); b.p = nullptr; b.n = 0; }
+    g.bytes_resident = 0;
+    g.hooks = ApusHipHooks{};
+    g.enabled = false;
+}
+
+int apus_hip_is_enabled(void) { return g.enabled ? 1 : 0; }
+const ApusHipHooks *apus_hip_hooks(void) { return &g.hooks; }
+uint64_t apus_hip_bytes_uploaded(void) { return g.bytes_uploaded; }
+uint64_t apus_hip_bytes_resident(void) { return g.bytes_resident; }
+uint64_t apus_hip_dispatches(void) { return g.dispatches; }
+const char *apus_hip_last_error(void) { return g_err; }
+
+int apus_hip_fp8_linear(const ApusFp8W *w, const float *x, float *out, int M, int K, int O) {
+    if (!w || w->O != O || w->K != K) { set_err("fp8_linear: weight shape mismatch"); return 1; }
+    return linear_host(APUS_W_FP8, w->codes, w->scales, x, out, M, K, O);
+}
+
+int apus_hip_fp4_linear(const ApusFp4W *w, const float *x, float *out, int M, int K, int O) {
+    if (!w || w->O != O || w->K != K) { set_err("fp4_linear: weight shape mismatch"); return 1; }
+    return linear_host(APUS_W_FP4, w->packed, w->scales, x, out, M, K, O);
+}
+
+int apus_hip_act_quant(const float *x, int M, int K, uint8_t *codes, float *scales) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init() || !shape_ok(M, K, 1)) return 1;
+    const size_t nab = K / 128;
+    float *dx = (float *)scratch(0, (size_t)M * K * 4);
+    uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
+    float *dsc = (float *)scratch(2, (size_t)M * nab * 4);
+    if (!dx || !dc || !dsc) return 1;
+    if (!upload(dx, x, (size_t)M * K * 4)) return 1;
+    if (!launched(apus_launch_act_quant(dx, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
+    if (!download(codes, dc, (size_t)M * K) || !download(scales, dsc, (size_t)M * nab * 4) || !finish())
+        return 1;
+    return 0;
+}
+
+int apus_hip_fp4_gemm(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
+                      const float *as, float *out, int M, int O, int K) {
+    return gemm_host(APUS_W_FP4, w, ws, acodes, as, out, M, O, K);
+}
+
+int apus_hip_fp8_gemm(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
+                      const float *as, float *out, int M, int O, int K) {
+    return gemm_host(APUS_W_FP8, w, ws, acodes, as, out, M, O, K);
+}
+
+int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent, const uint8_t *acodes,
+                              const float *as, size_t O, size_t K) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init()) return 1;
+    if (!n_ent) return 0;
+    if (!shape_ok(1, (int)K, (int)O)) return 1;
+    size_t rows = 0, outrows = 0;
+    for (size_t i = 0; i < n_ent; i++) {
+        if (ents[i].m0 + ents[i].M > rows) rows = ents[i].m0 + ents[i].M;
+        outrows += ents[i].M;
+    }
+    const size_t nab = K / 128;
+    uint8_t *dc = (uint8_t *)scratch(1, rows * K + 1);
+    float *dsc = (float *)scratch(2, rows * nab * 4 + 4);
+    float *dout = (float *)scratch(3, outrows * O * 4 + 4);
+    ApusGemmEnt *dents = (ApusGemmEnt *)scratch(6, n_ent * sizeof(ApusGemmEnt));
+    if (!dc || !dsc || !dout || !dents) return 1;
+    if (!upload(dc, acodes, rows * K) || !upload(dsc, as, rows * nab * 4)) return 1;
+    std::vector<ApusGemmEnt> he(n_ent);
+    size_t orow = 0;
+    for (size_t i = 0; i < n_ent; i++) {
+        const DenseW *d = dense_weight(ents[i].w, ents[i].ws, O * K / 2, O * K / 32);
+        if (!d) return 1;
+        he[i] = ApusGemmEnt{d->w, d->ws, dout, nullptr, nullptr, (int32_t)ents[i].m0,
+                            (int32_t)orow, (int32_t)ents[i].M, 0};
+        orow += ents[i].M;
+    }
+    if (!upload(dents, he.data(), n_ent * sizeof(ApusGemmEnt))) return 1;
+    ApusGemmArgs a{};
+    a.acodes = dc; a.ascale = dsc; a.ents = dents;
+    a.O = (int)O; a.K = (int)K; a.ldo = (int)O; a.round_out = 0;
+    if (!launched(apus_launch_gemm(APUS_W_FP4, &a, (int)n_ent, g.stream), "grouped gemm")) return 1;
+    orow = 0;
+    for (size_t i = 0; i < n_ent; i++) {
+        if (ents[i].M && !download(ents[i].out, dout + orow * O, ents[i].M * O * 4)) return 1;
+        orow += ents[i].M;
+    }
+    return finish() ? 0 : 1;
+}
+
+int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, const float *wgt,
+                        int s, float *y) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init()) return 1;
+    if (!w || s <= 0) { set_err("moe_routed: bad arguments"); return 1; }
+    const int E = w->E, topk = w->topk, dim = w->dim, inter = w->inter;
+    if (E <= 0 || topk <= 0 || dim % 128 || inter % 128 || dim <= 0 || inter <= 0) {
+        set_err("moe_routed: unsupported shape E=%d dim=%d inter=%d", E, dim, inter);
+        return 1;
+    }
+    const int nj = s * topk;
+    for (int q = 0; q < nj; q++)
+        if (idx[q] < 0 || idx[q] >= E) { set_err("moe_routed: expert id out of range"); return 1; }
+    /* resident expert slabs keyed by (layer, eid) */
+    std::vector<uint8_t *> tab(6 * (size_t)E, nullptr);
+    const size_t sz[6] = {(size_t)inter * dim / 2, (size_t)inter * dim / 32,
+                          (size_t)dim * inter / 2, (size_t)dim * inter / 32,
+                          (size_t)inter * dim / 2, (size_t)inter * dim / 32};
+    for (int q = 0; q < nj; q++) {
+        const int e = idx[q];
+        if (tab[e]) continue;
+        const uint64_t key = ((uint64_t)(uint32_t)w->layer_id << 32) | (uint32_t)e;
+        auto it = g.experts.find(key);
+        if (it == g.experts.end()) {
+            ApusFp4W r1, r2, r3;
+            if (w->hook_resolve) {
+                if (w->hook_resolve(w->hook_ctx, w->layer_id, e, &r1, &r2, &r3)) {
+                    set_err("moe_routed: expert resolve failed");
+                    return 1;
+                }
+            } else {
+                r1 = w->w1[e]; r2 = w->w2[e]; r3 = w->w3[e];
+            }
+            const void *src[6] = {r1.packed, r1.scales, r2.packed, r2.scales, r3.packed, r3.scales};
+            ExpertW ew{};
+            size_t tot = 0;
+            for (int i = 0; i < 6; i++) tot += align256(sz[i]);
+            uint8_t *base = nullptr;
+            if (!ok(hipMalloc(&base, tot), "hipMalloc expert")) return 1;
+            size_t off = 0;
+            for (int i = 0; i < 6; i++) {
+                ew.p[i] = base + off;
+                if (!upload(ew.p[i], src[i], sz[i])) return 1;
+                off += align256(sz[i]);
+            }
+            ew.bytes = tot;
+            g.bytes_uploaded += tot;
+            g.bytes_resident += tot;
+            it = g.experts.emplace(key, ew).first;
+        }
+        for (int i = 0; i < 6; i++) tab[(size_t)i * E + e] = it->second.p[i];
+    }
+    MoeWs sizes = moe_carve(nullptr, s, topk, E, dim, inter);
+    void *ws = scratch(7, sizes.total);
+    float *dx = (float *)scratch(0, (size_t)s * dim * 4);
+    int32_t *didx = (int32_t *)scratch(1, (size_t)nj * 4 + (size_t)nj * 4);
+    float *dwgt = (float *)((uint8_t *)didx + (size_t)nj * 4);
+    float *dy = (float *)scratch(3, (size_t)s * dim * 4);
+    if (!ws || !dx || !didx || !dy) return 1;
+    MoeWs mw = moe_carve(ws, s, topk, E, dim, inter);
+    if (!upload(mw.tab, tab.data(), tab.size() * sizeof(void *)) ||
+        !upload(dx, x, (size_t)s * dim * 4) || !upload(didx, idx, (size_t)nj * 4) ||
+        !upload(dwgt, wgt, (size_t)nj * 4))
+        return 1;
+    if (moe_pipeline(E, dim, inter, w->limit, mw.tab, dx, didx, dwgt, s, topk, dy, mw)) return 1;
+    if (!download(y, dy, (size_t)s * dim * 4) || !finish()) return 1;
+    return 0;
+}
+
+/* ---------------------------------------------------- device entry points */
+
+int apus_hip_act_quant_dev(const float *x, int M, int K, uint8_t *codes, float *scales) {
+    if (!ensure_init() || !shape_ok(M, K, 1)) return 1;
+    return launched(apus_launch_act_quant(x, K, nullptr, M, K, codes, scales, g.stream), "act_quant") ? 0 : 1;
+}
+
+int apus_hip_fp4_gemm_dev(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
+                          const float *as, float *out, int M, int O, int K, int round_out) {
+    if (!ensure_init() || !shape_ok(M, K, O)) return 1;
+    return gemm_dev(APUS_W_FP4, w, ws, acodes, as, out, M, O, K, round_out);
+}
+
+int apus_hip_fp8_gemm_dev(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
+                          const float *as, float *out, int M, int O, int K, int round_out) {
+    if (!ensure_init() || !shape_ok(M, K, O)) return 1;
+    return gemm_dev(APUS_W_FP8, w, ws, acodes, as, out, M, O, K, round_out);
+}
+
+size_t apus_hip_linear_workspace(int M, int K) {
+    return align256((size_t)M * K) + align256((size_t)M * (K / 128) * 4);
+}
+
+static int linear_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x, float *out,
+                      int M, int K, int O, void *workspace) {
+    if (!ensure_init() || !shape_ok(M, K, O)) return 1;
+    if (!workspace) { set_err("linear_dev: workspace required"); return 1; }
+    uint8_t *dc = (uint8_t *)workspace;
+    float *dsc = (float *)(dc + align256((size_t)M * K));
+    if (!launched(apus_launch_act_quant(x, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
+    return gemm_dev(wfmt, w, ws, dc, dsc, out, M, O, K, 1);
+}
+
+int apus_hip_fp4_linear_dev(const uint8_t *w, const uint8_t *ws, const float *x, float *out,
+                            int M, int K, int O, void *workspace) {
+    return linear_dev(APUS_W_FP4, w, ws, x, out, M, K, O, workspace);
+}
+
+int apus_hip_fp8_linear_dev(const uint8_t *w, const uint8_t *ws, const float *x, float *out,
+                            int M, int K, int O, void *workspace) {
+    return linear_dev(APUS_W_FP8, w, ws, x, out, M, K, O, workspace);
+}
+
+/* ------------------------------------------------------------- the store */
+
+ApusHipStore *apus_hip_store_create(int n_layers, int E, int dim, int inter, char *err,
+                                    size_t errcap) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init() || n_layers <= 0 || E <= 0 || dim % 128 || inter % 128) {
+        if (g_err[0] == 0) set_err("store_create: bad arguments");
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        return nullptr;
+    }
+    ApusHipStore *st = new ApusHipStore();
+    st->L = n_layers; st->E = E; st->dim = dim; st->inter = inter;
+    const size_t sz[6] = {(size_t)inter * dim / 2, (size_t)inter * dim / 32,
+                          (size_t)dim * inter / 2, (size_t)dim * inter / 32,
+                          (size_t)inter * dim / 2, (size_t)inter * dim / 32};
+    st->expert_bytes = 0;
+    for (int i = 0; i < 6; i++) { st->sz[i] = sz[i]; st->expert_bytes += align256(sz[i]); }
+    for (int l = 0; l < n_layers; l++) {
+        uint8_t *base = nullptr;
+        uint8_t **tab = nullptr;
+        if (hipMalloc(&base, st->expert_bytes * E) != hipSuccess ||
+            hipMalloc(&tab, 6 * (size_t)E * sizeof(void *)) != hipSuccess) {
+            set_err("store_create: HBM exhausted at layer %d", l);
+            if (err && errcap) snprintf(err, errcap, "%s", g_err);
+            if (base) hipFree(base);
+            for (size_t i = 0; i < st->layer_base.size(); i++) {
+                hipFree(st->layer_base[i]); hipFree(st->layer_tab[i]);
+            }
+            delete st;
+            return nullptr;
+        }
+        std::vector<uint8_t *> h(6 * (size_t)E);
+        for (int e = 0; e < E; e++) {
+            size_t off = 0;
+            for (int i = 0; i < 6; i++) {
+                h[(size_t)i * E + e] = base + st->expert_bytes * e + off;
+                off += align256(sz[i]);
+            }
+        }
+        hipMemcpy(tab, h.data(), h.size() * sizeof(void *), hipMemcpyHostToDevice);
+        st->layer_base.push_back(base);
+        st->layer_tab.push_back(tab);
+    }
+    g.bytes_resident += st->expert_bytes * E * n_layers;
+    return st;
+}
+
+void apus_hip_store_free(ApusHipStore *st) {
+    if (!st) return;
+    std::lock_guard<std::mutex> lk(g_mu);
+    hipStreamSynchronize(g.stream);
+    for (size_t i = 0; i < st->layer_base.size(); i++) {
+        hipFree(st->layer_base[i]);
+        hipFree(st->layer_tab[i]);
+    }
+    g.bytes_resident -= st->expert_bytes * st->E * st->L;
+    delete st;
+}
+
+uint64_t apus_hip_store_bytes(const ApusHipStore *st) {
+    return st ? (uint64_t)st->expert_bytes * st->E * st->L : 0;
+}
+
+int apus_hip_store_fill_random(ApusHipStore *st, uint64_t seed) {
+    if (!st) return 1;
+    static const int kinds[6] = {0, 1, 0, 1, 0, 1};
+    for (int l = 0; l < st->L; l++)
+        for (int e = 0; e < st->E; e++) {
+            size_t off = 0;
+            for (int i = 0; i < 6; i++) {
+                uint8_t *p = st->layer_base[l] + st->expert_bytes * e + off;
+                const uint64_t sid = ((uint64_t)l * st->E + e) * 8 + i;
+                if (!launched(apus_launch_fill(p, st->sz[i], seed, sid, 0, kinds[i], g.stream), "fill"))
+                    return 1;
+                off += align256(st->sz[i]);
+            }
+        }
+    return finish() ? 0 : 1;
+}
+
+int apus_hip_store_put(ApusHipStore *st, int layer, int eid, const ApusFp4W *w1,
+                       const ApusFp4W *w2, const ApusFp4W *w3) {
+    if (!st || layer < 0 || layer >= st->L || eid < 0 || eid >= st->E) return 1;
+    const void *src[6] = {w1->packed, w1->scales, w2->packed, w2->scales, w3->packed, w3->scales};
+    size_t off = 0;
+    for (int i = 0; i < 6; i++) {
+        uint8_t *p = st->layer_base[layer] + st->expert_bytes * eid + off;
+        if (!upload(p, src[i], st->sz[i])) return 1;
+        g.bytes_uploaded += st->sz[i];
+        off += align256(st->sz[i]);
+    }
+    return finish() ? 0 : 1;
+}
+
+int apus_hip_store_get(const ApusHipStore *st, int layer, int eid, const uint8_t *ptrs[6]) {
+    if (!st || layer < 0 || layer >= st->L || eid < 0 || eid >= st->E) return 1;
+    size_t off = 0;
+    for (int i = 0; i < 6; i++) {
+        ptrs[i] = st->layer_base[layer] + st->expert_bytes * eid + off;
+        off += align256(st->sz[i]);
+    }
+    return 0;
+}
+
+size_t apus_hip_moe_workspace(const ApusHipStore *st, int s, int topk) {
+    if (!st) return 0;
+    return moe_carve(nullptr, s, topk, st->E, st->dim, st->inter).total;
+}
+
+int apus_hip_moe_routed_dev(const ApusHipStore *st, int layer, const float *x, const int32_t *idx,
+                            const float *wgt, int s, int topk, float limit, float *y,
+                            void *workspace) {
+    if (!st || layer < 0 || layer >= st->L || s <= 0 || topk <= 0 || !workspace) {
+        set_err("moe_routed_dev: bad arguments");
+        return 1;
+    }
+    MoeWs mw = moe_carve(workspace, s, topk, st->E, st->dim, st->inter);
+    return moe_pipeline(st->E, st->dim, st->inter, limit, st->layer_tab[layer], x, idx, wgt, s,
+                        topk, y, mw);
+}
+
+/* --------------------------------------------------------------- helpers */
+
+void *apus_hip_malloc(size_t bytes) {
+    if (!ensure_init()) return nullptr;
+    void *p = nullptr;
+    if (!ok(hipMalloc(&p, bytes ? bytes : 1), "hipMalloc")) return nullptr;
+    return p;
+}
+
+int apus_hip_free(void *p) { return ok(hipFree(p), "hipFree") ? 0 : 1; }
+
+int apus_hip_h2d(void *dst, const void *src, size_t bytes) {
+    if (!ensure_init()) return 1;
+    return upload(dst, src, bytes) && finish() ? 0 : 1;
+}
+
+int apus_hip_d2h(void *dst, const void *src, size_t bytes) {
+    if (!ensure_init()) return 1;
+    return download(dst, src, bytes) && finish() ? 0 : 1;
+}
+
+int apus_hip_memset(void *dst, int value, size_t bytes) {
+    if (!ensure_init()) return 1;
+    return ok(hipMemsetAsync(dst, value, bytes, g.stream), "hipMemsetAsync") ? 0 : 1;
+}
+
+int apus_hip_fill_random(void *dst, size_t bytes, uint64_t seed, uint64_t stream_id, int kind) {
+    if (!ensure_init()) return 1;
+    return launched(apus_launch_fill((uint8_t *)dst, bytes, seed, stream_id, 0, kind, g.stream),
+                    "fill") ? 0 : 1;
+}
+
+int apus_hip_synchronize(void) {
+    if (!ensure_init()) return 1;
+    return finish() ? 0 : 1;
+}
+
+int apus_hip_timer_start(void) {
+    if (!ensure_init()) return 1;
+    return ok(hipEventRecord(g.ev0, g.stream), "hipEventRecord") ? 0 : 1;
+}
+
+float apus_hip_timer_stop(void) {
+    if (!ensure_init()) return -1.0f;
+    if (!ok(hipEventRecord(g.ev1, g.stream), "hipEventRecord")) return -1.0f;
+    if (!ok(hipEventSynchronize(g.ev1), "hipEventSynchronize")) return -1.0f;
+    float ms = 0.0f;
+    if (!ok(hipEventElapsedTime(&ms, g.ev0, g.ev1), "hipEventElapsedTime")) return -1.0f;
+    return ms;
+}
+
+int apus_hip_graph_begin(void) {
+    if (!ensure_init()) return 1;
+    if (g.graph_exec) { (void)hipGraphExecDestroy(g.graph_exec); g.graph_exec = nullptr; }
+    if (g.graph) { (void)hipGraphDestroy(g.graph); g.graph = nullptr; }
+    return ok(hipStreamBeginCapture(g.stream, hipStreamCaptureModeThreadLocal),
+              "hipStreamBeginCapture") ? 0 : 1;
+}
+
+int apus_hip_graph_end(void) {
+    if (!ensure_init()) return 1;
+    if (!ok(hipStreamEndCapture(g.stream, &g.graph), "hipStreamEndCapture")) return 1;
+    return ok(hipGraphInstantiate(&g.graph_exec, g.graph, nullptr, nullptr, 0),
+              "hipGraphInstantiate") ? 0 : 1;
+}
+
+int apus_hip_graph_replay(int times) {
+    if (!ensure_init() || !g.graph_exec) { set_err("graph_replay: no captured graph"); return 1; }
+    for (int i = 0; i < times; i++)
+        if (!ok(hipGraphLaunch(g.graph_exec, g.stream), "hipGraphLaunch")) return 1;
+    return 0;
+}
+
+int apus_hip_device_info(char *name, size_t cap, int *cus) {
+    if (!ensure_init()) return 1;
+    hipDeviceProp_t prop;
+    if (!ok(hipGetDeviceProperties(&prop, 0), "hipGetDeviceProperties")) return 1;
+    if (name && cap) snprintf(name, cap, "%s %s", prop.name, prop.gcnArchName);
+    if (cus) *cus = prop.multiProcessorCount;
+    return 0;
+}
+
+float apus_hip_host_bf16_round(float x) { return apus_bf16_rne(x); }
+uint8_t apus_hip_host_e4m3_quant(float x) { return (uint8_t)apus_e4m3_code(x); }
+float apus_hip_host_act_scale(float amax) { return apus_pow2_from_exp(apus_act_scale_exp(amax)); }
+
+}  // extern "C"

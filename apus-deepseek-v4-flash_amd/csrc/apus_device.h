@@ -1,0 +1,58 @@
+/*
+ * apus_device.h — gfx950 building blocks for the HIP backend: the
+ * block-scaled F8F6F4 MFMA wrapper, 128-bit loads, wave reductions.
+ *
+ * MFMA operand layout (v_mfma_scale_f32_16x16x128_f8f6f4, CDNA4): lane l
+ * holds row (l % 16) of A and column (l % 16) of B, and within that row /
+ * column the 32 consecutive K elements of sub-block (l / 16); each lane also
+ * supplies the E8M0 scale of its own 32-element sub-block (one byte of a
+ * 32-bit register, picked by op_sel). FP8 operands take 32 bytes per lane,
+ * FP4 operands 16 bytes (two E2M1 per byte, low nibble first). The result
+ * D[i][j] = sum_k A[i][k] B[k][j] lands in lane l as D[4*(l/16) + q][l % 16],
+ * q = 0..3. The K order inside one instruction is irrelevant to the result
+ * set, so the kernels are free to choose which 32-element groups of the
+ * reduction dimension feed which lane group.
+ */
+#ifndef APUS_DEVICE_H
+#define APUS_DEVICE_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "apus_numerics.h"
+
+typedef int   apus_v8i __attribute__((ext_vector_type(8)));
+typedef float apus_v4f __attribute__((ext_vector_type(4)));
+
+/* operand format codes of the F8F6F4 MFMA (cbsz for A, blgp for B) */
+#define APUS_FMT_E4M3 0
+#define APUS_FMT_E2M1 4
+
+/* One 16x16x128 block-scaled MFMA. AF/BF: operand formats; SA/SB: which byte
+ * of the scale registers holds this lane's E8M0 scale. */
+template <int AF, int BF, int SA, int SB>
+__device__ __forceinline__ apus_v4f apus_mfma_scaled(apus_v8i a, apus_v8i b,
+                                                     apus_v4f c, int sa, int sb) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, AF, BF, SA, sa, SB, sb);
+}
+
+__device__ __forceinline__ uint4 apus_ld16(const uint8_t *p) {
+    return *reinterpret_cast<const uint4 *>(p);
+}
+
+typedef unsigned apus_v4u __attribute__((ext_vector_type(4)));
+
+/* streamed (read-once) 16-byte load: one global_load_dwordx4 with the
+ * non-temporal hint, so weight slabs do not evict the activations that
+ * every workgroup re-reads */
+__device__ __forceinline__ apus_v4u apus_ld16_stream(const uint8_t *p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const apus_v4u *>(p));
+}
+
+__device__ __forceinline__ float apus_wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+#endif /* APUS_DEVICE_H */

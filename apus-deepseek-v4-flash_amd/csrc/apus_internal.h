@@ -1,0 +1,84 @@
+/*
+ * apus_internal.h — launchers shared between the kernel translation unit and
+ * the C-ABI backend. Not part of the public interface (include/apus_hip.h).
+ * All launchers are asynchronous on the given stream and take device
+ * pointers only.
+ */
+#ifndef APUS_INTERNAL_H
+#define APUS_INTERNAL_H
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+/* weight formats of the block-scaled GEMM */
+enum { APUS_W_FP4 = 0, APUS_W_FP8 = 1 };
+
+/* One GEMM of a (possibly grouped) launch. Output row m of this entry is
+ *   out[orow(m) * ldo + o] = sum_k A[arow(m), k] * W[o, k]   (o < O)
+ * with arow(m) = arows ? arows[m] : a0 + m, orow(m) = orows ? orows[m] : o0 + m.
+ * W: FP4 [O, K/2] packed + [O, K/32] E8M0, or FP8 [O, K] + [ceil(O/128), K/128]
+ * E8M0 tiles. A: E4M3 codes [*, K] with fp32 power-of-two scales [*, K/128]. */
+typedef struct {
+    const uint8_t *w, *ws;
+    float *out;
+    const int32_t *arows, *orows;
+    int32_t a0, o0, M, pad;
+} ApusGemmEnt;
+
+typedef struct {
+    const uint8_t *acodes;   /* [rows, K] */
+    const float *ascale;     /* [rows, K/128] */
+    const ApusGemmEnt *ents; /* grouped: device array; else NULL */
+    ApusGemmEnt ent0;        /* the entry when ents == NULL */
+    int O, K, ldo, round_out;
+} ApusGemmArgs;
+
+/* y[m] = A x W^T for every entry; n_ent entries (1 with ents == NULL). */
+hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
+                            hipStream_t st);
+
+/* BF16 round + per-128 E4M3 act quant of rows of x (row stride ldx floats);
+ * arows optional gather. codes [M, K], scales [M, K/128]. K % 128 == 0. */
+hipError_t apus_launch_act_quant(const float *x, int ldx, const int32_t *arows,
+                                 int M, int K, uint8_t *codes, float *scales,
+                                 hipStream_t st);
+
+/* h = bf16(silu(clamp g) * clamp u) then act quant of h (no extra bf16 step
+ * needed: h is already bf16). g, u, codes: [M, N]; scales [M, N/128]. */
+hipError_t apus_launch_swiglu_quant(const float *g, const float *u, int M,
+                                    int N, float limit, uint8_t *codes,
+                                    float *scales, hipStream_t st);
+
+/* Counting sort of the routed pairs by expert and GEMM entry tables.
+ * idx [nj] (nj = s * topk) expert ids; writes pair_sorted [nj] (pair q),
+ * tok_sorted [nj] (q / topk), and entry tables e13 [2E] (w1 then w3, output
+ * rows in sorted order), e2 [E] (output rows = pair ids). The weight
+ * pointer tables are device arrays of E pointers each. */
+typedef struct {
+    const uint8_t *const *w1, *const *w1s, *const *w2, *const *w2s,
+                  *const *w3, *const *w3s;
+} ApusExpertTable;
+
+hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
+                                 ApusExpertTable tab, float *g, float *u,
+                                 float *eo, int inter, int dim,
+                                 int32_t *pair_sorted, int32_t *tok_sorted,
+                                 ApusGemmEnt *e13, ApusGemmEnt *e2,
+                                 hipStream_t st);
+
+/* y[t, i] = sum_j wgt[t, j] * eo[t*topk + j, i] in j order (mul, then add,
+ * each rounded), starting from +0. */
+hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,
+                                 int topk, int dim, float *y, hipStream_t st);
+
+/* Counter-based fill (kind as orc_fill_bytes: 0 uniform byte, 1 E8M0
+ * 118..130, 2 E4M3 of ~N(0,1), 3 E8M0 117..123). */
+hipError_t apus_launch_fill(uint8_t *dst, size_t n, uint64_t seed,
+                            uint64_t stream_id, uint64_t first, int kind,
+                            hipStream_t st);
+
+/* elementwise BF16 rounding in place */
+hipError_t apus_launch_bf16_round(float *v, size_t n, hipStream_t st);
+
+#endif /* APUS_INTERNAL_H */

@@ -1,0 +1,388 @@
+/*
+ * apus_kernels.hip — gfx950 kernels of the HIP backend.
+ *
+ *  - act quant: BF16 round + per-128 E4M3 quantisation, one wave per
+ *    128-element group (c/attn.h:393-403, c/fp4.h:293-321), bit-exact.
+ *  - block-scaled GEMM on F8F6F4 MFMA: E4M3 activations against MXFP4 or
+ *    FP8-E4M3 weights (c/fp4.h:367-395, c/fp8.h:191-218), grouped over
+ *    expert entries with gather/scatter row tables (c/fp4.h:936-986).
+ *  - SwiGLU + act quant of h (c/moe.h:113-126 followed by the act quant of
+ *    the w2 input, c/moe.h:309-314), one wave per 128 group.
+ *  - routed-pair counting sort and GEMM entry tables (c/moe.h:465-474).
+ *  - (t, j)-ordered weighted accumulation (c/moe.h:148-158).
+ *  - counter-based weight fill for HBM-resident synthetic experts.
+ */
+#include "apus_device.h"
+#include "apus_internal.h"
+
+/* ------------------------------------------------------------ act quant */
+
+/* One wave per (row, 128-group): two elements per lane. */
+__global__ __launch_bounds__(256) void apus_act_quant_kernel(
+    const float *__restrict__ x, int ldx, const int32_t *__restrict__ arows,
+    int M, int K, uint8_t *__restrict__ codes, float *__restrict__ scales) {
+    const int nab = K >> 7;
+    const int gid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (gid >= M * nab) return;
+    const int m = gid / nab, b = gid - m * nab;
+    const int src = arows ? arows[m] : m;
+    const float2 v = *reinterpret_cast<const float2 *>(x + (size_t)src * ldx + b * 128 + lane * 2);
+    const float v0 = apus_bf16_rne(v.x), v1 = apus_bf16_rne(v.y);
+    const float amax = apus_wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+    const uint32_t e = apus_act_scale_exp(amax);
+    const float inv = apus_inv_pow2_from_exp(e);
+    const uint32_t c0 = apus_e4m3_code(v0 * inv), c1 = apus_e4m3_code(v1 * inv);
+    *reinterpret_cast<uint16_t *>(codes + (size_t)m * K + b * 128 + lane * 2) =
+        (uint16_t)(c0 | (c1 << 8));
+    if (lane == 0) scales[(size_t)m * nab + b] = apus_pow2_from_exp(e);
+}
+
+hipError_t apus_launch_act_quant(const float *x, int ldx, const int32_t *arows,
+                                 int M, int K, uint8_t *codes, float *scales,
+                                 hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    const int groups = M * (K >> 7);
+    hipLaunchKernelGGL(apus_act_quant_kernel, dim3((groups + 3) / 4), dim3(256), 0, st,
+                       x, ldx, arows, M, K, codes, scales);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------ block-scaled GEMM */
+
+/*
+ * Tiling. A workgroup owns 16 consecutive weight rows (the 16 MFMA columns)
+ * of one entry and all of that entry's rows (tokens) in tiles of 16. The
+ * reduction dimension is cut into slices of 512; slice s belongs to wave
+ * s % waves, so the waves of a workgroup split K and their partial 16x16
+ * tiles are summed through LDS in a fixed wave order (the result does not
+ * depend on timing, nor on M or on the position of a row in the entry).
+ *
+ * One MFMA covers exactly one 128-element K group (group q = 4s + step), so
+ * the activation scale and, for FP8, the 128x128 weight tile scale are the
+ * same for all 32-element blocks of the instruction. Operand placement
+ * (measured on gfx950): an E4M3 operand lane of lane group g holds K
+ * [16g, 16g+16) in bytes 0..15 and [64+16g, +16) in bytes 16..31; an E2M1
+ * operand lane holds the contiguous K [32g, 32g+32); the E8M0 scale of
+ * (row r, 32-block b) is taken from lane 16b + r. Hence per step:
+ *   A (E4M3 codes) lane g: bytes [q*128 + 16g, +16) and [q*128 + 64 + 16g, +16)
+ *   B E4M3 weights: the same two 16-byte pieces of weight row o
+ *   B E2M1 weights: bytes [q*64 + 16g, +16) of row o, scale byte 4q + g
+ * which makes each instruction read 64 contiguous bytes per weight row.
+ */
+template <int WF, bool GROUPED>
+__global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
+    __shared__ float red[8][16][17];
+    const ApusGemmEnt ent = GROUPED ? args.ents[blockIdx.y] : args.ent0;
+    if (ent.M <= 0) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int O = args.O, K = args.K;
+    const int r = lane & 15, g = lane >> 4;
+    const int o = blockIdx.x * 16 + r;
+    const bool ovalid = o < O;
+    const int nq = K >> 7;                 /* 128-groups */
+    const int nslice = (nq + 3) >> 2;
+
+    for (int t0 = 0; t0 < ent.M; t0 += 16) {
+        apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
+        const int m = t0 + r;
+        const bool mvalid = m < ent.M;
+        const int arow = mvalid ? (ent.arows ? ent.arows[m] : ent.a0 + m) : 0;
+        for (int s = wave; s < nslice; s += nw) {
+            apus_v8i bw[4], aw[4];
+            int sbv[4], sav[4];
+            /* FP4 weight scales of this slice: 16 bytes, byte 4*step + g */
+            apus_v4u sw4 = {0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
+            if (WF == APUS_W_FP4 && ovalid) {
+                if ((s + 1) * 4 <= nq) {
+                    sw4 = *reinterpret_cast<const apus_v4u *>(ent.ws + (size_t)o * (K >> 5) + s * 16);
+                } else {
+                    for (int st = 0; st < 4; ++st)
+                        if (s * 4 + st < nq)
+                            sw4[st] = *reinterpret_cast<const unsigned *>(ent.ws + (size_t)o * (K >> 5) + (s * 4 + st) * 4);
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int q = s * 4 + st;
+                const bool qvalid = q < nq;
+                /* B */
+                if (WF == APUS_W_FP4) {
+                    if (ovalid && qvalid) {
+                        apus_v4u w = apus_ld16_stream(ent.w + (size_t)o * (K >> 1) + q * 64 + g * 16);
+                        bw[st] = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                    } else {
+                        bw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                    }
+                    sbv[st] = (int)((sw4[st] >> (8 * g)) & 0xffu);
+                } else {
+                    if (ovalid && qvalid) {
+                        const uint8_t *p = ent.w + (size_t)o * K + q * 128 + g * 16;
+                        apus_v4u w0 = apus_ld16_stream(p), w1 = apus_ld16_stream(p + 64);
+                        bw[st] = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                          (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                        sbv[st] = ent.ws[(size_t)(o >> 7) * nq + q];
+                    } else {
+                        bw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                        sbv[st] = 0x7f;
+                    }
+                }
+                /* A */
+                if (mvalid && qvalid) {
+                    const uint8_t *p = args.acodes + (size_t)arow * K + q * 128 + g * 16;
+                    uint4 a0 = apus_ld16(p), a1 = apus_ld16(p + 64);
+                    aw[st] = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                      (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                    sav[st] = (int)apus_e8m0_of(args.ascale[(size_t)arow * nq + q]);
+                } else {
+                    aw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                    sav[st] = 0x7f;
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (WF == APUS_W_FP4)
+                    acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(aw[st], bw[st], acc, sav[st], sbv[st]);
+                else
+                    acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(aw[st], bw[st], acc, sav[st], sbv[st]);
+            }
+        }
+        /* D[i][j]: i = token 4g+q of this tile, j = weight row r */
+#pragma unroll
+        for (int q = 0; q < 4; ++q) red[wave][4 * g + q][r] = acc[q];
+        __syncthreads();
+        for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+            const int i = e >> 4, j = e & 15;
+            const int mm = t0 + i, oo = blockIdx.x * 16 + j;
+            if (mm < ent.M && oo < O) {
+                float v = red[0][i][j];
+                for (int w = 1; w < nw; ++w) v += red[w][i][j];
+                if (args.round_out) v = apus_bf16_rne(v);
+                const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
+                ent.out[(size_t)orow * args.ldo + oo] = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
+                            hipStream_t st) {
+    if (n_ent <= 0) return hipSuccess;
+    const int nslice = (a->K / 128 + 3) / 4;
+    const int nw = nslice < 8 ? nslice : 8;
+    dim3 grid((a->O + 15) / 16, n_ent), block(64 * nw);
+    const bool grouped = a->ents != nullptr;
+    if (wfmt == APUS_W_FP4) {
+        if (grouped) hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP4, true>), grid, block, 0, st, *a);
+        else         hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP4, false>), grid, block, 0, st, *a);
+    } else {
+        if (grouped) hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP8, true>), grid, block, 0, st, *a);
+        else         hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP8, false>), grid, block, 0, st, *a);
+    }
+    return hipGetLastError();
+}
+
+/* ---------------------------------------------------- SwiGLU + act quant */
+
+__global__ __launch_bounds__(256) void apus_swiglu_quant_kernel(
+    const float *__restrict__ gm, const float *__restrict__ um, int M, int N,
+    float limit, uint8_t *__restrict__ codes, float *__restrict__ scales) {
+    const int nab = N >> 7;
+    const int gid = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (gid >= M * nab) return;
+    const int m = gid / nab, b = gid - m * nab;
+    const size_t off = (size_t)m * N + b * 128 + lane * 2;
+    const float2 gv = *reinterpret_cast<const float2 *>(gm + off);
+    const float2 uv = *reinterpret_cast<const float2 *>(um + off);
+    float h[2];
+    const float ga[2] = {gv.x, gv.y}, ua[2] = {uv.x, uv.y};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        float gg = ga[i], uu = ua[i];
+        if (limit > 0.0f) {
+            uu = uu > limit ? limit : (uu < -limit ? -limit : uu);
+            gg = gg > limit ? limit : gg;
+        }
+        const float sig = 1.0f / (1.0f + expf(-gg));
+        h[i] = apus_bf16_rne((gg * sig) * uu);
+    }
+    /* h is bf16-valued, so the act quant's own BF16 round is the identity */
+    const float amax = apus_wave_max(fmaxf(fabsf(h[0]), fabsf(h[1])));
+    const uint32_t e = apus_act_scale_exp(amax);
+    const float inv = apus_inv_pow2_from_exp(e);
+    const uint32_t c0 = apus_e4m3_code(h[0] * inv), c1 = apus_e4m3_code(h[1] * inv);
+    *reinterpret_cast<uint16_t *>(codes + off) = (uint16_t)(c0 | (c1 << 8));
+    if (lane == 0) scales[(size_t)m * nab + b] = apus_pow2_from_exp(e);
+}
+
+hipError_t apus_launch_swiglu_quant(const float *g, const float *u, int M,
+                                    int N, float limit, uint8_t *codes,
+                                    float *scales, hipStream_t st) {
+    if (M <= 0) return hipSuccess;
+    const int groups = M * (N >> 7);
+    hipLaunchKernelGGL(apus_swiglu_quant_kernel, dim3((groups + 3) / 4), dim3(256), 0, st,
+                       g, u, M, N, limit, codes, scales);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ MoE route */
+
+/* Single workgroup: histogram of expert ids, exclusive scan, placement.
+ * Placement order inside an expert is whatever the LDS atomics give: each
+ * output row of the grouped GEMMs depends only on its own activation row,
+ * and results are written back by pair id, so the order is not observable
+ * in the results. */
+__global__ __launch_bounds__(1024) void apus_moe_route_kernel(
+    const int32_t *__restrict__ idx, int nj, int topk, int E,
+    ApusExpertTable tab, float *g, float *u, float *eo, int inter, int dim,
+    int32_t *pair_sorted, int32_t *tok_sorted, ApusGemmEnt *e13,
+    ApusGemmEnt *e2) {
+    extern __shared__ int sh[];
+    int *cnt = sh, *off = sh + E, *cur = sh + 2 * E;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int q = threadIdx.x; q < nj; q += blockDim.x) atomicAdd(&cnt[idx[q]], 1);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int run = 0;
+        for (int e = 0; e < E; ++e) { off[e] = run; cur[e] = run; run += cnt[e]; }
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < nj; q += blockDim.x) {
+        const int pos = atomicAdd(&cur[idx[q]], 1);
+        pair_sorted[pos] = q;
+        tok_sorted[pos] = q / topk;
+    }
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
+        const int c = cnt[e], o0 = off[e];
+        ApusGemmEnt a;
+        a.arows = tok_sorted + o0; a.orows = nullptr; a.a0 = 0; a.o0 = o0; a.M = c; a.pad = 0;
+        a.w = tab.w1[e]; a.ws = tab.w1s[e]; a.out = g;
+        e13[e] = a;
+        a.w = tab.w3[e]; a.ws = tab.w3s[e]; a.out = u;
+        e13[E + e] = a;
+        ApusGemmEnt b;
+        b.w = tab.w2[e]; b.ws = tab.w2s[e]; b.out = eo;
+        b.arows = nullptr; b.orows = pair_sorted + o0; b.a0 = o0; b.o0 = 0; b.M = c; b.pad = 0;
+        e2[e] = b;
+    }
+    (void)inter; (void)dim;
+}
+
+hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
+                                 ApusExpertTable tab, float *g, float *u,
+                                 float *eo, int inter, int dim,
+                                 int32_t *pair_sorted, int32_t *tok_sorted,
+                                 ApusGemmEnt *e13, ApusGemmEnt *e2,
+                                 hipStream_t st) {
+    hipLaunchKernelGGL(apus_moe_route_kernel, dim3(1), dim3(1024), 3 * E * sizeof(int), st,
+                       idx, nj, topk, E, tab, g, u, eo, inter, dim, pair_sorted,
+                       tok_sorted, e13, e2);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------- MoE accumulate */
+
+__global__ __launch_bounds__(256) void apus_moe_accum_kernel(
+    const float *__restrict__ eo, const float *__restrict__ wgt, int s,
+    int topk, int dim, float *__restrict__ y) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    const int t = blockIdx.y;
+    if (i >= dim) return;
+    float acc = 0.0f;
+    for (int j = 0; j < topk; ++j) {
+        const float p = __fmul_rn(wgt[t * topk + j], eo[(size_t)(t * topk + j) * dim + i]);
+        acc = __fadd_rn(acc, p);
+    }
+    y[(size_t)t * dim + i] = acc;
+    (void)s;
+}
+
+hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,
+                                 int topk, int dim, float *y, hipStream_t st) {
+    if (s <= 0) return hipSuccess;
+    hipLaunchKernelGGL(apus_moe_accum_kernel, dim3((dim + 255) / 256, s), dim3(256), 0, st,
+                       eo, wgt, s, topk, dim, y);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------------ fill */
+
+__device__ __forceinline__ uint64_t apus_hash64(uint64_t seed, uint64_t stream,
+                                                uint64_t index) {
+    uint64_t z = seed * 0x9e3779b97f4a7c15ull + stream * 0xd1b54a32d192ed03ull +
+                 index * 0xbf58476d1ce4e5b9ull + 0x94d049bb133111ebull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+/* Each thread fills 8 consecutive bytes starting at first + 8*tid. */
+__global__ __launch_bounds__(256) void apus_fill_kernel(uint8_t *dst, size_t n,
+                                                        uint64_t seed, uint64_t sid,
+                                                        uint64_t first, int kind) {
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t i0 = t * 8;
+    if (i0 >= n) return;
+    uint8_t b[8];
+    if (kind == 0 && ((first & 7) == 0)) {
+        const uint64_t h = apus_hash64(seed, sid, (first + i0) >> 3);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) b[k] = (uint8_t)(h >> (8 * k));
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint64_t pos = first + i0 + k;
+            if (kind == 0) { b[k] = (uint8_t)(apus_hash64(seed, sid, pos >> 3) >> (8 * (pos & 7))); continue; }
+            const uint64_t h = apus_hash64(seed, sid, pos);
+            if (kind == 1) b[k] = (uint8_t)(118u + (uint32_t)((h >> 32) % 13u));
+            else if (kind == 2) {
+                const int32_t sum = (int32_t)(h & 0xffff) + (int32_t)((h >> 16) & 0xffff) +
+                                    (int32_t)((h >> 32) & 0xffff) + (int32_t)(h >> 48);
+                const float v = __fmul_rn((float)(sum - 131070), 1.0f / 37837.6f);
+                b[k] = (uint8_t)apus_e4m3_code(v);
+            } else b[k] = (uint8_t)(117u + (uint32_t)((h >> 32) % 7u));
+        }
+    }
+    if (i0 + 8 <= n && ((reinterpret_cast<uintptr_t>(dst + i0) & 7) == 0)) {
+        uint64_t v = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v |= (uint64_t)b[k] << (8 * k);
+        *reinterpret_cast<uint64_t *>(dst + i0) = v;
+    } else {
+        for (int k = 0; k < 8 && i0 + k < n; ++k) dst[i0 + k] = b[k];
+    }
+}
+
+hipError_t apus_launch_fill(uint8_t *dst, size_t n, uint64_t seed,
+                            uint64_t stream_id, uint64_t first, int kind,
+                            hipStream_t st) {
+    if (!n) return hipSuccess;
+    const size_t threads = (n + 7) / 8;
+    const size_t max_blocks = (size_t)1 << 30;
+    for (size_t done = 0; done < threads;) {
+        size_t nb = (threads - done + 255) / 256;
+        if (nb > max_blocks) nb = max_blocks;
+        const size_t bytes0 = done * 8;
+        hipLaunchKernelGGL(apus_fill_kernel, dim3((unsigned)nb), dim3(256), 0, st,
+                           dst + bytes0, n - bytes0, seed, stream_id, first + bytes0, kind);
+        done += nb * 256;
+    }
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ bf16 round */
+
+__global__ __launch_bounds__(256) void apus_bf16_round_kernel(float *v, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) v[i] = apus_bf16_rne(v[i]);
+}
+
+hipError_t apus_launch_bf16_round(float *v, size_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(apus_bf16_round_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, n);
+    return hipGetLastError();
+}

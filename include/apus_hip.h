@@ -1,0 +1,242 @@
+/*
+ * include/apus_hip.h — C ABI of the MI355X (gfx950) backend for apus's
+ * quantized-matmul path: MXFP4 expert GEMV/GEMM, FP8-E4M3 block-scaled dense
+ * GEMV/GEMM and the routed-expert SwiGLU dispatch.
+ *
+ * The surface mirrors apus's Metal backend boundary (c/backend_metal.h):
+ * a function-pointer hook table that the engine's call sites try first,
+ * enable/disable/is_enabled, counters, and direct entry points for
+ * kernel-level tests. Every hook returns 0 when it produced the result and
+ * nonzero when the shape or state is unsupported, in which case the caller
+ * runs its CPU kernel (c/backend_metal.h:63-65, c/attn.h:412-414). Nothing
+ * here crashes on an unsupported request.
+ *
+ * Numerics contract (same as c/backend_metal.h:19-29): activations are
+ * BF16-rounded and quantised per 128 along K exactly as the CPU does
+ * (bit-identical codes and scales); weights are consumed in their stored
+ * E2M1/E4M3 + E8M0 form (decoded values bit-identical); the block dots run
+ * on the F8F6F4 matrix cores with FP32 accumulation, so matmul outputs match
+ * the CPU within FP32 summation-order error; BF16 output rounding happens
+ * at the same points as on the CPU.
+ *
+ * Threading: one HIP stream per process, hooks are synchronous at the ABI
+ * (outputs written before return) and not re-entrant, like the Metal hooks
+ * (c/backend_metal.mm:38-39). Host-pointer entry points copy through pinned
+ * staging; *_dev entry points take device pointers, are asynchronous on the
+ * backend stream and never synchronise.
+ *
+ * Weight residency: dense weights passed by host pointer are uploaded once
+ * and cached by host pointer (stable, immutable pointers assumed, as
+ * c/backend_metal.h:38-43). Routed experts are cached by (layer, expert id),
+ * never by pointer, in an HBM-resident expert store.
+ */
+#ifndef APUS_HIP_H
+#define APUS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- weight views: layout-identical to the reference types. When the
+ * engine's own headers are included first their definitions are used. */
+#ifndef APUS_ST_H
+/* c/st.h:88-89 */
+typedef struct { const uint8_t *codes, *scales; int64_t O, K; } ApusFp8W;
+typedef struct { const uint8_t *packed, *scales; int64_t O, K; } ApusFp4W;
+#endif
+
+#ifndef APUS_FP4_H
+/* c/fp4.h:184-188 — one entry of a grouped same-(O,K) MXFP4 GEMM */
+typedef struct {
+    const uint8_t *w, *ws;
+    float *out;
+    size_t m0, M;
+} ApusFp4GemmEnt;
+#endif
+
+#ifndef APUS_MOE_H
+/* c/moe.h:37-63 — MoE weights (only the routed-expert fields, layer_id and
+ * hook_resolve/hook_ctx are read by this backend). */
+typedef struct {
+    int E, topk, inter, dim, hash;
+    float route_scale, limit;
+    const float *gate_w;
+    const float *gate_bias;
+    const int64_t *tid2eid;
+    ApusFp4W *w1, *w2, *w3;
+    ApusFp8W sw1, sw2, sw3;
+    void *hook_ctx;
+    int  (*hook_resolve)(void *ctx, int layer, int eid,
+                         ApusFp4W *w1, ApusFp4W *w2, ApusFp4W *w3);
+    void (*hook_hint)(void *ctx, int layer, int eid);
+    void (*hook_layer_end)(void *ctx, int layer);
+    void *hook_hint_ctx;
+    void *hook_layer_end_ctx;
+    int layer_id;
+} ApusMoeW;
+#endif
+
+/* ---- hook table. The first three members are ApusBackendHooks
+ * (c/backend_metal.h:73-80) in the same order; the last three are the new
+ * call sites this backend adds (top of apus_fp4_linear, c/attn.h:432;
+ * apus_fp4_gemm_mt_grouped, c/fp4.h:936; routed dispatch in
+ * apus_moe_forward before c/moe.h:433). Unimplemented members are NULL. */
+typedef struct {
+    int (*fp8_linear)(const ApusFp8W *w, const float *x, float *out,
+                      int M, int K, int O);
+    int (*f32_linear)(const float *w, const float *x, float *out,
+                      int M, int K, int O, int flags);
+    int (*head_gemv)(const void *head, const float *x, float *out,
+                     int64_t O, int64_t K);
+    int (*fp4_linear)(const ApusFp4W *w, const float *x, float *out,
+                      int M, int K, int O);
+    int (*fp4_gemm_grouped)(const ApusFp4GemmEnt *ents, size_t n_ent,
+                            const uint8_t *acodes, const float *as,
+                            size_t O, size_t K);
+    int (*moe_routed)(const ApusMoeW *w, const float *x, const int32_t *idx,
+                      const float *wgt, int s, float *y);
+} ApusHipHooks;
+
+/* ---- lifecycle (c/backend_metal.h:84-91) ---- */
+/* Initialise device 0, stream and weight caches; fill the hook table.
+ * 0 on success; nonzero with err filled when no usable gfx950 device. */
+int  apus_hip_enable(char *err, size_t errcap);
+/* Detach: drop weight caches and device state. */
+void apus_hip_disable(void);
+int  apus_hip_is_enabled(void);
+/* The hook table (all NULL until enabled). */
+const ApusHipHooks *apus_hip_hooks(void);
+
+/* ---- counters (c/backend_metal.h:93-97) ---- */
+uint64_t apus_hip_bytes_uploaded(void);   /* weight bytes copied to HBM */
+uint64_t apus_hip_bytes_resident(void);   /* weight bytes held in HBM */
+uint64_t apus_hip_dispatches(void);       /* kernel launches issued */
+
+/* ---- hooks, also callable directly. Host pointers; synchronous. ---- */
+/* c/attn.h:408-430 apus_fp8_linear: bf16(x) -> act quant -> FP8 GEMM ->
+ * bf16(out). x [M,K], out [M,O]. */
+int apus_hip_fp8_linear(const ApusFp8W *w, const float *x, float *out,
+                        int M, int K, int O);
+/* c/attn.h:432-448 apus_fp4_linear: same with an MXFP4 weight. */
+int apus_hip_fp4_linear(const ApusFp4W *w, const float *x, float *out,
+                        int M, int K, int O);
+/* c/fp4.h:936-986 apus_fp4_gemm_mt_grouped on pre-quantised activations
+ * acodes [rows, K] / as [rows, K/128]; entry i writes ents[i].out [M, O]
+ * (unrounded FP32) from activation rows [m0, m0+M). */
+int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent,
+                              const uint8_t *acodes, const float *as,
+                              size_t O, size_t K);
+/* c/moe.h:433-563: routed-expert dispatch for s tokens with the routing
+ * already decided: idx/wgt [s, topk]. y [s, dim] receives the FP32 routed
+ * sum (ApusMoeInterm.moe_routed, c/moe.h:564-565). Expert weights come
+ * from w->hook_resolve when set, else from w->w1/w2/w3, and are kept in
+ * HBM keyed by (w->layer_id, expert id). */
+int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx,
+                        const float *wgt, int s, float *y);
+
+/* ---- direct kernel entry points (host pointers, synchronous) ---- */
+/* c/fp4.h:293-321 via c/attn.h:393-403: BF16 round + per-128 act quant.
+ * codes [M,K], scales [M, K/128]. K % 128 == 0. */
+int apus_hip_act_quant(const float *x, int M, int K, uint8_t *codes,
+                       float *scales);
+/* c/fp4.h:815-848 apus_fp4_gemm_mt (scratch not needed): unrounded FP32
+ * out [M,O] from pre-quantised activations. */
+int apus_hip_fp4_gemm(const uint8_t *w, const uint8_t *ws,
+                      const uint8_t *acodes, const float *as, float *out,
+                      int M, int O, int K);
+/* c/fp8.h:557-586 apus_fp8_gemm_mt; mirrors apus_metal_fp8_gemm
+ * (c/backend_metal.h:110-112). */
+int apus_hip_fp8_gemm(const uint8_t *w, const uint8_t *ws,
+                      const uint8_t *acodes, const float *as, float *out,
+                      int M, int O, int K);
+
+/* ---- device-pointer entry points (asynchronous on the backend stream) ----
+ * Same semantics as the host versions; all pointers are device pointers.
+ * They exist for callers that keep activations in HBM between layers and
+ * for measurement with inputs already resident. */
+int apus_hip_act_quant_dev(const float *x, int M, int K, uint8_t *codes,
+                           float *scales);
+int apus_hip_fp4_gemm_dev(const uint8_t *w, const uint8_t *ws,
+                          const uint8_t *acodes, const float *as, float *out,
+                          int M, int O, int K, int round_out);
+int apus_hip_fp8_gemm_dev(const uint8_t *w, const uint8_t *ws,
+                          const uint8_t *acodes, const float *as, float *out,
+                          int M, int O, int K, int round_out);
+/* Linear = act quant + GEMM (+ BF16 out) with a caller workspace of
+ * apus_hip_linear_workspace(M, K) bytes. */
+size_t apus_hip_linear_workspace(int M, int K);
+int apus_hip_fp4_linear_dev(const uint8_t *w, const uint8_t *ws,
+                            const float *x, float *out, int M, int K, int O,
+                            void *workspace);
+int apus_hip_fp8_linear_dev(const uint8_t *w, const uint8_t *ws,
+                            const float *x, float *out, int M, int K, int O,
+                            void *workspace);
+
+/* ---- HBM-resident expert store (replaces the NVMe/RAM tiers of
+ * c/cache.h for the routed experts; keyed by (layer, expert id)) ---- */
+typedef struct ApusHipStore ApusHipStore;
+/* Reserve n_layers x E experts of shape gate/up [inter, dim], down
+ * [dim, inter] (MXFP4), laid out as one slab per expert in HBM. Returns
+ * NULL (err filled) when HBM cannot hold it. */
+ApusHipStore *apus_hip_store_create(int n_layers, int E, int dim, int inter,
+                                    char *err, size_t errcap);
+void     apus_hip_store_free(ApusHipStore *st);
+uint64_t apus_hip_store_bytes(const ApusHipStore *st);
+/* Fill every expert with counter-based synthetic weights on the device
+ * (nibbles uniform, E8M0 scales uniform in 118..130). Tensor t of
+ * (layer, e) uses stream id ((layer * E + e) * 8 + t), t = 0..5 for
+ * w1, w1s, w2, w2s, w3, w3s. */
+int      apus_hip_store_fill_random(ApusHipStore *st, uint64_t seed);
+/* Upload one expert from host memory (layout of c/st.h ApusFp4W). */
+int      apus_hip_store_put(ApusHipStore *st, int layer, int eid,
+                            const ApusFp4W *w1, const ApusFp4W *w2,
+                            const ApusFp4W *w3);
+/* Device pointers of one expert's six tensors (w1, w1s, w2, w2s, w3, w3s). */
+int      apus_hip_store_get(const ApusHipStore *st, int layer, int eid,
+                            const uint8_t *ptrs[6]);
+/* Workspace bytes for apus_hip_moe_routed_dev with s tokens x topk. */
+size_t   apus_hip_moe_workspace(const ApusHipStore *st, int s, int topk);
+/* Routed dispatch of one layer with everything in HBM: x [s, dim] f32,
+ * idx/wgt [s, topk] (device), y [s, dim] f32 (device). Asynchronous. */
+int      apus_hip_moe_routed_dev(const ApusHipStore *st, int layer,
+                                 const float *x, const int32_t *idx,
+                                 const float *wgt, int s, int topk,
+                                 float limit, float *y, void *workspace);
+
+/* ---- device memory and timing helpers (tests and benchmarks) ---- */
+void *apus_hip_malloc(size_t bytes);
+int   apus_hip_free(void *p);
+int   apus_hip_h2d(void *dst, const void *src, size_t bytes);
+int   apus_hip_d2h(void *dst, const void *src, size_t bytes);
+int   apus_hip_memset(void *dst, int value, size_t bytes);
+int   apus_hip_fill_random(void *dst, size_t bytes, uint64_t seed,
+                           uint64_t stream_id, int kind);
+int   apus_hip_synchronize(void);
+/* Events on the backend stream: record a start mark, later the elapsed
+ * milliseconds since it (synchronises on the end event). */
+int   apus_hip_timer_start(void);
+float apus_hip_timer_stop(void);
+/* Capture the launches issued on the backend stream between begin and end
+ * into one HIP graph, then replay it (asynchronously) `times` times. Only
+ * *_dev entry points may be issued while capturing. */
+int   apus_hip_graph_begin(void);
+int   apus_hip_graph_end(void);
+int   apus_hip_graph_replay(int times);
+/* Last error message of this thread ("" when none). */
+const char *apus_hip_last_error(void);
+/* Device name and compute-unit count of the current device. */
+int   apus_hip_device_info(char *name, size_t cap, int *cus);
+
+/* ---- host twins of the device numerics (no GPU needed) ---- */
+float    apus_hip_host_bf16_round(float x);
+uint8_t  apus_hip_host_e4m3_quant(float x);
+float    apus_hip_host_act_scale(float amax);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* APUS_HIP_H */

@@ -1,0 +1,290 @@
+"""ctypes binding of the CPU checkers (TEST INFRASTRUCTURE ONLY).
+
+  Oracle   : oracle/liboracle.so, the restatement of apus's quantized-matmul
+             path (oracle/apus_oracle.c).
+  Reference: oracle/_ref/libapus_ref.so, apus's own C kernels compiled from the
+             apus sources in place (oracle/ref_shim.c, oracle/Makefile).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libapus_ref.so")
+
+u8p = C.POINTER(C.c_uint8)
+f32p = C.POINTER(C.c_float)
+f64p = C.POINTER(C.c_double)
+i32p = C.POINTER(C.c_int32)
+u8pp = C.POINTER(u8p)
+
+
+def _p(a, t):
+    return a.ctypes.data_as(t)
+
+
+class Oracle:
+    def __init__(self, path=ORACLE_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle`")
+        L = C.CDLL(path)
+        sz = C.c_size_t
+        sig = {
+            "orc_ue8m0_f32": (C.c_float, [C.c_uint8]),
+            "orc_fp4_value": (C.c_float, [C.c_uint]),
+            "orc_fp4_dequant_row": (None, [u8p, u8p, f32p, sz]),
+            "orc_bf16_round": (C.c_float, [C.c_float]),
+            "orc_e4m3_quant": (C.c_uint8, [C.c_float]),
+            "orc_e4m3_dequant": (C.c_float, [C.c_uint8]),
+            "orc_act_quant_row": (None, [f32p, sz, u8p, f32p]),
+            "orc_act_quant_rows": (None, [f32p, sz, sz, u8p, f32p]),
+            "orc_fp4_gemm": (None, [u8p, u8p, u8p, f32p, f32p, sz, sz, sz]),
+            "orc_fp4_linear": (None, [u8p, u8p, f32p, f32p, sz, sz, sz]),
+            "orc_fp8_gemm": (None, [u8p, u8p, u8p, f32p, f32p, sz, sz, sz]),
+            "orc_fp8_linear": (None, [u8p, u8p, f32p, f32p, sz, sz, sz]),
+            "orc_swiglu": (None, [f32p, f32p, f32p, sz, C.c_float]),
+            "orc_moe_routed": (None, [u8pp, u8pp, u8pp, u8pp, u8pp, u8pp, C.c_int, C.c_int,
+                                      C.c_float, f32p, i32p, f32p, C.c_int, C.c_int, f32p]),
+            "orc_fp4_truth_f64": (None, [u8p, u8p, u8p, f32p, f64p, f64p, sz, sz, sz]),
+            "orc_fp8_truth_f64": (None, [u8p, u8p, u8p, f32p, f64p, f64p, sz, sz, sz]),
+            "orc_pin_unary": (C.c_uint64, [C.c_int, C.c_void_p, C.c_uint64, C.c_uint64,
+                                           C.POINTER(C.c_uint32)]),
+            "orc_hash64": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
+            "orc_fill_bytes": (None, [C.c_uint64, C.c_uint64, C.c_uint64, u8p, sz, C.c_int]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(L, n)
+            f.restype, f.argtypes = r, a
+        self.L = L
+
+    # scalar helpers
+    def ue8m0(self, b): return self.L.orc_ue8m0_f32(b)
+    def fp4_value(self, n): return self.L.orc_fp4_value(n)
+    def e4m3_dequant(self, c): return self.L.orc_e4m3_dequant(c)
+
+    def fp4_dequant_row(self, packed, scales):
+        K = packed.size * 2
+        out = np.empty(K, np.float32)
+        self.L.orc_fp4_dequant_row(_p(packed, u8p), _p(scales, u8p), _p(out, f32p), K)
+        return out
+
+    def act_quant_row(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        K = x.size
+        codes = np.empty(K, np.uint8)
+        sc = np.empty((K + 127) // 128, np.float32)
+        self.L.orc_act_quant_row(_p(x, f32p), K, _p(codes, u8p), _p(sc, f32p))
+        return codes, sc
+
+    def act_quant(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        codes = np.empty((M, K), np.uint8)
+        sc = np.empty((M, (K + 127) // 128), np.float32)
+        self.L.orc_act_quant_rows(_p(x, f32p), M, K, _p(codes, u8p), _p(sc, f32p))
+        return codes, sc
+
+    def fp4_gemm(self, w, ws, acodes, asc):
+        M, K = acodes.shape
+        O = w.shape[0]
+        out = np.empty((M, O), np.float32)
+        self.L.orc_fp4_gemm(_p(w, u8p), _p(ws, u8p), _p(acodes, u8p), _p(asc, f32p),
+                            _p(out, f32p), M, O, K)
+        return out
+
+    def fp8_gemm(self, w, ws, acodes, asc):
+        M, K = acodes.shape
+        O = w.shape[0]
+        out = np.empty((M, O), np.float32)
+        self.L.orc_fp8_gemm(_p(w, u8p), _p(ws, u8p), _p(acodes, u8p), _p(asc, f32p),
+                            _p(out, f32p), M, O, K)
+        return out
+
+    def fp4_linear(self, w, ws, x):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        O = w.shape[0]
+        out = np.empty((M, O), np.float32)
+        self.L.orc_fp4_linear(_p(w, u8p), _p(ws, u8p), _p(x, f32p), _p(out, f32p), M, K, O)
+        return out
+
+    def fp8_linear(self, w, ws, x):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        O = w.shape[0]
+        out = np.empty((M, O), np.float32)
+        self.L.orc_fp8_linear(_p(w, u8p), _p(ws, u8p), _p(x, f32p), _p(out, f32p), M, K, O)
+        return out
+
+    def swiglu(self, g, u, limit):
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        h = np.empty_like(g)
+        self.L.orc_swiglu(_p(g, f32p), _p(u, f32p), _p(h, f32p), g.size, limit)
+        return h
+
+    def fp4_truth(self, w, ws, acodes, asc):
+        M, K = acodes.shape
+        O = w.shape[0]
+        out = np.empty((M, O), np.float64)
+        esc = np.empty((M, O), np.float64)
+        self.L.orc_fp4_truth_f64(_p(w, u8p), _p(ws, u8p), _p(acodes, u8p), _p(asc, f32p),
+                                 _p(out, f64p), _p(esc, f64p), M, O, K)
+        return out, esc
+
+    def fp8_truth(self, w, ws, acodes, asc):
+        M, K = acodes.shape
+        O = w.shape[0]
+        out = np.empty((M, O), np.float64)
+        esc = np.empty((M, O), np.float64)
+        self.L.orc_fp8_truth_f64(_p(w, u8p), _p(ws, u8p), _p(acodes, u8p), _p(asc, f32p),
+                                 _p(out, f64p), _p(esc, f64p), M, O, K)
+        return out, esc
+
+    def moe_routed(self, experts, x, idx, wgt, limit):
+        x = np.ascontiguousarray(x, np.float32)
+        idx = np.ascontiguousarray(idx, np.int32)
+        wgt = np.ascontiguousarray(wgt, np.float32)
+        s, dim = x.shape
+        topk = idx.shape[1]
+        inter = experts[0][0].shape[0]
+        tabs = [(u8p * len(experts))(*[_p(e[i], u8p) for e in experts]) for i in range(6)]
+        y = np.empty((s, dim), np.float32)
+        self.L.orc_moe_routed(*tabs, dim, inter, limit, _p(x, f32p), _p(idx, i32p),
+                              _p(wgt, f32p), s, topk, _p(y, f32p))
+        return y
+
+    def fill_bytes(self, seed, stream, n, kind, first=0):
+        out = np.empty(n, np.uint8)
+        self.L.orc_fill_bytes(seed, stream, first, _p(out, u8p), n, kind)
+        return out
+
+    def pin_unary(self, which, fnptr, lo, hi):
+        bad = C.c_uint32()
+        n = self.L.orc_pin_unary(which, fnptr, lo, hi, C.byref(bad))
+        return n, bad.value
+
+
+class _WeightView(C.Structure):
+    """c/st.h:88-89: {codes|packed, scales, O, K} — same layout for fp8 and fp4."""
+    _fields_ = [("w", C.c_void_p), ("s", C.c_void_p), ("O", C.c_int64), ("K", C.c_int64)]
+
+
+class Reference:
+    """apus's own CPU kernels (compiled from the apus sources)."""
+
+    def __init__(self, path=REF_SO):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} missing: run `make -C oracle ref` where the apus "
+                                    "sources are present")
+        L = C.CDLL(path)
+        sz = C.c_size_t
+        sig = {
+            "apus_ue8m0_f32": (C.c_float, [C.c_uint8]),
+            "apus_e4m3_quant_f32": (C.c_uint8, [C.c_float]),
+            "apus_e4m3_dequant_f32": (C.c_float, [C.c_uint8]),
+            "apus_bf16_round": (C.c_float, [C.c_float]),
+            "apus_fp4_act_quant_scalar": (None, [f32p, sz, u8p, f32p]),
+            "apus_fp4_dequant_row_scalar": (None, [u8p, u8p, f32p, sz]),
+            "apus_fp4_gemm_scalar": (None, [u8p, u8p, u8p, f32p, f32p, f32p, sz, sz, sz]),
+            "apus_fp4_gemm_mt": (None, [u8p, u8p, u8p, f32p, f32p, f32p, sz, sz, sz]),
+            "apus_fp8_gemm_scalar": (None, [u8p, u8p, u8p, f32p, f32p, f32p, sz, sz, sz]),
+            "apus_fp8_gemm_mt": (None, [u8p, u8p, u8p, f32p, f32p, f32p, sz, sz, sz]),
+            "apus_fp4_linear": (None, [C.c_void_p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
+            "apus_fp8_linear": (None, [C.c_void_p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
+            "ref_swiglu": (None, [f32p, f32p, f32p, sz, C.c_float]),
+            "ref_act_quant_rows": (None, [f32p, C.c_int, C.c_int, f32p, u8p, f32p]),
+            "ref_x86_avx2_hits": (C.c_ulong, []),
+            "ref_pool_threads": (C.c_int, []),
+            "ref_moe_routed": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
+                                         f32p, u8pp, u8pp, u8pp, u8pp, u8pp, u8pp, f32p, i32p,
+                                         C.c_int, f32p, f32p, f32p]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(L, n)
+            f.restype, f.argtypes = r, a
+        self.L = L
+
+    def act_quant(self, x):
+        """c/attn.h:393-403: BF16 round then apus_fp4_act_quant_scalar per row."""
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        xb = np.empty_like(x)
+        codes = np.empty((M, K), np.uint8)
+        sc = np.empty((M, (K + 127) // 128), np.float32)
+        self.L.ref_act_quant_rows(_p(x, f32p), M, K, _p(xb, f32p), _p(codes, u8p), _p(sc, f32p))
+        return codes, sc
+
+    def _gemm(self, fn, w, ws, acodes, asc):
+        M, K = acodes.shape
+        O = w.shape[0]
+        out = np.empty((M, O), np.float32)
+        scratch = np.empty(M * K * 2 + 64, np.float32)
+        fn(_p(w, u8p), _p(ws, u8p), _p(acodes, u8p), _p(asc, f32p), _p(scratch, f32p),
+           _p(out, f32p), M, O, K)
+        return out
+
+    def fp4_gemm_scalar(self, *a): return self._gemm(self.L.apus_fp4_gemm_scalar, *a)
+    def fp4_gemm_mt(self, *a): return self._gemm(self.L.apus_fp4_gemm_mt, *a)
+    def fp8_gemm_scalar(self, *a): return self._gemm(self.L.apus_fp8_gemm_scalar, *a)
+    def fp8_gemm_mt(self, *a): return self._gemm(self.L.apus_fp8_gemm_mt, *a)
+
+    def _linear(self, fn, w, ws, x, fp4):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        O = w.shape[0]
+        out = np.empty((M, O), np.float32)
+        view = _WeightView(w.ctypes.data, ws.ctypes.data, O, K)   # ApusFp4W / ApusFp8W
+        fn(C.addressof(view), _p(x, f32p), _p(out, f32p), M, K, O)
+        return out
+
+    def fp4_linear(self, w, ws, x): return self._linear(self.L.apus_fp4_linear, w, ws, x, True)
+    def fp8_linear(self, w, ws, x): return self._linear(self.L.apus_fp8_linear, w, ws, x, False)
+
+    def swiglu(self, g, u, limit):
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        h = np.empty_like(g)
+        self.L.ref_swiglu(_p(g, f32p), _p(u, f32p), _p(h, f32p), g.size, limit)
+        return h
+
+    def moe_routed(self, experts, gate_w, x, idx, route_scale, limit):
+        """Real apus_moe_forward with idx forced through hash routing; returns
+        (router_w, routed_y)."""
+        x = np.ascontiguousarray(x, np.float32)
+        idx = np.ascontiguousarray(idx, np.int32)
+        gate_w = np.ascontiguousarray(gate_w, np.float32)
+        s, dim = x.shape
+        topk = idx.shape[1]
+        E = len(experts)
+        inter = experts[0][0].shape[0]
+        tabs = [(u8p * E)(*[_p(e[i], u8p) for e in experts]) for i in range(6)]
+        rw = np.empty((s, topk), np.float32)
+        y = np.empty((s, dim), np.float32)
+        out = np.empty((s, dim), np.float32)
+        rc = self.L.ref_moe_routed(E, topk, dim, inter, route_scale, limit, _p(gate_w, f32p),
+                                   *tabs, _p(x, f32p), _p(idx, i32p), s, _p(rw, f32p),
+                                   _p(y, f32p), _p(out, f32p))
+        if rc != 0:
+            raise RuntimeError("reference routing did not follow the forced expert ids")
+        return rw, y
+
+
+def bf16_round_np(x):
+    """Vectorised BF16 RNE (same rule as orc_bf16_round), for input prep."""
+    x = np.ascontiguousarray(x, np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    r = np.where(nan, x.view(np.uint32), r)
+    return r.view(np.float32).reshape(x.shape)
+
+
+def have_ref():
+    return os.path.exists(REF_SO)

@@ -1,0 +1,101 @@
+/*
+ * oracle/ref_shim.c — builds the reference's OWN CPU kernels (c/fp4.h,
+ * c/fp8.h, c/attn.h linears, c/moe.h dispatch, c/pool.h, c/x86.h) from the
+ * sources where they lie under the apus checkout (-I <apus>/c) into
+ * oracle/_ref/libapus_ref.so. Nothing from the reference is copied here:
+ * this file only instantiates the header-only implementations and adds a
+ * few exported wrappers for entry points the headers keep static.
+ *
+ * TEST INFRASTRUCTURE ONLY: used to pin the oracle restatement and as the
+ * measured CPU baseline (kind "reference") in bench.py.
+ */
+#define APUS_COMPAT_IMPLEMENTATION
+#define APUS_FP4_IMPLEMENTATION
+#define APUS_FP8_IMPLEMENTATION
+#define APUS_JSON_IMPLEMENTATION
+#define APUS_ST_IMPLEMENTATION
+#define APUS_MHC_IMPLEMENTATION
+#define APUS_ATTN_IMPLEMENTATION
+#define APUS_MOE_IMPLEMENTATION
+#include "compat.h"
+#include "fp4.h"
+#include "fp8.h"
+#include "json.h"
+#include "st.h"
+#include "mhc.h"
+#include "attn.h"
+#include "moe.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+/* c/moe.h:113-126 is static; expose the elementwise SwiGLU range */
+void ref_swiglu(const float *g, const float *u, float *h, size_t n,
+                float limit) {
+    ApusSwigluJob j = { g, u, h, limit };
+    apus_expert_swiglu_range(&j, 0, n);
+}
+
+unsigned long ref_x86_avx2_hits(void) { return apus_x86_avx2_hits(); }
+int ref_pool_threads(void) { return apus_pool_threads(); }
+
+/* Run the real apus_moe_forward (c/moe.h:369) with hash routing so the
+ * caller fixes the expert ids: tid2eid[t*topk+j] = idx[t*topk+j], ids[t]=t.
+ * Routing weights come from the gate scores as in the reference; they are
+ * returned in router_w so a restatement can use the identical weights.
+ * The shared expert runs on all-zero FP8 weights (its output is not used:
+ * routed_y is ApusMoeInterm.moe_routed, the routed-only FP32 sum). */
+int ref_moe_routed(int E, int topk, int dim, int inter, float route_scale,
+                   float limit, const float *gate_w,
+                   const uint8_t *const *w1, const uint8_t *const *w1s,
+                   const uint8_t *const *w2, const uint8_t *const *w2s,
+                   const uint8_t *const *w3, const uint8_t *const *w3s,
+                   const float *x, const int32_t *idx, int s,
+                   float *router_w, float *routed_y, float *out) {
+    ApusMoeW w;
+    memset(&w, 0, sizeof w);
+    w.E = E; w.topk = topk; w.inter = inter; w.dim = dim; w.hash = 1;
+    w.route_scale = route_scale; w.limit = limit;
+    w.gate_w = gate_w;
+    int64_t *tid2eid = malloc((size_t)s * topk * sizeof(int64_t));
+    int64_t *ids = malloc((size_t)s * sizeof(int64_t));
+    for (int i = 0; i < s * topk; i++) tid2eid[i] = idx[i];
+    for (int t = 0; t < s; t++) ids[t] = t;
+    w.tid2eid = tid2eid;
+    ApusFp4W *a1 = calloc((size_t)E, sizeof(ApusFp4W));
+    ApusFp4W *a2 = calloc((size_t)E, sizeof(ApusFp4W));
+    ApusFp4W *a3 = calloc((size_t)E, sizeof(ApusFp4W));
+    for (int e = 0; e < E; e++) {
+        a1[e] = (ApusFp4W){ w1[e], w1s[e], inter, dim };
+        a2[e] = (ApusFp4W){ w2[e], w2s[e], dim, inter };
+        a3[e] = (ApusFp4W){ w3[e], w3s[e], inter, dim };
+    }
+    w.w1 = a1; w.w2 = a2; w.w3 = a3;
+    size_t nsd = (size_t)((inter + 127) / 128) * (size_t)((dim + 127) / 128);
+    uint8_t *z1 = calloc((size_t)inter * dim, 1), *z2 = calloc((size_t)inter * dim, 1);
+    uint8_t *z3 = calloc((size_t)inter * dim, 1);
+    uint8_t *zs = malloc(nsd);
+    memset(zs, 127, nsd);
+    w.sw1 = (ApusFp8W){ z1, zs, inter, dim };
+    w.sw2 = (ApusFp8W){ z2, zs, dim, inter };
+    w.sw3 = (ApusFp8W){ z3, zs, inter, dim };
+    int32_t *ridx = malloc((size_t)s * topk * sizeof(int32_t));
+    ApusMoeInterm im;
+    memset(&im, 0, sizeof im);
+    im.router_w = router_w;
+    im.router_idx = ridx;
+    im.moe_routed = routed_y;
+    apus_moe_forward(&w, x, ids, s, out, &im);
+    int ok = memcmp(ridx, idx, (size_t)s * topk * sizeof(int32_t)) == 0;
+    free(tid2eid); free(ids); free(a1); free(a2); free(a3);
+    free(z1); free(z2); free(z3); free(zs); free(ridx);
+    return ok ? 0 : -1;
+}
+
+/* c/attn.h:393-403 apus_act_quant_rows is static; run it over M rows
+ * exactly as apus_fp4_linear / apus_fp8_linear do (BF16 round + act quant). */
+void ref_act_quant_rows(const float *x, int M, int K, float *xb, uint8_t *codes,
+                        float *scales) {
+    ApusActQuantJob aq = { x, xb, codes, scales, K, apus_fp4_act_blocks((size_t)K) };
+    apus_act_quant_rows(&aq, 0, (size_t)M);
+}

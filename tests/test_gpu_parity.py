@@ -1,0 +1,111 @@
+"""GPU parity: libapus_hip.so (through its C ABI) against the CPU oracle.
+
+Bars (written into each test):
+  * activation codes/scales: bit-exact;
+  * raw GEMM outputs (FP32): max|d|/max|ref| <= 1e-3 (BASELINE) and per-output
+    err/esc <= 1e-4 vs the float64 truth. The reference gates its sequential
+    FP32 CPU kernels at err/esc < 2e-5 (tests/m3/test_fp4.c:365-503); the
+    F8F6F4 matrix cores accumulate each 128-wide block in their own order and
+    precision, measured at err/esc ~2e-5 on gfx950, hence the 5x margin;
+  * BF16-rounded linear outputs: each element within one BF16 ulp of the
+    oracle's unrounded fp32 value plus 1e-4*max|ref| (the sums differ only in
+    summation order, so a value near a rounding boundary may round the other
+    way), and max|d|/max|ref| <= 1e-3 + 2^-8 (one BF16 ulp) overall.
+"""
+import numpy as np
+import pytest
+
+from helpers import (acts, bf16_linear_ok, err_esc, fp4_weights, fp4_weights_corners,
+                     fp8_weights, max_rel)
+
+pytestmark = pytest.mark.gpu
+
+
+def test_device_is_gfx950(hip):
+    name, cus = hip.device_info()
+    print("device:", name, "CUs:", cus)
+    assert "gfx950" in name
+
+
+@pytest.mark.parametrize("M,K", [(1, 128), (3, 256), (7, 4096), (64, 2048)])
+def test_act_quant_bitexact(hip, oracle, rng, M, K):
+    x = acts(rng, M, K, 3.0)
+    x[0, :128] = 0.0                       # zero group -> amax floor path
+    if M > 1:
+        x[1, 128 % K:] *= 100.0            # large later groups
+    x[-1, 5] = 1e-30                       # tiny value next to normal ones
+    c_ref, s_ref = oracle.act_quant(x)
+    c, s = hip.act_quant(x)
+    assert np.array_equal(c, c_ref)
+    assert np.array_equal(s.view(np.uint32), s_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,O,K", [(1, 16, 128), (1, 64, 512), (3, 64, 256), (5, 40, 640),
+                                   (1, 2048, 4096), (16, 256, 4096), (33, 96, 1024)])
+def test_fp4_gemm(hip, oracle, rng, M, O, K):
+    w, ws = fp4_weights_corners(rng, O, K)
+    x = acts(rng, M, K, 3.0)
+    c, s = oracle.act_quant(x)
+    want = oracle.fp4_gemm(w, ws, c, s)
+    truth, esc = oracle.fp4_truth(w, ws, c, s)
+    got = hip.fp4_gemm(w, ws, c, s)
+    mr, ee = max_rel(got, want), err_esc(got, truth, esc)
+    print(f"fp4 gemm M={M} O={O} K={K}: max_rel={mr:.3g} err/esc={ee:.3g}")
+    assert mr <= 1e-3
+    assert ee <= 1e-4
+
+
+@pytest.mark.parametrize("M,O,K", [(1, 128, 128), (2, 130, 384), (1, 4096, 4096),
+                                   (17, 256, 1024)])
+def test_fp8_gemm(hip, oracle, rng, M, O, K):
+    w, ws = fp8_weights(rng, O, K)
+    x = acts(rng, M, K, 2.0)
+    c, s = oracle.act_quant(x)
+    want = oracle.fp8_gemm(w, ws, c, s)
+    truth, esc = oracle.fp8_truth(w, ws, c, s)
+    got = hip.fp8_gemm(w, ws, c, s)
+    mr, ee = max_rel(got, want), err_esc(got, truth, esc)
+    print(f"fp8 gemm M={M} O={O} K={K}: max_rel={mr:.3g} err/esc={ee:.3g}")
+    assert mr <= 1e-3
+    assert ee <= 1e-4
+
+
+def _check_linear(got, want, unrounded, tag):
+    ok = bf16_linear_ok(got, unrounded, 1e-4 * np.abs(unrounded).max())
+    flips = float(np.mean(got != want))
+    mr = max_rel(got, want)
+    print(f"{tag}: bf16 flips vs oracle {flips:.2%}, max_rel={mr:.3g}")
+    assert ok.all(), np.argwhere(~ok)[:5]
+    assert mr <= 1e-3 + 2.0 ** -8
+
+
+@pytest.mark.parametrize("M,O,K", [(1, 2048, 4096), (4, 4096, 2048)])
+def test_fp4_linear(hip, oracle, rng, M, O, K):
+    w, ws = fp4_weights(rng, O, K)
+    x = acts(rng, M, K)
+    want = oracle.fp4_linear(w, ws, x)
+    c, s = oracle.act_quant(x)
+    got = hip.fp4_linear(w, ws, x)
+    _check_linear(got, want, oracle.fp4_gemm(w, ws, c, s), f"fp4 linear M={M} O={O} K={K}")
+
+
+@pytest.mark.parametrize("M,O,K", [(1, 4096, 4096), (3, 256, 512)])
+def test_fp8_linear(hip, oracle, rng, M, O, K):
+    w, ws = fp8_weights(rng, O, K)
+    x = acts(rng, M, K)
+    want = oracle.fp8_linear(w, ws, x)
+    c, s = oracle.act_quant(x)
+    got = hip.fp8_linear(w, ws, x)
+    _check_linear(got, want, oracle.fp8_gemm(w, ws, c, s), f"fp8 linear M={M} O={O} K={K}")
+
+
+def test_fp4_gemm_m_independent(hip, oracle, rng):
+    """Batched rows are bitwise equal to the same rows computed alone
+    (the reference's M-independence gate, tests/m12/README.md:331-354)."""
+    O, K = 256, 2048
+    w, ws = fp4_weights(rng, O, K)
+    c, s = oracle.act_quant(acts(rng, 20, K))
+    full = hip.fp4_gemm(w, ws, c, s)
+    for m in (0, 7, 19):
+        one = hip.fp4_gemm(w, ws, c[m:m + 1].copy(), s[m:m + 1].copy())
+        assert np.array_equal(one.view(np.uint32), full[m:m + 1].view(np.uint32))
