@@ -290,14 +290,14 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         return 1;
     ApusGemmArgs a{};
     a.acodes = w.xc; a.ascale = w.xs; a.ents = w.e13;
-    a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
+    a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1; a.max_m = (2 * nj + E - 1) / E;
     if (!launched(apus_launch_gemm(APUS_W_FP4, &a, 2 * E, g.stream), "gemm w1/w3")) return 1;
     if (!launched(apus_launch_swiglu_quant(w.gm, w.um, nj, inter, limit, w.hc, w.hs, g.stream),
                   "swiglu_quant"))
         return 1;
     ApusGemmArgs b{};
     b.acodes = w.hc; b.ascale = w.hs; b.ents = w.e2;
-    b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
+    b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1; b.max_m = (2 * nj + E - 1) / E;
     if (!launched(apus_launch_gemm(APUS_W_FP4, &b, E, g.stream), "gemm w2")) return 1;
     if (!launched(apus_launch_moe_accum(w.eo, wgt, s, topk, dim, y, g.stream), "moe_accum"))
         return 1;
@@ -398,9 +398,10 @@ int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent, const ui
     if (!ensure_init()) return 1;
     if (!n_ent) return 0;
     if (!shape_ok(1, (int)K, (int)O)) return 1;
-    size_t rows = 0, outrows = 0;
+    size_t rows = 0, outrows = 0, max_m = 0;
     for (size_t i = 0; i < n_ent; i++) {
         if (ents[i].m0 + ents[i].M > rows) rows = ents[i].m0 + ents[i].M;
+        if (ents[i].M > max_m) max_m = ents[i].M;
         outrows += ents[i].M;
     }
     const size_t nab = K / 128;
@@ -422,7 +423,7 @@ int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent, const ui
     if (!upload(dents, he.data(), n_ent * sizeof(ApusGemmEnt))) return 1;
     ApusGemmArgs a{};
     a.acodes = dc; a.ascale = dsc; a.ents = dents;
-    a.O = (int)O; a.K = (int)K; a.ldo = (int)O; a.round_out = 0;
+    a.O = (int)O; a.K = (int)K; a.ldo = (int)O; a.round_out = 0; a.max_m = (int)max_m;
     if (!launched(apus_launch_gemm(APUS_W_FP4, &a, (int)n_ent, g.stream), "grouped gemm")) return 1;
     orow = 0;
     for (size_t i = 0; i < n_ent; i++) {

@@ -1,0 +1,454 @@
+/*
+ * apus_gemm.hip — block-scaled GEMM kernels on the gfx950 F8F6F4 matrix cores:
+ * E4M3 activations (quantised per 128 along K, E8M0 scales) against MXFP4
+ * (E2M1 + E8M0 per 32) or FP8-E4M3 (E8M0 per 128x128 tile) weights.
+ * Semantics: c/fp4.h:367-395 and c/fp8.h:191-218 (normative GEMMs),
+ * c/fp4.h:936-986 (grouped entries over shared activation rows).
+ *
+ * Three schedules, chosen by apus_launch_gemm:
+ *  - split-K (apus_gemm_kernel): few row tiles, e.g. one dense GEMV; the
+ *    waves of a workgroup split K and reduce through LDS.
+ *  - decode (apus_gemm_decode_kernel): grouped launches of few-row entries
+ *    (routed experts at decode); activations staged once in LDS, each wave
+ *    streams a whole-K 16-row weight tile through a prefetch ring.
+ *  - stream (apus_gemm_stream_kernel): grouped launches with many rows per
+ *    entry (prefill); up to 4 token tiles accumulated per weight pass.
+ * In all three, every output is one accumulation chain over its 128-groups
+ * in a fixed order, so results do not depend on M, on the position of a row
+ * within its entry, or on timing.
+ */
+#include "apus_device.h"
+#include "apus_internal.h"
+
+/*
+ * Tiling. A workgroup owns 16 consecutive weight rows (the 16 MFMA columns)
+ * of one entry and all of that entry's rows (tokens) in tiles of 16. The
+ * reduction dimension is cut into slices of 512; slice s belongs to wave
+ * s % waves, so the waves of a workgroup split K and their partial 16x16
+ * tiles are summed through LDS in a fixed wave order (the result does not
+ * depend on timing, nor on M or on the position of a row in the entry).
+ *
+ * One MFMA covers exactly one 128-element K group (group q = 4s + step), so
+ * the activation scale and, for FP8, the 128x128 weight tile scale are the
+ * same for all 32-element blocks of the instruction. Operand placement
+ * (measured on gfx950): an E4M3 operand lane of lane group g holds K
+ * [16g, 16g+16) in bytes 0..15 and [64+16g, +16) in bytes 16..31; an E2M1
+ * operand lane holds the contiguous K [32g, 32g+32); the E8M0 scale of
+ * (row r, 32-block b) is taken from lane 16b + r. Hence per step:
+ *   A (E4M3 codes) lane g: bytes [q*128 + 16g, +16) and [q*128 + 64 + 16g, +16)
+ *   B E4M3 weights: the same two 16-byte pieces of weight row o
+ *   B E2M1 weights: bytes [q*64 + 16g, +16) of row o, scale byte 4q + g
+ * which makes each instruction read 64 contiguous bytes per weight row.
+ */
+template <int WF, bool GROUPED>
+__global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
+    __shared__ float red[8][16][17];
+    const ApusGemmEnt ent = GROUPED ? args.ents[blockIdx.y] : args.ent0;
+    if (ent.M <= 0) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nw = blockDim.x >> 6;
+    const int O = args.O, K = args.K;
+    const int r = lane & 15, g = lane >> 4;
+    const int o = blockIdx.x * 16 + r;
+    const bool ovalid = o < O;
+    const int nq = K >> 7;                 /* 128-groups */
+    const int nslice = (nq + 3) >> 2;
+
+    for (int t0 = 0; t0 < ent.M; t0 += 16) {
+        apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
+        const int m = t0 + r;
+        const bool mvalid = m < ent.M;
+        const int arow = mvalid ? (ent.arows ? ent.arows[m] : ent.a0 + m) : 0;
+        for (int s = wave; s < nslice; s += nw) {
+            apus_v8i bw[4], aw[4];
+            int sbv[4], sav[4];
+            /* FP4 weight scales of this slice: 16 bytes, byte 4*step + g */
+            apus_v4u sw4 = {0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
+            if (WF == APUS_W_FP4 && ovalid) {
+                if ((s + 1) * 4 <= nq) {
+                    sw4 = *reinterpret_cast<const apus_v4u *>(ent.ws + (size_t)o * (K >> 5) + s * 16);
+                } else {
+                    for (int st = 0; st < 4; ++st)
+                        if (s * 4 + st < nq)
+                            sw4[st] = *reinterpret_cast<const unsigned *>(ent.ws + (size_t)o * (K >> 5) + (s * 4 + st) * 4);
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int q = s * 4 + st;
+                const bool qvalid = q < nq;
+                /* B */
+                if (WF == APUS_W_FP4) {
+                    if (ovalid && qvalid) {
+                        apus_v4u w = apus_ld16_stream(ent.w + (size_t)o * (K >> 1) + q * 64 + g * 16);
+                        bw[st] = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                    } else {
+                        bw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                    }
+                    sbv[st] = (int)((sw4[st] >> (8 * g)) & 0xffu);
+                } else {
+                    if (ovalid && qvalid) {
+                        const uint8_t *p = ent.w + (size_t)o * K + q * 128 + g * 16;
+                        apus_v4u w0 = apus_ld16_stream(p), w1 = apus_ld16_stream(p + 64);
+                        bw[st] = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                          (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                        sbv[st] = ent.ws[(size_t)(o >> 7) * nq + q];
+                    } else {
+                        bw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                        sbv[st] = 0x7f;
+                    }
+                }
+                /* A */
+                if (mvalid && qvalid) {
+                    const uint8_t *p = args.acodes + (size_t)arow * K + q * 128 + g * 16;
+                    uint4 a0 = apus_ld16(p), a1 = apus_ld16(p + 64);
+                    aw[st] = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                      (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                    sav[st] = (int)apus_e8m0_of(args.ascale[(size_t)arow * nq + q]);
+                } else {
+                    aw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                    sav[st] = 0x7f;
+                }
+            }
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                if (WF == APUS_W_FP4)
+                    acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(aw[st], bw[st], acc, sav[st], sbv[st]);
+                else
+                    acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(aw[st], bw[st], acc, sav[st], sbv[st]);
+            }
+        }
+        /* D[i][j]: i = token 4g+q of this tile, j = weight row r */
+#pragma unroll
+        for (int q = 0; q < 4; ++q) red[wave][4 * g + q][r] = acc[q];
+        __syncthreads();
+        for (int e = threadIdx.x; e < 256; e += blockDim.x) {
+            const int i = e >> 4, j = e & 15;
+            const int mm = t0 + i, oo = blockIdx.x * 16 + j;
+            if (mm < ent.M && oo < O) {
+                float v = red[0][i][j];
+                for (int w = 1; w < nw; ++w) v += red[w][i][j];
+                if (args.round_out) v = apus_bf16_rne(v);
+                const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
+                ent.out[(size_t)orow * args.ldo + oo] = v;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+/*
+ * Streaming variant for launches with many row tiles (grouped expert GEMMs):
+ * every wave owns one 16-row tile over the whole K, so no cross-wave
+ * reduction is needed; each output is a single accumulation chain over the
+ * 128-groups in order q = 0, 1, ... (again independent of M and of the row's
+ * position). The weight fragment of slice s+1 is loaded while slice s is
+ * multiplied, and up to MT token tiles are accumulated per weight pass, so a
+ * weight slab is streamed from HBM once per MT*16 tokens.
+ * Operand placement as in apus_gemm_kernel.
+ */
+template <int WF>
+struct ApusBFrag {
+    apus_v4u w[4][WF == APUS_W_FP4 ? 1 : 2];
+    apus_v4u s;       /* FP4: 16 group-scale bytes; FP8: byte st = tile scale */
+};
+
+template <int WF>
+__device__ __forceinline__ void apus_load_b(ApusBFrag<WF> &f, const ApusGemmEnt &ent, int o,
+                                            bool ovalid, int s, int nq, int K, int g) {
+    const bool full = (s + 1) * 4 <= nq;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const int q = s * 4 + st;
+        const bool v = ovalid && q < nq;
+        if (WF == APUS_W_FP4) {
+            f.w[st][0] = v ? apus_ld16_stream(ent.w + (size_t)o * (K >> 1) + q * 64 + g * 16)
+                           : apus_v4u{0u, 0u, 0u, 0u};
+        } else {
+            const uint8_t *p = ent.w + (size_t)o * K + q * 128 + g * 16;
+            f.w[st][0] = v ? apus_ld16_stream(p) : apus_v4u{0u, 0u, 0u, 0u};
+            f.w[st][1] = v ? apus_ld16_stream(p + 64) : apus_v4u{0u, 0u, 0u, 0u};
+        }
+    }
+    if (WF == APUS_W_FP4) {
+        if (ovalid && full) {
+            f.s = *reinterpret_cast<const apus_v4u *>(ent.ws + (size_t)o * (K >> 5) + s * 16);
+        } else {
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                f.s[st] = (ovalid && s * 4 + st < nq)
+                    ? *reinterpret_cast<const unsigned *>(ent.ws + (size_t)o * (K >> 5) + (s * 4 + st) * 4)
+                    : 0x7f7f7f7fu;
+        }
+    } else {
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+            f.s[st] = (ovalid && s * 4 + st < nq) ? ent.ws[(size_t)(o >> 7) * nq + s * 4 + st] : 0x7fu;
+    }
+}
+
+template <int WF, int MT>
+__global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args) {
+    const ApusGemmEnt ent = args.ents[blockIdx.y];
+    if (ent.M <= 0) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int O = args.O, K = args.K;
+    const int r = lane & 15, g = lane >> 4;
+    const int tile = blockIdx.x * 4 + wave;
+    if (tile * 16 >= O) return;
+    const int o = tile * 16 + r;
+    const bool ovalid = o < O;
+    const int nq = K >> 7;
+    const int nslice = (nq + 3) >> 2;
+
+    for (int c0 = 0; c0 < ent.M; c0 += 16 * MT) {
+        const int ntile = min(MT, (ent.M - c0 + 15) >> 4);
+        apus_v4f acc[MT];
+        int arow[MT];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+            const int m = c0 + t * 16 + r;
+            arow[t] = m < ent.M ? (ent.arows ? ent.arows[m] : ent.a0 + m) : -1;
+        }
+        ApusBFrag<WF> cur, nxt;
+        apus_load_b<WF>(cur, ent, o, ovalid, 0, nq, K, g);
+        for (int s = 0; s < nslice; ++s) {
+            if (s + 1 < nslice) apus_load_b<WF>(nxt, ent, o, ovalid, s + 1, nq, K, g);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                if (t >= ntile) break;
+                const int ar = arow[t];
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const int q = s * 4 + st;
+                    apus_v8i a = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
+                    int sa = 0x7f;
+                    if (ar >= 0 && q < nq) {
+                        const uint8_t *p = args.acodes + (size_t)ar * K + q * 128 + g * 16;
+                        const uint4 a0 = apus_ld16(p), a1 = apus_ld16(p + 64);
+                        a = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                     (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                        sa = (int)apus_e8m0_of(args.ascale[(size_t)ar * nq + q]);
+                    }
+                    if (WF == APUS_W_FP4) {
+                        const apus_v4u w = cur.w[st][0];
+                        const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                        const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                        acc[t] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[t], sa, sb);
+                    } else {
+                        const apus_v4u w0 = cur.w[st][0], w1 = cur.w[st][1];
+                        const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                                    (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                        acc[t] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc[t], sa, (int)cur.s[st]);
+                    }
+                }
+            }
+            cur = nxt;
+        }
+        /* lane holds D[4g+q][r]: token c0 + 16t + 4g + q, weight row o */
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            if (t >= ntile) break;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int mm = c0 + t * 16 + 4 * g + q;
+                if (mm < ent.M && ovalid) {
+                    float v = acc[t][q];
+                    if (args.round_out) v = apus_bf16_rne(v);
+                    const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
+                    ent.out[(size_t)orow * args.ldo + o] = v;
+                }
+            }
+        }
+    }
+}
+
+/*
+ * Decode schedule. K = 512 * NS is a template constant and O % 16 == 0 (the
+ * launcher checks), so the slice loop is straight-line code with no per-lane
+ * bounds tests: a divergent branch or a loop back edge around the prefetch
+ * ring makes the compiler drain every outstanding load (s_waitcnt vmcnt(0)),
+ * which would empty the ring each step. The workgroup's four waves share one entry; its
+ * activation rows (R at a time, whole K) are staged in LDS as E4M3 codes and
+ * E8M0 bytes, rows beyond the entry read row 0 and are zeroed by a select.
+ */
+#define APUS_DEC_WAVES 4
+
+template <int WF>
+__device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const uint8_t *wrow,
+                                                 const uint8_t *srow, int s, int g) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const int q = s * 4 + st;
+        if (WF == APUS_W_FP4) {
+            f.w[st][0] = apus_ld16_stream(wrow + q * 64 + g * 16);
+        } else {
+            f.w[st][0] = apus_ld16_stream(wrow + q * 128 + g * 16);
+            f.w[st][1] = apus_ld16_stream(wrow + q * 128 + 64 + g * 16);
+        }
+    }
+    if (WF == APUS_W_FP4) {
+        f.s = *reinterpret_cast<const apus_v4u *>(srow + s * 16);
+    } else {
+        const unsigned b4 = *reinterpret_cast<const unsigned *>(srow + s * 4);
+        f.s = apus_v4u{b4 & 0xffu, (b4 >> 8) & 0xffu, (b4 >> 16) & 0xffu, b4 >> 24};
+    }
+}
+
+template <int WF, int R, int NS, int PD>
+__global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int K = NS * 512, NQ = NS * 4, K16 = K / 16, LDK = K + 16;
+    constexpr int STAGE = R * K16 / 256;               /* 16-byte loads per thread */
+    const ApusGemmEnt ent = args.ents[blockIdx.y];
+    if (ent.M <= 0) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int O = args.O;
+    const int r = lane & 15, g = lane >> 4;
+    const int tile = blockIdx.x * APUS_DEC_WAVES + wave;
+    const bool tvalid = tile * 16 < O;                 /* uniform per wave */
+    const int o = tvalid ? tile * 16 + r : r;
+    uint8_t *lcodes = lds;
+    uint8_t *lsc = lds + R * LDK;
+    const uint8_t *wrow = ent.w + (size_t)o * (WF == APUS_W_FP4 ? (K >> 1) : K);
+    const uint8_t *srow = WF == APUS_W_FP4 ? ent.ws + (size_t)o * (K >> 5)
+                                           : ent.ws + (size_t)(o >> 7) * NQ;
+
+    for (int c0 = 0; c0 < ent.M; c0 += R) {
+        const int rows = min(R, ent.M - c0);
+        __syncthreads();
+        /* stage: row indices, then every code/scale load, then the LDS
+         * writes (no load waits on another load's result more than once) */
+        int ridx[R];
+        if (ent.arows) {
+#pragma unroll
+            for (int j = 0; j < R; ++j) ridx[j] = ent.arows[c0 + min(j, rows - 1)];
+        } else {
+#pragma unroll
+            for (int j = 0; j < R; ++j) ridx[j] = ent.a0 + c0 + min(j, rows - 1);
+        }
+        constexpr int RPJ = 256 / K16;                   /* rows per 256 loads */
+        static_assert(RPJ >= 1 && R % RPJ == 0, "staging shape");
+        uint4 v[STAGE];
+#pragma unroll
+        for (int j = 0; j < STAGE; ++j) {
+            const int rsub = threadIdx.x / K16;         /* 0..RPJ-1 */
+            const int cc = threadIdx.x - rsub * K16;
+            int ar = ridx[j * RPJ];
+#pragma unroll
+            for (int t = 1; t < RPJ; ++t) ar = rsub == t ? ridx[j * RPJ + t] : ar;
+            v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);   /* rows past the entry
+                                                                          repeat its last row */
+        }
+        const int si = threadIdx.x % (R * NQ), srr = si / NQ;
+        int sar = ridx[0];
+#pragma unroll
+        for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
+        const float scv = args.ascale[(size_t)sar * NQ + (si - srr * NQ)];
+#pragma unroll
+        for (int j = 0; j < STAGE; ++j) {
+            const int rsub = threadIdx.x / K16;
+            const int cc = threadIdx.x - rsub * K16;
+            if (j * RPJ + rsub < rows)
+                *reinterpret_cast<uint4 *>(lcodes + (j * RPJ + rsub) * LDK + cc * 16) = v[j];
+        }
+        if (threadIdx.x < R * NQ && srr < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv);
+        __syncthreads();
+        if (!tvalid) continue;
+
+        const bool rvalid = r < rows;
+        const int rr = rvalid ? r : 0;
+        const uint8_t *arow = lcodes + rr * LDK + g * 16;
+        const uint8_t *asrow = lsc + rr * NQ;
+        const int z = rvalid ? -1 : 0;
+        apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
+        ApusBFrag<WF> ring[PD];
+#pragma unroll
+        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, u, g);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            ApusBFrag<WF> &cur = ring[s % PD];
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int q = s * 4 + st;
+                const uint4 a0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
+                const uint4 a1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+                const apus_v8i a = apus_v8i{(int)a0.x & z, (int)a0.y & z, (int)a0.z & z,
+                                            (int)a0.w & z, (int)a1.x & z, (int)a1.y & z,
+                                            (int)a1.z & z, (int)a1.w & z};
+                const int sa = asrow[q];
+                if (WF == APUS_W_FP4) {
+                    const apus_v4u w = cur.w[st][0];
+                    const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                    const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                    acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, sa, sb);
+                } else {
+                    const apus_v4u w0 = cur.w[st][0], w1 = cur.w[st][1];
+                    const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                                (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                    acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, sa, (int)cur.s[st]);
+                }
+            }
+            if (s + PD < NS) apus_load_b_full<WF>(cur, wrow, srow, s + PD, g);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = 4 * g + q;
+            if (m < rows) {
+                float val = acc[q];
+                if (args.round_out) val = apus_bf16_rne(val);
+                const int mm = c0 + m;
+                const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
+                ent.out[(size_t)orow * args.ldo + o] = val;
+            }
+        }
+    }
+}
+
+hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
+                            hipStream_t st) {
+    if (n_ent <= 0) return hipSuccess;
+    const bool grouped = a->ents != nullptr;
+    const size_t row_tiles = (size_t)n_ent * ((a->O + 15) / 16);
+    /* grouped launches of few-row entries (K = 2048 or 4096) */
+    if (grouped && a->max_m > 0 && a->max_m <= 8 && row_tiles >= 2048 &&
+        (a->K == 2048 || a->K == 4096) && a->O % 16 == 0) {
+        constexpr int R = 8;
+        const size_t lds = (size_t)R * (a->K + 16) + (size_t)R * (a->K / 128);
+        dim3 grid((a->O + 16 * APUS_DEC_WAVES - 1) / (16 * APUS_DEC_WAVES), n_ent), block(256);
+        if (wfmt == APUS_W_FP4) {
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3>), grid, block, lds, st, *a);
+            else              hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 4, 3>), grid, block, lds, st, *a);
+        } else {
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 8, 2>), grid, block, lds, st, *a);
+            else              hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2>), grid, block, lds, st, *a);
+        }
+        return hipGetLastError();
+    }
+    /* grouped launches with many rows per entry */
+    if (grouped && row_tiles >= 2048) {
+        dim3 grid((a->O + 63) / 64, n_ent), block(256);
+        const bool wide = a->max_m == 0 || a->max_m > 16;
+        if (wfmt == APUS_W_FP4) {
+            if (wide) hipLaunchKernelGGL((apus_gemm_stream_kernel<APUS_W_FP4, 4>), grid, block, 0, st, *a);
+            else      hipLaunchKernelGGL((apus_gemm_stream_kernel<APUS_W_FP4, 1>), grid, block, 0, st, *a);
+        } else {
+            if (wide) hipLaunchKernelGGL((apus_gemm_stream_kernel<APUS_W_FP8, 4>), grid, block, 0, st, *a);
+            else      hipLaunchKernelGGL((apus_gemm_stream_kernel<APUS_W_FP8, 1>), grid, block, 0, st, *a);
+        }
+        return hipGetLastError();
+    }
+    /* few row tiles: split K over the waves of a workgroup */
+    const int nslice = (a->K / 128 + 3) / 4;
+    const int nw = nslice < 8 ? nslice : 8;
+    dim3 grid((a->O + 15) / 16, n_ent), block(64 * nw);
+    if (wfmt == APUS_W_FP4) {
+        if (grouped) hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP4, true>), grid, block, 0, st, *a);
+        else         hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP4, false>), grid, block, 0, st, *a);
+    } else {
+        if (grouped) hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP8, true>), grid, block, 0, st, *a);
+        else         hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP8, false>), grid, block, 0, st, *a);
+    }
+    return hipGetLastError();
+}

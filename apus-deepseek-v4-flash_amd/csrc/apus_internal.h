@@ -32,6 +32,8 @@ typedef struct {
     const ApusGemmEnt *ents; /* grouped: device array; else NULL */
     ApusGemmEnt ent0;        /* the entry when ents == NULL */
     int O, K, ldo, round_out;
+    int max_m;               /* typical largest M of an entry (a performance hint
+                              * only: any M is computed; 0 = unknown) */
 } ApusGemmArgs;
 
 /* y[m] = A x W^T for every entry; n_ent entries (1 with ents == NULL). */

@@ -3,9 +3,7 @@
  *
  *  - act quant: BF16 round + per-128 E4M3 quantisation, one wave per
  *    128-element group (c/attn.h:393-403, c/fp4.h:293-321), bit-exact.
- *  - block-scaled GEMM on F8F6F4 MFMA: E4M3 activations against MXFP4 or
- *    FP8-E4M3 weights (c/fp4.h:367-395, c/fp8.h:191-218), grouped over
- *    expert entries with gather/scatter row tables (c/fp4.h:936-986).
+ *  (the block-scaled GEMMs live in apus_gemm.hip)
  *  - SwiGLU + act quant of h (c/moe.h:113-126 followed by the act quant of
  *    the w2 input, c/moe.h:309-314), one wave per 128 group.
  *  - routed-pair counting sort and GEMM entry tables (c/moe.h:465-474).
@@ -45,142 +43,6 @@ hipError_t apus_launch_act_quant(const float *x, int ldx, const int32_t *arows,
     const int groups = M * (K >> 7);
     hipLaunchKernelGGL(apus_act_quant_kernel, dim3((groups + 3) / 4), dim3(256), 0, st,
                        x, ldx, arows, M, K, codes, scales);
-    return hipGetLastError();
-}
-
-/* ------------------------------------------------------ block-scaled GEMM */
-
-/*
- * Tiling. A workgroup owns 16 consecutive weight rows (the 16 MFMA columns)
- * of one entry and all of that entry's rows (tokens) in tiles of 16. The
- * reduction dimension is cut into slices of 512; slice s belongs to wave
- * s % waves, so the waves of a workgroup split K and their partial 16x16
- * tiles are summed through LDS in a fixed wave order (the result does not
- * depend on timing, nor on M or on the position of a row in the entry).
- *
- * One MFMA covers exactly one 128-element K group (group q = 4s + step), so
- * the activation scale and, for FP8, the 128x128 weight tile scale are the
- * same for all 32-element blocks of the instruction. Operand placement
- * (measured on gfx950): an E4M3 operand lane of lane group g holds K
- * [16g, 16g+16) in bytes 0..15 and [64+16g, +16) in bytes 16..31; an E2M1
- * operand lane holds the contiguous K [32g, 32g+32); the E8M0 scale of
- * (row r, 32-block b) is taken from lane 16b + r. Hence per step:
- *   A (E4M3 codes) lane g: bytes [q*128 + 16g, +16) and [q*128 + 64 + 16g, +16)
- *   B E4M3 weights: the same two 16-byte pieces of weight row o
- *   B E2M1 weights: bytes [q*64 + 16g, +16) of row o, scale byte 4q + g
- * which makes each instruction read 64 contiguous bytes per weight row.
- */
-template <int WF, bool GROUPED>
-__global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
-    __shared__ float red[8][16][17];
-    const ApusGemmEnt ent = GROUPED ? args.ents[blockIdx.y] : args.ent0;
-    if (ent.M <= 0) return;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nw = blockDim.x >> 6;
-    const int O = args.O, K = args.K;
-    const int r = lane & 15, g = lane >> 4;
-    const int o = blockIdx.x * 16 + r;
-    const bool ovalid = o < O;
-    const int nq = K >> 7;                 /* 128-groups */
-    const int nslice = (nq + 3) >> 2;
-
-    for (int t0 = 0; t0 < ent.M; t0 += 16) {
-        apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
-        const int m = t0 + r;
-        const bool mvalid = m < ent.M;
-        const int arow = mvalid ? (ent.arows ? ent.arows[m] : ent.a0 + m) : 0;
-        for (int s = wave; s < nslice; s += nw) {
-            apus_v8i bw[4], aw[4];
-            int sbv[4], sav[4];
-            /* FP4 weight scales of this slice: 16 bytes, byte 4*step + g */
-            apus_v4u sw4 = {0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
-            if (WF == APUS_W_FP4 && ovalid) {
-                if ((s + 1) * 4 <= nq) {
-                    sw4 = *reinterpret_cast<const apus_v4u *>(ent.ws + (size_t)o * (K >> 5) + s * 16);
-                } else {
-                    for (int st = 0; st < 4; ++st)
-                        if (s * 4 + st < nq)
-                            sw4[st] = *reinterpret_cast<const unsigned *>(ent.ws + (size_t)o * (K >> 5) + (s * 4 + st) * 4);
-                }
-            }
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const int q = s * 4 + st;
-                const bool qvalid = q < nq;
-                /* B */
-                if (WF == APUS_W_FP4) {
-                    if (ovalid && qvalid) {
-                        apus_v4u w = apus_ld16_stream(ent.w + (size_t)o * (K >> 1) + q * 64 + g * 16);
-                        bw[st] = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
-                    } else {
-                        bw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
-                    }
-                    sbv[st] = (int)((sw4[st] >> (8 * g)) & 0xffu);
-                } else {
-                    if (ovalid && qvalid) {
-                        const uint8_t *p = ent.w + (size_t)o * K + q * 128 + g * 16;
-                        apus_v4u w0 = apus_ld16_stream(p), w1 = apus_ld16_stream(p + 64);
-                        bw[st] = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
-                                          (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
-                        sbv[st] = ent.ws[(size_t)(o >> 7) * nq + q];
-                    } else {
-                        bw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
-                        sbv[st] = 0x7f;
-                    }
-                }
-                /* A */
-                if (mvalid && qvalid) {
-                    const uint8_t *p = args.acodes + (size_t)arow * K + q * 128 + g * 16;
-                    uint4 a0 = apus_ld16(p), a1 = apus_ld16(p + 64);
-                    aw[st] = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
-                                      (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-                    sav[st] = (int)apus_e8m0_of(args.ascale[(size_t)arow * nq + q]);
-                } else {
-                    aw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
-                    sav[st] = 0x7f;
-                }
-            }
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                if (WF == APUS_W_FP4)
-                    acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(aw[st], bw[st], acc, sav[st], sbv[st]);
-                else
-                    acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(aw[st], bw[st], acc, sav[st], sbv[st]);
-            }
-        }
-        /* D[i][j]: i = token 4g+q of this tile, j = weight row r */
-#pragma unroll
-        for (int q = 0; q < 4; ++q) red[wave][4 * g + q][r] = acc[q];
-        __syncthreads();
-        for (int e = threadIdx.x; e < 256; e += blockDim.x) {
-            const int i = e >> 4, j = e & 15;
-            const int mm = t0 + i, oo = blockIdx.x * 16 + j;
-            if (mm < ent.M && oo < O) {
-                float v = red[0][i][j];
-                for (int w = 1; w < nw; ++w) v += red[w][i][j];
-                if (args.round_out) v = apus_bf16_rne(v);
-                const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
-                ent.out[(size_t)orow * args.ldo + oo] = v;
-            }
-        }
-        __syncthreads();
-    }
-}
-
-hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
-                            hipStream_t st) {
-    if (n_ent <= 0) return hipSuccess;
-    const int nslice = (a->K / 128 + 3) / 4;
-    const int nw = nslice < 8 ? nslice : 8;
-    dim3 grid((a->O + 15) / 16, n_ent), block(64 * nw);
-    const bool grouped = a->ents != nullptr;
-    if (wfmt == APUS_W_FP4) {
-        if (grouped) hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP4, true>), grid, block, 0, st, *a);
-        else         hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP4, false>), grid, block, 0, st, *a);
-    } else {
-        if (grouped) hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP8, true>), grid, block, 0, st, *a);
-        else         hipLaunchKernelGGL((apus_gemm_kernel<APUS_W_FP8, false>), grid, block, 0, st, *a);
-    }
     return hipGetLastError();
 }
 

@@ -65,3 +65,38 @@ def test_moe_batched_equals_per_token(hip, rng):
     for t in range(s):
         one = hip.moe_routed(experts, x[t:t + 1], idx[t:t + 1], wgt[t:t + 1], 10.0, layer_id=7)
         assert np.array_equal(one.view(np.uint32), full[t:t + 1].view(np.uint32)), t
+
+
+@pytest.mark.parametrize("Ms", [[1, 3, 0, 8, 2] * 30, [12, 1, 20] * 40])
+def test_fp4_gemm_grouped_many(hip, oracle, rng, Ms):
+    """Grouped launches large enough for the streaming schedules (decode:
+    every M <= 8; stream: larger M), K = 2048, checked entry by entry."""
+    O, K = 256, 2048
+    rows = sum(Ms)
+    c, s = oracle.act_quant(acts(rng, rows, K, 2.0))
+    ents, m0 = [], 0
+    w, ws = fp4_weights(rng, O * 8, K)            # 8 distinct weights, reused
+    for i, M in enumerate(Ms):
+        j = i % 8
+        ents.append((w[j * O:(j + 1) * O], ws[j * O:(j + 1) * O], m0, M))
+        m0 += M
+    outs = hip.fp4_gemm_grouped(ents, c, s, O)
+    for i in range(0, len(ents), 7):
+        wj, wsj, m0, M = ents[i]
+        if M == 0:
+            continue
+        want = oracle.fp4_gemm(wj, wsj, c[m0:m0 + M].copy(), s[m0:m0 + M].copy())
+        assert max_rel(outs[i], want) <= 1e-3, i
+
+
+def test_moe_routed_decode_shape(hip, oracle, rng):
+    """dim = inter = 2048 and few rows per expert: the decode schedule."""
+    E, dim, inter, s, topk = 64, 2048, 2048, 8, 6
+    experts = moe_experts(rng, E, dim, inter)
+    x = acts(rng, s, dim)
+    idx, wgt = topk_routing(rng, s, E, topk)
+    want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
+    got = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=99)
+    mr = max_rel(got, want)
+    print(f"moe decode-shape: max_rel={mr:.3g} identical={np.mean(got == want):.1%}")
+    assert mr <= 2.0 ** -7
