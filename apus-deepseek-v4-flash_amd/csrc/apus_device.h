@@ -55,4 +55,14 @@ __device__ __forceinline__ float apus_wave_max(float v) {
     return v;
 }
 
+/* Workgroup barrier for LDS hand-off only: waits for this wave's LDS
+ * operations, not for its outstanding global loads. __syncthreads() also
+ * fences global memory, i.e. waits for every load in flight (vmcnt 0), which
+ * would drain a register prefetch ring at each barrier. */
+__device__ __forceinline__ void apus_lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 #endif /* APUS_DEVICE_H */

@@ -5,15 +5,17 @@
  * Semantics: c/fp4.h:367-395 and c/fp8.h:191-218 (normative GEMMs),
  * c/fp4.h:936-986 (grouped entries over shared activation rows).
  *
- * Three schedules, chosen by apus_launch_gemm:
+ * Schedules, chosen by apus_launch_gemm:
  *  - split-K (apus_gemm_kernel): few row tiles, e.g. one dense GEMV; the
  *    waves of a workgroup split K and reduce through LDS.
  *  - decode (apus_gemm_decode_kernel): grouped launches of few-row entries
  *    (routed experts at decode); activations staged once in LDS, each wave
  *    streams a whole-K 16-row weight tile through a prefetch ring.
- *  - stream (apus_gemm_stream_kernel): grouped launches with many rows per
- *    entry (prefill); up to 4 token tiles accumulated per weight pass.
- * In all three, every output is one accumulation chain over its 128-groups
+ *  - prefill (apus_gemm_prefill_kernel): grouped launches with many rows
+ *    per entry; activation slices double-buffered in LDS, 4 token tiles per
+ *    weight pass.
+ *  - stream (apus_gemm_stream_kernel): other grouped shapes.
+ * In all of them, every output is one accumulation chain over its 128-groups
  * in a fixed order, so results do not depend on M, on the position of a row
  * within its entry, or on timing.
  */
@@ -302,7 +304,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
     constexpr int K = NS * 512, NQ = NS * 4, K16 = K / 16, LDK = K + 16;
     constexpr int STAGE = R * K16 / 256;               /* 16-byte loads per thread */
     const ApusGemmEnt ent = args.ents[blockIdx.y];
-    if (ent.M <= 0) return;
+    if (ent.M <= args.m_min || (args.m_max > 0 && ent.M > args.m_max)) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int O = args.O;
     const int r = lane & 15, g = lane >> 4;
@@ -406,27 +408,177 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
     }
 }
 
+/*
+ * Prefill schedule (grouped launches whose entries have many rows, e.g.
+ * routed experts over a 512-token prompt). A workgroup of 8 waves owns
+ * 8 weight row tiles (128 rows) of one entry and takes the entry's rows in
+ * chunks of TT token tiles (16*TT rows). For each 512-wide K slice the
+ * chunk's activation codes are staged in LDS (double buffered: the loads of
+ * slice s+1 are in flight while slice s is multiplied), and each wave
+ * multiplies its weight fragment, held in a prefetch ring, against all TT
+ * token tiles, so the weights are streamed from HBM once per chunk.
+ * K = 512 * NS is a template constant (straight-line slice loop).
+ */
+#define APUS_PRE_WAVES 8
+
+template <int WF, int NS, int TT, int PD>
+__global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs args) {
+    constexpr int K = NS * 512, NQ = NS * 4;
+    constexpr int ROWS = 16 * TT;                 /* activation rows per chunk */
+    constexpr int PITCH = 512 + 16;               /* LDS bytes per row per slice */
+    constexpr int CHUNKS = ROWS * 32 / 512;       /* 16-byte loads per thread per slice */
+    __shared__ __align__(16) uint8_t abuf[2][ROWS * PITCH];
+    __shared__ uint8_t sbuf[2][ROWS * 4];
+    const ApusGemmEnt ent = args.ents[blockIdx.y];
+    if (ent.M <= args.m_min || (args.m_max > 0 && ent.M > args.m_max)) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int o = (blockIdx.x * APUS_PRE_WAVES + wave) * 16 + r;   /* O % 128 == 0 */
+    const uint8_t *wrow = ent.w + (size_t)o * (WF == APUS_W_FP4 ? (K >> 1) : K);
+    const uint8_t *srow = WF == APUS_W_FP4 ? ent.ws + (size_t)o * (K >> 5)
+                                           : ent.ws + (size_t)(o >> 7) * NQ;
+
+    for (int c0 = 0; c0 < ent.M; c0 += ROWS) {
+        const int rows = min(ROWS, ent.M - c0);
+        /* the activation rows this thread stages (rows past the entry repeat
+         * its last row; their outputs are never stored) */
+        const uint8_t *abase[CHUNKS];
+#pragma unroll
+        for (int j = 0; j < CHUNKS; ++j) {
+            const int i = threadIdx.x + j * 512;
+            const int rr = min(i >> 5, rows - 1);
+            const int ar = ent.arows ? ent.arows[c0 + rr] : ent.a0 + c0 + rr;
+            abase[j] = args.acodes + (size_t)ar * K + (i & 31) * 16;
+        }
+        const int srr = min((int)((threadIdx.x % (ROWS * 4)) >> 2), rows - 1);
+        const int sar = ent.arows ? ent.arows[c0 + srr] : ent.a0 + c0 + srr;
+        const float *sbase = args.ascale + (size_t)sar * NQ + (threadIdx.x & 3);
+        uint4 v[CHUNKS];
+        float sv;
+#define APUS_PRE_FETCH(S)                                                      \
+        do {                                                                   \
+            _Pragma("unroll") for (int j = 0; j < CHUNKS; ++j)                 \
+                v[j] = apus_ld16(abase[j] + (S) * 512);                        \
+            sv = sbase[(S) * 4];                                               \
+        } while (0)
+#define APUS_PRE_STORE(B)                                                      \
+        do {                                                                   \
+            _Pragma("unroll") for (int j = 0; j < CHUNKS; ++j) {               \
+                const int i = threadIdx.x + j * 512;                           \
+                *reinterpret_cast<uint4 *>(&abuf[B][(i >> 5) * PITCH + (i & 31) * 16]) = v[j]; \
+            }                                                                  \
+            if (threadIdx.x < ROWS * 4) sbuf[B][threadIdx.x] = (uint8_t)apus_e8m0_of(sv); \
+        } while (0)
+        apus_lds_barrier();           /* previous chunk's readers are done */
+        APUS_PRE_FETCH(0);
+        APUS_PRE_STORE(0);
+        apus_v4f acc[TT];
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+        ApusBFrag<WF> ring[PD];
+#pragma unroll
+        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, u, g);
+        apus_lds_barrier();
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            /* no instruction moves across slice boundaries: the unrolled
+             * loop would otherwise hoist every slice's loads to the top */
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 1 < NS) APUS_PRE_FETCH(s + 1);
+            ApusBFrag<WF> &cur = ring[s % PD];
+            const uint8_t *ab = abuf[s & 1];
+            const uint8_t *sb8 = sbuf[s & 1];
+            {
+                /* all TT tiles every time: a partial chunk multiplies repeated
+                 * rows whose outputs are not stored (no branch in the loop) */
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    const uint8_t *ap = ab + (t * 16 + r) * PITCH + g * 16;
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        const uint4 a0 = *reinterpret_cast<const uint4 *>(ap + st * 128);
+                        const uint4 a1 = *reinterpret_cast<const uint4 *>(ap + st * 128 + 64);
+                        const apus_v8i a = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                                    (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                        const int sa = sb8[(t * 16 + r) * 4 + st];
+                        if (WF == APUS_W_FP4) {
+                            const apus_v4u w = cur.w[st][0];
+                            const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                            const int sbv = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                            acc[t] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[t], sa, sbv);
+                        } else {
+                            const apus_v4u w0 = cur.w[st][0], w1 = cur.w[st][1];
+                            const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                                        (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                            acc[t] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc[t], sa, (int)cur.s[st]);
+                        }
+                    }
+                    /* the tile's MFMAs complete here: MFMAs touch no memory,
+                     * so the compiler would otherwise sink them all below
+                     * the slice barriers and keep every operand live */
+                    asm volatile("" : "+v"(acc[t]) :: "memory");
+                }
+            }
+            if (s + PD < NS) apus_load_b_full<WF>(cur, wrow, srow, s + PD, g);
+            if (s + 1 < NS) APUS_PRE_STORE((s + 1) & 1);
+            apus_lds_barrier();
+        }
+        {
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int m = t * 16 + 4 * g + q;
+                    if (m < rows) {
+                        float val = acc[t][q];
+                        if (args.round_out) val = apus_bf16_rne(val);
+                        const int mm = c0 + m;
+                        const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
+                        ent.out[(size_t)orow * args.ldo + o] = val;
+                    }
+                }
+            }
+        }
+    }
+}
+
 hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
                             hipStream_t st) {
     if (n_ent <= 0) return hipSuccess;
     const bool grouped = a->ents != nullptr;
     const size_t row_tiles = (size_t)n_ent * ((a->O + 15) / 16);
-    /* grouped launches of few-row entries (K = 2048 or 4096) */
-    if (grouped && a->max_m > 0 && a->max_m <= 8 && row_tiles >= 2048 &&
-        (a->K == 2048 || a->K == 4096) && a->O % 16 == 0) {
+    /* grouped launches with K = 2048 or 4096: entries with at most 8 rows
+     * take the decode schedule, larger ones the prefill schedule (two
+     * launches over the same entry table, each skipping the other's entries) */
+    if (grouped && row_tiles >= 2048 && (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
         constexpr int R = 8;
+        ApusGemmArgs d = *a;
+        d.m_min = 0;
+        d.m_max = R;
         const size_t lds = (size_t)R * (a->K + 16) + (size_t)R * (a->K / 128);
-        dim3 grid((a->O + 16 * APUS_DEC_WAVES - 1) / (16 * APUS_DEC_WAVES), n_ent), block(256);
+        dim3 gd(a->O / (16 * APUS_DEC_WAVES), n_ent), bd(256);
         if (wfmt == APUS_W_FP4) {
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3>), grid, block, lds, st, *a);
-            else              hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 4, 3>), grid, block, lds, st, *a);
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3>), gd, bd, lds, st, d);
+            else              hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 4, 3>), gd, bd, lds, st, d);
         } else {
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 8, 2>), grid, block, lds, st, *a);
-            else              hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2>), grid, block, lds, st, *a);
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 8, 2>), gd, bd, lds, st, d);
+            else              hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2>), gd, bd, lds, st, d);
+        }
+        if (a->max_m > 0 && a->max_m <= R) return hipGetLastError();
+        ApusGemmArgs p = *a;
+        p.m_min = R;
+        p.m_max = 0;
+        dim3 gp(a->O / (16 * APUS_PRE_WAVES), n_ent), bp(512);
+        if (wfmt == APUS_W_FP4) {
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, 4, 2>), gp, bp, 0, st, p);
+            else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, 4, 2>), gp, bp, 0, st, p);
+        } else {
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 8, 2, 2>), gp, bp, 0, st, p);
+            else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 4, 2, 2>), gp, bp, 0, st, p);
         }
         return hipGetLastError();
     }
-    /* grouped launches with many rows per entry */
+    /* other grouped shapes with many row tiles */
     if (grouped && row_tiles >= 2048) {
         dim3 grid((a->O + 63) / 64, n_ent), block(256);
         const bool wide = a->max_m == 0 || a->max_m > 16;

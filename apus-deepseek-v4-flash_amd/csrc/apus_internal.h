@@ -34,6 +34,8 @@ typedef struct {
     int O, K, ldo, round_out;
     int max_m;               /* typical largest M of an entry (a performance hint
                               * only: any M is computed; 0 = unknown) */
+    int m_min, m_max;        /* set by the launcher: a kernel computes only the
+                              * entries with m_min < M <= m_max (m_max 0: no cap) */
 } ApusGemmArgs;
 
 /* y[m] = A x W^T for every entry; n_ent entries (1 with ents == NULL). */

@@ -67,7 +67,7 @@ def test_moe_batched_equals_per_token(hip, rng):
         assert np.array_equal(one.view(np.uint32), full[t:t + 1].view(np.uint32)), t
 
 
-@pytest.mark.parametrize("Ms", [[1, 3, 0, 8, 2] * 30, [12, 1, 20] * 40])
+@pytest.mark.parametrize("Ms", [[1, 3, 0, 8, 2] * 30, [12, 1, 20, 70] * 33])
 def test_fp4_gemm_grouped_many(hip, oracle, rng, Ms):
     """Grouped launches large enough for the streaming schedules (decode:
     every M <= 8; stream: larger M), K = 2048, checked entry by entry."""
@@ -99,4 +99,25 @@ def test_moe_routed_decode_shape(hip, oracle, rng):
     got = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=99)
     mr = max_rel(got, want)
     print(f"moe decode-shape: max_rel={mr:.3g} identical={np.mean(got == want):.1%}")
+    assert mr <= 2.0 ** -7
+
+
+def test_moe_routed_prefill_shape(hip, oracle, rng):
+    """dim = inter = 2048 and many rows per expert: experts with more than
+    8 rows take the prefill schedule, the others the decode schedule."""
+    E, dim, inter, s, topk = 64, 2048, 2048, 48, 6
+    experts = moe_experts(rng, E, dim, inter)
+    x = acts(rng, s, dim)
+    # skewed routing: expert 0..5 popular, so some experts get > 16 rows
+    idx = np.stack([rng.choice(E, topk, replace=False,
+                               p=np.r_[np.full(6, 0.1), np.full(E - 6, 0.4 / (E - 6))])
+                    for _ in range(s)]).astype(np.int32)
+    wgt = rng.random((s, topk)).astype(np.float32)
+    wgt /= wgt.sum(1, keepdims=True)
+    counts = np.bincount(idx.ravel(), minlength=E)
+    assert counts.max() > 16 and (counts[counts > 0] <= 8).any()
+    want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
+    got = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=98)
+    mr = max_rel(got, want)
+    print(f"moe prefill-shape: max_rel={mr:.3g} identical={np.mean(got == want):.1%}")
     assert mr <= 2.0 ** -7
