@@ -63,6 +63,11 @@ class ApusMoeW(C.Structure):
                 ("hook_layer_end_ctx", vp), ("layer_id", C.c_int)]
 
 
+class ApusHipGemmEnt(C.Structure):
+    _fields_ = [("w", vp), ("ws", vp), ("out", vp), ("arows", vp), ("orows", vp),
+                ("a0", C.c_int32), ("o0", C.c_int32), ("M", C.c_int32), ("reserved", C.c_int32)]
+
+
 HOOK_FIELDS = ("fp8_linear", "f32_linear", "head_gemv", "fp4_linear", "fp4_gemm_grouped",
                "moe_routed")
 
@@ -91,6 +96,8 @@ SIGNATURES = {
     "apus_hip_act_quant_dev": (C.c_int, [vp, C.c_int, C.c_int, vp, vp]),
     "apus_hip_fp4_gemm_dev": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int]),
     "apus_hip_fp8_gemm_dev": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "apus_hip_gemm_grouped_dev": (C.c_int, [C.c_int, vp, C.c_int, vp, vp, C.c_int, C.c_int,
+                                            C.c_int, C.c_int, C.c_int]),
     "apus_hip_linear_workspace": (C.c_size_t, [C.c_int, C.c_int]),
     "apus_hip_fp4_linear_dev": (C.c_int, [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
     "apus_hip_fp8_linear_dev": (C.c_int, [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
@@ -113,6 +120,10 @@ SIGNATURES = {
     "apus_hip_synchronize": (C.c_int, []),
     "apus_hip_timer_start": (C.c_int, []),
     "apus_hip_timer_stop": (C.c_float, []),
+    "apus_hip_lanes": (C.c_int, [C.c_int]),
+    "apus_hip_lane": (C.c_int, [C.c_int]),
+    "apus_hip_fork": (C.c_int, []),
+    "apus_hip_join": (C.c_int, []),
     "apus_hip_graph_begin": (C.c_int, []),
     "apus_hip_graph_end": (C.c_int, []),
     "apus_hip_graph_replay": (C.c_int, [C.c_int]),

@@ -63,6 +63,10 @@ struct State {
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    /* concurrency lanes for the *_dev entry points: lane 0 is `stream` */
+    hipStream_t lane[8] = {};
+    hipEvent_t lane_ev[8] = {};
+    int nlanes = 1, cur_lane = 0;
     std::unordered_map<const void *, DenseW> dense;
     std::unordered_map<uint64_t, ExpertW> experts;
     DevBuf scratch[8];
@@ -97,6 +101,8 @@ bool ensure_init() {
     if (!ok(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking), "hipStreamCreate")) return false;
     if (!ok(hipEventCreate(&g.ev0), "hipEventCreate")) return false;
     if (!ok(hipEventCreate(&g.ev1), "hipEventCreate")) return false;
+    g.lane[0] = g.stream;
+    if (!ok(hipEventCreateWithFlags(&g.lane_ev[0], hipEventDisableTiming), "hipEventCreate")) return false;
     const char *mb = getenv("APUS_HIP_DENSE_MB");
     g.dense_budget = (size_t)(mb ? strtoull(mb, nullptr, 10) : 131072ull) << 20;
     g.inited = true;
@@ -113,6 +119,9 @@ void *scratch(int i, size_t n) {
     b.n = want;
     return b.p;
 }
+
+/* stream of the currently selected lane (for *_dev launches) */
+hipStream_t dev_stream() { return g.lane[g.cur_lane]; }
 
 bool upload(void *dst, const void *src, size_t n) {
     return ok(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g.stream), "H2D");
@@ -182,14 +191,14 @@ bool shape_ok(int M, int K, int O) {
 }
 
 int gemm_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
-             const float *as, float *out, int M, int O, int K, int round_out) {
+             const float *as, float *out, int M, int O, int K, int round_out, hipStream_t st) {
     ApusGemmArgs a{};
     a.acodes = acodes; a.ascale = as; a.ents = nullptr;
     a.ent0.w = w; a.ent0.ws = ws; a.ent0.out = out;
     a.ent0.arows = nullptr; a.ent0.orows = nullptr;
     a.ent0.a0 = 0; a.ent0.o0 = 0; a.ent0.M = M;
     a.O = O; a.K = K; a.ldo = O; a.round_out = round_out;
-    return launched(apus_launch_gemm(wfmt, &a, 1, g.stream), "gemm") ? 0 : 1;
+    return launched(apus_launch_gemm(wfmt, &a, 1, st), "gemm") ? 0 : 1;
 }
 
 /* host-pointer linear: stage x, quantise, GEMM, BF16 out, copy back */
@@ -210,7 +219,7 @@ int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
     if (!dx || !dc || !dsc || !dout) return 1;
     if (!upload(dx, x, (size_t)M * K * 4)) return 1;
     if (!launched(apus_launch_act_quant(dx, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
-    if (gemm_dev(wfmt, d->w, d->ws, dc, dsc, dout, M, O, K, 1)) return 1;
+    if (gemm_dev(wfmt, d->w, d->ws, dc, dsc, dout, M, O, K, 1, g.stream)) return 1;
     if (!download(out, dout, (size_t)M * O * 4) || !finish()) return 1;
     return 0;
 }
@@ -232,7 +241,7 @@ int gemm_host(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acod
     if (!upload(dw, w, wbytes) || !upload(dws, ws, sbytes) ||
         !upload(dc, acodes, (size_t)M * K) || !upload(dsc, as, (size_t)M * nab * 4))
         return 1;
-    if (gemm_dev(wfmt, dw, dws, dc, dsc, dout, M, O, K, 0)) return 1;
+    if (gemm_dev(wfmt, dw, dws, dc, dsc, dout, M, O, K, 0, g.stream)) return 1;
     if (!download(out, dout, (size_t)M * O * 4) || !finish()) return 1;
     return 0;
 }
@@ -278,28 +287,28 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
  * pointers (w1, w1s, w2, w2s, w3, w3s) */
 int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
                  const float *x, const int32_t *idx, const float *wgt, int s,
-                 int topk, float *y, const MoeWs &w) {
+                 int topk, float *y, const MoeWs &w, hipStream_t st) {
     const int nj = s * topk;
     ApusExpertTable t;
     t.w1 = tab; t.w1s = tab + E; t.w2 = tab + 2 * E; t.w2s = tab + 3 * E;
     t.w3 = tab + 4 * E; t.w3s = tab + 5 * E;
-    if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, w.xc, w.xs, g.stream), "act_quant"))
+    if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, w.xc, w.xs, st), "act_quant"))
         return 1;
     if (!launched(apus_launch_moe_route(idx, nj, topk, E, t, w.gm, w.um, w.eo, inter, dim,
-                                        w.pair, w.tok, w.e13, w.e2, g.stream), "moe_route"))
+                                        w.pair, w.tok, w.e13, w.e2, st), "moe_route"))
         return 1;
     ApusGemmArgs a{};
     a.acodes = w.xc; a.ascale = w.xs; a.ents = w.e13;
     a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1; a.max_m = (2 * nj + E - 1) / E;
-    if (!launched(apus_launch_gemm(APUS_W_FP4, &a, 2 * E, g.stream), "gemm w1/w3")) return 1;
-    if (!launched(apus_launch_swiglu_quant(w.gm, w.um, nj, inter, limit, w.hc, w.hs, g.stream),
+    if (!launched(apus_launch_gemm(APUS_W_FP4, &a, 2 * E, st), "gemm w1/w3")) return 1;
+    if (!launched(apus_launch_swiglu_quant(w.gm, w.um, nj, inter, limit, w.hc, w.hs, st),
                   "swiglu_quant"))
         return 1;
     ApusGemmArgs b{};
     b.acodes = w.hc; b.ascale = w.hs; b.ents = w.e2;
     b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1; b.max_m = (2 * nj + E - 1) / E;
-    if (!launched(apus_launch_gemm(APUS_W_FP4, &b, E, g.stream), "gemm w2")) return 1;
-    if (!launched(apus_launch_moe_accum(w.eo, wgt, s, topk, dim, y, g.stream), "moe_accum"))
+    if (!launched(apus_launch_gemm(APUS_W_FP4, &b, E, st), "gemm w2")) return 1;
+    if (!launched(apus_launch_moe_accum(w.eo, wgt, s, topk, dim, y, st), "moe_accum"))
         return 1;
     return 0;
 }
@@ -497,7 +506,7 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
         !upload(dx, x, (size_t)s * dim * 4) || !upload(didx, idx, (size_t)nj * 4) ||
         !upload(dwgt, wgt, (size_t)nj * 4))
         return 1;
-    if (moe_pipeline(E, dim, inter, w->limit, mw.tab, dx, didx, dwgt, s, topk, dy, mw)) return 1;
+    if (moe_pipeline(E, dim, inter, w->limit, mw.tab, dx, didx, dwgt, s, topk, dy, mw, g.stream)) return 1;
     if (!download(y, dy, (size_t)s * dim * 4) || !finish()) return 1;
     return 0;
 }
@@ -506,19 +515,31 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
 
 int apus_hip_act_quant_dev(const float *x, int M, int K, uint8_t *codes, float *scales) {
     if (!ensure_init() || !shape_ok(M, K, 1)) return 1;
-    return launched(apus_launch_act_quant(x, K, nullptr, M, K, codes, scales, g.stream), "act_quant") ? 0 : 1;
+    return launched(apus_launch_act_quant(x, K, nullptr, M, K, codes, scales, dev_stream()), "act_quant") ? 0 : 1;
 }
 
 int apus_hip_fp4_gemm_dev(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
                           const float *as, float *out, int M, int O, int K, int round_out) {
     if (!ensure_init() || !shape_ok(M, K, O)) return 1;
-    return gemm_dev(APUS_W_FP4, w, ws, acodes, as, out, M, O, K, round_out);
+    return gemm_dev(APUS_W_FP4, w, ws, acodes, as, out, M, O, K, round_out, dev_stream());
 }
 
 int apus_hip_fp8_gemm_dev(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
                           const float *as, float *out, int M, int O, int K, int round_out) {
     if (!ensure_init() || !shape_ok(M, K, O)) return 1;
-    return gemm_dev(APUS_W_FP8, w, ws, acodes, as, out, M, O, K, round_out);
+    return gemm_dev(APUS_W_FP8, w, ws, acodes, as, out, M, O, K, round_out, dev_stream());
+}
+
+int apus_hip_gemm_grouped_dev(int wfmt, const ApusHipGemmEnt *ents, int n_ent,
+                              const uint8_t *acodes, const float *as, int O, int K, int ldo,
+                              int round_out, int max_m) {
+    if (!ensure_init() || !shape_ok(1, K, O)) return 1;
+    if (wfmt != APUS_W_FP4 && wfmt != APUS_W_FP8) { set_err("gemm_grouped_dev: bad format"); return 1; }
+    static_assert(sizeof(ApusHipGemmEnt) == sizeof(ApusGemmEnt), "entry layout");
+    ApusGemmArgs a{};
+    a.acodes = acodes; a.ascale = as; a.ents = reinterpret_cast<const ApusGemmEnt *>(ents);
+    a.O = O; a.K = K; a.ldo = ldo; a.round_out = round_out; a.max_m = max_m;
+    return launched(apus_launch_gemm(wfmt, &a, n_ent, dev_stream()), "gemm_grouped_dev") ? 0 : 1;
 }
 
 size_t apus_hip_linear_workspace(int M, int K) {
@@ -531,8 +552,8 @@ static int linear_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const float
     if (!workspace) { set_err("linear_dev: workspace required"); return 1; }
     uint8_t *dc = (uint8_t *)workspace;
     float *dsc = (float *)(dc + align256((size_t)M * K));
-    if (!launched(apus_launch_act_quant(x, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
-    return gemm_dev(wfmt, w, ws, dc, dsc, out, M, O, K, 1);
+    if (!launched(apus_launch_act_quant(x, K, nullptr, M, K, dc, dsc, dev_stream()), "act_quant")) return 1;
+    return gemm_dev(wfmt, w, ws, dc, dsc, out, M, O, K, 1, dev_stream());
 }
 
 int apus_hip_fp4_linear_dev(const uint8_t *w, const uint8_t *ws, const float *x, float *out,
@@ -663,7 +684,7 @@ int apus_hip_moe_routed_dev(const ApusHipStore *st, int layer, const float *x, c
     }
     MoeWs mw = moe_carve(workspace, s, topk, st->E, st->dim, st->inter);
     return moe_pipeline(st->E, st->dim, st->inter, limit, st->layer_tab[layer], x, idx, wgt, s,
-                        topk, y, mw);
+                        topk, y, mw, dev_stream());
 }
 
 /* --------------------------------------------------------------- helpers */
@@ -694,7 +715,7 @@ int apus_hip_memset(void *dst, int value, size_t bytes) {
 
 int apus_hip_fill_random(void *dst, size_t bytes, uint64_t seed, uint64_t stream_id, int kind) {
     if (!ensure_init()) return 1;
-    return launched(apus_launch_fill((uint8_t *)dst, bytes, seed, stream_id, 0, kind, g.stream),
+    return launched(apus_launch_fill((uint8_t *)dst, bytes, seed, stream_id, 0, kind, dev_stream()),
                     "fill") ? 0 : 1;
 }
 
@@ -715,6 +736,44 @@ float apus_hip_timer_stop(void) {
     float ms = 0.0f;
     if (!ok(hipEventElapsedTime(&ms, g.ev0, g.ev1), "hipEventElapsedTime")) return -1.0f;
     return ms;
+}
+
+int apus_hip_lanes(int n) {
+    if (!ensure_init()) return 1;
+    if (n < 1 || n > 8) { set_err("lanes: 1..8"); return 1; }
+    for (int i = g.nlanes; i < n; i++) {
+        if (!ok(hipStreamCreateWithFlags(&g.lane[i], hipStreamNonBlocking), "hipStreamCreate") ||
+            !ok(hipEventCreateWithFlags(&g.lane_ev[i], hipEventDisableTiming), "hipEventCreate"))
+            return 1;
+        g.nlanes = i + 1;
+    }
+    return 0;
+}
+
+int apus_hip_lane(int i) {
+    if (!ensure_init()) return 1;
+    if (i < 0 || i >= g.nlanes) { set_err("lane %d not created", i); return 1; }
+    g.cur_lane = i;
+    return 0;
+}
+
+int apus_hip_fork(void) {
+    if (!ensure_init()) return 1;
+    if (!ok(hipEventRecord(g.lane_ev[0], g.lane[0]), "hipEventRecord")) return 1;
+    for (int i = 1; i < g.nlanes; i++)
+        if (!ok(hipStreamWaitEvent(g.lane[i], g.lane_ev[0], 0), "hipStreamWaitEvent")) return 1;
+    return 0;
+}
+
+int apus_hip_join(void) {
+    if (!ensure_init()) return 1;
+    for (int i = 1; i < g.nlanes; i++) {
+        if (!ok(hipEventRecord(g.lane_ev[i], g.lane[i]), "hipEventRecord") ||
+            !ok(hipStreamWaitEvent(g.lane[0], g.lane_ev[i], 0), "hipStreamWaitEvent"))
+            return 1;
+    }
+    g.cur_lane = 0;
+    return 0;
 }
 
 int apus_hip_graph_begin(void) {

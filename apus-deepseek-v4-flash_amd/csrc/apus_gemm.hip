@@ -298,21 +298,24 @@ __device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const uint8_t
     }
 }
 
-template <int WF, int R, int NS, int PD>
+template <int WF, int R, int NS, int PD, int KS>
 __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args) {
     extern __shared__ __align__(16) uint8_t lds[];
     constexpr int K = NS * 512, NQ = NS * 4, K16 = K / 16, LDK = K + 16;
     constexpr int STAGE = R * K16 / 256;               /* 16-byte loads per thread */
+    constexpr int NSW = NS / KS;                       /* slices per wave */
+    static_assert(NS % KS == 0 && PD <= NSW, "decode shape");
     const ApusGemmEnt ent = args.ents[blockIdx.y];
     if (ent.M <= args.m_min || (args.m_max > 0 && ent.M > args.m_max)) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int O = args.O;
     const int r = lane & 15, g = lane >> 4;
-    const int tile = blockIdx.x * APUS_DEC_WAVES + wave;
-    const bool tvalid = tile * 16 < O;                 /* uniform per wave */
-    const int o = tvalid ? tile * 16 + r : r;
+    /* KS waves share a row tile and split its K range; O % (64 / KS) == 0 */
+    const int tile = blockIdx.x * (APUS_DEC_WAVES / KS) + wave / KS;
+    const int kpart = wave % KS;
+    const int o = tile * 16 + r;
     uint8_t *lcodes = lds;
     uint8_t *lsc = lds + R * LDK;
+    apus_v4f *lred = reinterpret_cast<apus_v4f *>(lds + ((R * LDK + R * NQ + 15) & ~15));
     const uint8_t *wrow = ent.w + (size_t)o * (WF == APUS_W_FP4 ? (K >> 1) : K);
     const uint8_t *srow = WF == APUS_W_FP4 ? ent.ws + (size_t)o * (K >> 5)
                                            : ent.ws + (size_t)(o >> 7) * NQ;
@@ -357,20 +360,20 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
         }
         if (threadIdx.x < R * NQ && srr < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv);
         __syncthreads();
-        if (!tvalid) continue;
-
         const bool rvalid = r < rows;
         const int rr = rvalid ? r : 0;
         const uint8_t *arow = lcodes + rr * LDK + g * 16;
         const uint8_t *asrow = lsc + rr * NQ;
         const int z = rvalid ? -1 : 0;
+        const int sbase = kpart * NSW;
         apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
         ApusBFrag<WF> ring[PD];
 #pragma unroll
-        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, u, g);
+        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            ApusBFrag<WF> &cur = ring[s % PD];
+        for (int si = 0; si < NSW; ++si) {
+            const int s = sbase + si;
+            ApusBFrag<WF> &cur = ring[si % PD];
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
                 const int q = s * 4 + st;
@@ -392,12 +395,21 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                     acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, sa, (int)cur.s[st]);
                 }
             }
-            if (s + PD < NS) apus_load_b_full<WF>(cur, wrow, srow, s + PD, g);
+            if (si + PD < NSW) apus_load_b_full<WF>(cur, wrow, srow, s + PD, g);
+        }
+        if (KS > 1) {
+            /* the K parts of a tile meet in LDS; part 0 adds them in part order */
+            lred[wave * 64 + lane] = acc;
+            __syncthreads();
+            if (kpart == 0) {
+#pragma unroll
+                for (int p = 1; p < KS; ++p) acc += lred[(wave + p) * 64 + lane];
+            }
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             const int m = 4 * g + q;
-            if (m < rows) {
+            if (kpart == 0 && m < rows) {
                 float val = acc[q];
                 if (args.round_out) val = apus_bf16_rne(val);
                 const int mm = c0 + m;
@@ -550,19 +562,32 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
     /* grouped launches with K = 2048 or 4096: entries with at most 8 rows
      * take the decode schedule, larger ones the prefill schedule (two
      * launches over the same entry table, each skipping the other's entries) */
-    if (grouped && row_tiles >= 2048 && (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
+    if (grouped && row_tiles >= 512 && (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
         constexpr int R = 8;
         ApusGemmArgs d = *a;
         d.m_min = 0;
         d.m_max = R;
-        const size_t lds = (size_t)R * (a->K + 16) + (size_t)R * (a->K / 128);
-        dim3 gd(a->O / (16 * APUS_DEC_WAVES), n_ent), bd(256);
+        /* small launches split each tile's K over 2 waves for more streams */
+        const int ks = row_tiles < 2048 ? 2 : 1;
+        const size_t lds = (((size_t)R * (a->K + 16) + (size_t)R * (a->K / 128) + 15) & ~(size_t)15) +
+                           (ks > 1 ? 256 * sizeof(float) * 4 : 0);
+        dim3 gd(a->O / (16 * APUS_DEC_WAVES / ks), n_ent), bd(256);
         if (wfmt == APUS_W_FP4) {
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3>), gd, bd, lds, st, d);
-            else              hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 4, 3>), gd, bd, lds, st, d);
+            if (a->K == 4096) {
+                if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3, 2>), gd, bd, lds, st, d);
+                else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3, 1>), gd, bd, lds, st, d);
+            } else {
+                if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 4, 2, 2>), gd, bd, lds, st, d);
+                else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 4, 3, 1>), gd, bd, lds, st, d);
+            }
         } else {
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 8, 2>), gd, bd, lds, st, d);
-            else              hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2>), gd, bd, lds, st, d);
+            if (a->K == 4096) {
+                if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 8, 2, 2>), gd, bd, lds, st, d);
+                else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 8, 2, 1>), gd, bd, lds, st, d);
+            } else {
+                if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2, 2>), gd, bd, lds, st, d);
+                else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2, 1>), gd, bd, lds, st, d);
+            }
         }
         if (a->max_m > 0 && a->max_m <= R) return hipGetLastError();
         ApusGemmArgs p = *a;

@@ -165,6 +165,23 @@ int apus_hip_fp4_gemm_dev(const uint8_t *w, const uint8_t *ws,
 int apus_hip_fp8_gemm_dev(const uint8_t *w, const uint8_t *ws,
                           const uint8_t *acodes, const float *as, float *out,
                           int M, int O, int K, int round_out);
+/* Grouped block-scaled GEMM over an entry table in device memory (the
+ * device form of c/fp4.h:936-986, for callers that keep their grouping on
+ * the device). Entry i computes, for m < M,
+ *   out[orow(m) * ldo + o] = sum_k acodes[arow(m), k] * W[o, k]   (o < O)
+ * with arow(m) = arows ? arows[m] : a0 + m and orow(m) = orows ? orows[m] :
+ * o0 + m; W is MXFP4 [O, K/2] + [O, K/32] (wfmt 0) or FP8 [O, K] +
+ * [ceil(O/128), K/128] (wfmt 1). max_m is a hint (typical largest M; 0 =
+ * unknown). round_out: BF16-round the outputs. */
+typedef struct {
+    const uint8_t *w, *ws;
+    float *out;
+    const int32_t *arows, *orows;
+    int32_t a0, o0, M, reserved;
+} ApusHipGemmEnt;
+int apus_hip_gemm_grouped_dev(int wfmt, const ApusHipGemmEnt *ents, int n_ent,
+                              const uint8_t *acodes, const float *as, int O, int K,
+                              int ldo, int round_out, int max_m);
 /* Linear = act quant + GEMM (+ BF16 out) with a caller workspace of
  * apus_hip_linear_workspace(M, K) bytes. */
 size_t apus_hip_linear_workspace(int M, int K);
@@ -219,6 +236,18 @@ int   apus_hip_synchronize(void);
  * milliseconds since it (synchronises on the end event). */
 int   apus_hip_timer_start(void);
 float apus_hip_timer_stop(void);
+/* Concurrency lanes: extra HIP streams for the *_dev entry points, so that
+ * independent work (e.g. GEMVs of different experts) can overlap. Lane 0 is
+ * the backend stream. apus_hip_lanes(n) creates lanes 1..n-1 (n <= 8);
+ * apus_hip_lane(i) routes later *_dev launches to lane i; apus_hip_fork()
+ * makes every lane wait for the work issued so far on lane 0; apus_hip_join()
+ * makes lane 0 wait for every lane and selects lane 0 again. Fork/join are
+ * recorded into a graph when issued during capture. Host-pointer entry points
+ * always use lane 0. */
+int   apus_hip_lanes(int n);
+int   apus_hip_lane(int i);
+int   apus_hip_fork(void);
+int   apus_hip_join(void);
 /* Capture the launches issued on the backend stream between begin and end
  * into one HIP graph, then replay it (asynchronously) `times` times. Only
  * *_dev entry points may be issued while capturing. */

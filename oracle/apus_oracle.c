@@ -31,7 +31,9 @@ float orc_fp4_value(unsigned nib) {
     unsigned e = (nib >> 1) & 3u, m = nib & 1u;
     float mag = e ? (float)(2u + m) * (float)(1u << e) * 0.25f
                   : 0.5f * (float)m;
-    return (nib & 8u) ? -mag : mag;
+    /* the negative-zero code 0b1000 decodes to +0.0, as in the reference
+     * table (c/fp4.h:204-207), so dequantised rows match it bit for bit */
+    return ((nib & 8u) && mag != 0.0f) ? -mag : mag;
 }
 
 void orc_fp4_dequant_row(const uint8_t *packed, const uint8_t *scales,

@@ -121,3 +121,58 @@ def test_moe_routed_prefill_shape(hip, oracle, rng):
     mr = max_rel(got, want)
     print(f"moe prefill-shape: max_rel={mr:.3g} identical={np.mean(got == want):.1%}")
     assert mr <= 2.0 ** -7
+
+
+def _grouped_dev(hip, wfmt, weights, Ms, codes, scales, O, K):
+    """Run apus_hip_gemm_grouped_dev over entries (weight j = weights[i % len])
+    with activation rows packed entry after entry; returns per-entry outputs."""
+    import ctypes as C
+    L = hip.lib()
+    dev = []
+    dc = hip.DevBuf.from_array(codes)
+    ds = hip.DevBuf.from_array(scales)
+    dw = [(hip.DevBuf.from_array(w), hip.DevBuf.from_array(ws)) for w, ws in weights]
+    rows = int(sum(Ms))
+    dout = hip.DevBuf(max(rows, 1) * O * 4)
+    ents = (hip.ApusHipGemmEnt * len(Ms))()
+    m0 = 0
+    for i, M in enumerate(Ms):
+        w, ws = dw[i % len(dw)]
+        ents[i] = hip.ApusHipGemmEnt(w.ptr, ws.ptr, dout.ptr, None, None, m0, m0, M, 0)
+        m0 += M
+    de = hip.DevBuf(C.sizeof(ents))
+    hip._check(L.apus_hip_h2d(de.ptr, C.addressof(ents), C.sizeof(ents)), "h2d")
+    hint = max(Ms) if max(Ms) <= 8 else 0
+    hip._check(L.apus_hip_gemm_grouped_dev(wfmt, de.ptr, len(Ms), dc.ptr, ds.ptr, O, K, O, 0,
+                                           hint), "grouped")
+    out = dout.to_array(np.float32, (max(rows, 1), O))
+    dev.extend([dc, ds, dout, de] + [b for p in dw for b in p])
+    res, m0 = [], 0
+    for M in Ms:
+        res.append(out[m0:m0 + M])
+        m0 += M
+    return res
+
+
+@pytest.mark.parametrize("wfmt,K,Ms", [
+    (0, 4096, [1, 3, 0, 8, 2] * 8),      # decode schedule, K split over 2 waves
+    (0, 2048, [2, 1, 5, 8] * 10),        # decode, K split, K = 2048
+    (1, 4096, [1, 2, 7] * 14),           # FP8 weights, decode with K split
+    (1, 2048, [1, 2, 7, 3] * 40),        # FP8 weights, decode, whole K per wave
+    (1, 2048, [30, 3, 17, 9] * 34),      # FP8 weights, prefill + decode
+])
+def test_grouped_dev_schedules(hip, oracle, rng, wfmt, K, Ms):
+    from helpers import fp8_weights
+    O = 256
+    weights = [fp4_weights(rng, O, K) if wfmt == 0 else fp8_weights(rng, O, K) for _ in range(4)]
+    rows = sum(Ms)
+    c, s = oracle.act_quant(acts(rng, rows, K, 2.0))
+    outs = _grouped_dev(hip, wfmt, weights, Ms, c, s, O, K)
+    m0 = 0
+    for i, M in enumerate(Ms):
+        if M and i % 5 == 0:
+            w, ws = weights[i % 4]
+            f = oracle.fp4_gemm if wfmt == 0 else oracle.fp8_gemm
+            want = f(w, ws, c[m0:m0 + M].copy(), s[m0:m0 + M].copy())
+            assert max_rel(outs[i], want) <= 1e-3, (i, M)
+        m0 += M
