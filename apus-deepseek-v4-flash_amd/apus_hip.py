@@ -116,6 +116,7 @@ SIGNATURES = {
     "apus_hip_h2d": (C.c_int, [vp, vp, C.c_size_t]),
     "apus_hip_d2h": (C.c_int, [vp, vp, C.c_size_t]),
     "apus_hip_memset": (C.c_int, [vp, C.c_int, C.c_size_t]),
+    "apus_hip_d2d": (C.c_int, [vp, vp, C.c_size_t]),
     "apus_hip_fill_random": (C.c_int, [vp, C.c_size_t, C.c_uint64, C.c_uint64, C.c_int]),
     "apus_hip_synchronize": (C.c_int, []),
     "apus_hip_timer_start": (C.c_int, []),

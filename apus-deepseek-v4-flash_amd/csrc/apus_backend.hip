@@ -708,6 +708,11 @@ int apus_hip_d2h(void *dst, const void *src, size_t bytes) {
     return download(dst, src, bytes) && finish() ? 0 : 1;
 }
 
+int apus_hip_d2d(void *dst, const void *src, size_t bytes) {
+    if (!ensure_init()) return 1;
+    return ok(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, dev_stream()), "D2D") ? 0 : 1;
+}
+
 int apus_hip_memset(void *dst, int value, size_t bytes) {
     if (!ensure_init()) return 1;
     return ok(hipMemsetAsync(dst, value, bytes, g.stream), "hipMemsetAsync") ? 0 : 1;

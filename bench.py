@@ -33,6 +33,10 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 FP4_PEAK_TFLOPS = 10100.0      # dense MXFP4 MFMA
 FP8_PEAK_TFLOPS = 5000.0       # dense FP8 MFMA
 METRIC = "MXFP4 expert GEMV GB/s (%HBM peak) @M=1; MoE grouped-GEMM TFLOP/s @512 tok"
+# HBM bytes per grouped 12-GEMV launch measured with rocprofv3 FETCH_SIZE and
+# WRITE_SIZE (FETCH scaled x2.0 from a 256 MiB copy calibration); command and
+# counts in profiles/config0_mxfp4_gemv_m1.txt. Re-measure when the kernel changes.
+CONFIG0_TRAFFIC_BYTES = 56300452
 
 
 def log(*a):
@@ -313,6 +317,8 @@ def main():
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list: gemv,fp8,decode,prefill")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
@@ -373,6 +379,16 @@ def main():
                            "config3_unique_experts": p["unique_experts"]})
         H.lib().apus_hip_store_free(store)
 
+    if args.calibrate_copy:
+        # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE counters give
+        # the scale between the counters and bytes moved
+        nb = 256 << 20
+        src, dst = dev.alloc(nb), dev.alloc(nb)
+        H._check(H.lib().apus_hip_fill_random(src.ptr, nb, 9, 9, 0), "fill")
+        for _ in range(2):
+            H._check(H.lib().apus_hip_d2d(dst.ptr, src.ptr, nb), "d2d")
+        H.synchronize()
+        log(f"[bench] calibration copy: 2 x {nb} bytes")
     cpu = None if args.no_cpu else cpu_baseline()
     if g is None:
         print(json.dumps({"metric": METRIC, "extras": extras, "cpu_baseline": cpu}))
@@ -406,7 +422,7 @@ def main():
                      "frac": round(g["launch_bytes"] / (g["launch_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "kernel": "apus_gemm_decode_kernel (grouped, 12 GEMVs)",
                      "launch_us": round(g["launch_us"], 3), "bytes_per_launch": g["launch_bytes"],
-                     "traffic": None},
+                     "traffic": CONFIG0_TRAFFIC_BYTES},
         "cpu_baseline": cpu,
         "extras": extras,
     }

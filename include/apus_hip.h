@@ -229,6 +229,8 @@ int   apus_hip_free(void *p);
 int   apus_hip_h2d(void *dst, const void *src, size_t bytes);
 int   apus_hip_d2h(void *dst, const void *src, size_t bytes);
 int   apus_hip_memset(void *dst, int value, size_t bytes);
+/* device-to-device copy on the current lane (asynchronous) */
+int   apus_hip_d2d(void *dst, const void *src, size_t bytes);
 int   apus_hip_fill_random(void *dst, size_t bytes, uint64_t seed,
                            uint64_t stream_id, int kind);
 int   apus_hip_synchronize(void);
