@@ -320,9 +320,10 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
     const uint8_t *srow = WF == APUS_W_FP4 ? ent.ws + (size_t)o * (K >> 5)
                                            : ent.ws + (size_t)(o >> 7) * NQ;
 
+    const int sbase = kpart * NSW;
     for (int c0 = 0; c0 < ent.M; c0 += R) {
         const int rows = min(R, ent.M - c0);
-        __syncthreads();
+        apus_lds_barrier();           /* the previous chunk's LDS reads are done */
         /* stage: row indices, then every code/scale load, then the LDS
          * writes (no load waits on another load's result more than once) */
         int ridx[R];
@@ -351,6 +352,11 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
 #pragma unroll
         for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
         const float scv = args.ascale[(size_t)sar * NQ + (si - srr * NQ)];
+        /* weight prefetch ring: issued after the staging loads (so waiting
+         * for those does not wait for these) and before the LDS hand-off */
+        ApusBFrag<WF> ring[PD];
+#pragma unroll
+        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
 #pragma unroll
         for (int j = 0; j < STAGE; ++j) {
             const int rsub = threadIdx.x / K16;
@@ -359,17 +365,13 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                 *reinterpret_cast<uint4 *>(lcodes + (j * RPJ + rsub) * LDK + cc * 16) = v[j];
         }
         if (threadIdx.x < R * NQ && srr < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv);
-        __syncthreads();
+        apus_lds_barrier();
         const bool rvalid = r < rows;
         const int rr = rvalid ? r : 0;
         const uint8_t *arow = lcodes + rr * LDK + g * 16;
         const uint8_t *asrow = lsc + rr * NQ;
         const int z = rvalid ? -1 : 0;
-        const int sbase = kpart * NSW;
         apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
-        ApusBFrag<WF> ring[PD];
-#pragma unroll
-        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
 #pragma unroll
         for (int si = 0; si < NSW; ++si) {
             const int s = sbase + si;

@@ -266,6 +266,79 @@ def bench_moe(H, dev, store, layers, s, idx, wgt, steps, dim=4096, inter=2048, E
 
 # ------------------------------------------------------------------ CPU baseline
 
+def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=2048, topk=6):
+    """Config 4: L MoE layers resident in HBM (256 MXFP4 experts each, config-2
+    shapes) plus one FP8 [4096, 4096] projection per layer, ~148 GB. A token
+    step runs, per layer, the FP8 linear and the routed dispatch of the
+    token's top-6 experts (seeded gating, different per layer and token).
+    `tokens` distinct steps are captured in one HIP graph and replayed."""
+    import ctypes as C
+    L_ = H.lib()
+    err = C.create_string_buffer(256)
+    t0 = time.perf_counter()
+    store = L_.apus_hip_store_create(L, E, dim, inter, err, 256)
+    if not store:
+        raise RuntimeError("store_create: " + err.value.decode())
+    try:
+        log(f"[bench] config 4: filling {L} layers x {E} experts "
+            f"({L_.apus_hip_store_bytes(store) / 1e9:.1f} GB) on device")
+        H._check(L_.apus_hip_store_fill_random(store, 44), "store fill")
+        dbytes, dsb = dim * dim, (dim // 128) * (dim // 128)
+        wd = dev.alloc(dbytes * L)
+        wds = dev.alloc(dsb * L)
+        H._check(L_.apus_hip_fill_random(wd.ptr, dbytes * L, 44, 1 << 40, 2), "fill fp8")
+        H._check(L_.apus_hip_fill_random(wds.ptr, dsb * L, 44, (1 << 40) + 1, 3), "fill fp8 s")
+        H.synchronize()
+        fill_s = time.perf_counter() - t0
+        log(f"[bench] config 4: resident in {fill_s:.1f} s")
+        rng = np.random.default_rng(4)
+        idx = np.zeros((tokens, L, topk), np.int32)
+        wgt = np.zeros((tokens, L, topk), np.float32)
+        for t in range(tokens):
+            i, w = gate_routing(rng, L, E, topk)
+            idx[t], wgt[t] = i, w
+        didx, dwgt = dev.upload(idx), dev.upload(wgt)
+        x = (np.random.default_rng(5).standard_normal((1, dim)).astype(np.float32).view(np.uint32)
+             & 0xFFFF0000).view(np.float32)
+        dx = dev.upload(x)
+        hd = dev.alloc(dim * 4)
+        y = dev.alloc(dim * 4 * L)
+        wlin = dev.alloc(L_.apus_hip_linear_workspace(1, dim))
+        wsp = dev.alloc(L_.apus_hip_moe_workspace(store, 1, topk))
+        per = topk * 4
+
+        def step(t):
+            for l in range(L):
+                H._check(L_.apus_hip_fp8_linear_dev(wd.ptr + l * dbytes, wds.ptr + l * dsb, dx.ptr,
+                                                    hd.ptr, 1, dim, dim, wlin.ptr), "fp8 linear")
+                off = (t * L + l) * per
+                H._check(L_.apus_hip_moe_routed_dev(store, l, dx.ptr, didx.ptr + off,
+                                                    dwgt.ptr + off, 1, topk, 10.0,
+                                                    y.ptr + l * dim * 4, wsp.ptr), "moe")
+
+        step(0)
+        H.synchronize()
+        H._check(L_.apus_hip_graph_begin(), "graph_begin")
+        for t in range(tokens):
+            step(t)
+        H._check(L_.apus_hip_graph_end(), "graph_end")
+        H._check(L_.apus_hip_graph_replay(1), "warm replay")
+        H.synchronize()
+        H._check(L_.apus_hip_timer_start(), "timer")
+        H._check(L_.apus_hip_graph_replay(reps), "replay")
+        ms = L_.apus_hip_timer_stop()
+        n = tokens * reps
+        t_tok = ms * 1e-3 / n
+        expert_bytes = 3 * (inter * dim // 2 + inter * dim // 32)
+        tok_bytes = L * (topk * expert_bytes + dbytes + dsb)
+        return {"tok_s": 1.0 / t_tok, "ms_per_token": t_tok * 1e3, "layers": L,
+                "resident_GB": (L_.apus_hip_store_bytes(store) + (dbytes + dsb) * L) / 1e9,
+                "bytes_per_token": tok_bytes, "gbs": tok_bytes / t_tok / 1e9,
+                "launches_per_token": L * 8, "fill_s": fill_s}
+    finally:
+        L_.apus_hip_store_free(store)
+
+
 def cpu_baseline(O=2048, K=4096, budget_s=12.0):
     """apus's own apus_fp4_gemm_mt (AVX2 rows + pthread pool) on config 0."""
     threads = min(os.cpu_count() or 1, 16)
@@ -316,7 +389,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: gemv,fp8,decode,prefill")
+    ap.add_argument("--only", default="", help="comma list: gemv,fp8,decode,prefill,full")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -378,6 +451,17 @@ def main():
                            "config3_weight_GBs": round(p["gbs"], 1),
                            "config3_unique_experts": p["unique_experts"]})
         H.lib().apus_hip_store_free(store)
+    if not args.skip_extras and want("full"):
+        log("[bench] config 4 full-footprint decode")
+        f = bench_full_footprint(H, dev)
+        extras.update({"config4_tok_s": round(f["tok_s"], 1),
+                       "config4_ms_per_token": round(f["ms_per_token"], 3),
+                       "config4_GBs": round(f["gbs"], 1),
+                       "config4_hbm_frac": round(f["gbs"] / HBM_PEAK_GBS, 4),
+                       "config4_layers": f["layers"],
+                       "config4_resident_GB": round(f["resident_GB"], 1),
+                       "config4_bytes_per_token": f["bytes_per_token"],
+                       "config4_launches_per_token": f["launches_per_token"]})
 
     if args.calibrate_copy:
         # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE counters give

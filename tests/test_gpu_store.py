@@ -1,0 +1,105 @@
+"""HBM-resident expert store (apus_hip_store_*) and the device-resident routed
+dispatch (apus_hip_moe_routed_dev).
+
+* Device-generated synthetic weights equal the host twin of the counter
+  generator (orc_fill_bytes) byte for byte, so the oracle can rebuild them.
+* apus_hip_moe_routed_dev over the store matches the oracle's routed
+  dispatch (bar 2^-7 as in test_gpu_moe.py) and equals the host-pointer hook
+  bit for bit (same kernels, same data).
+* store_put / store_get round-trip the six tensors of an expert.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from helpers import acts, max_rel, moe_experts, topk_routing
+
+pytestmark = pytest.mark.gpu
+
+KINDS = (0, 1, 0, 1, 0, 1)       # w1, w1s, w2, w2s, w3, w3s
+
+
+def shapes(dim, inter):
+    return [(inter, dim // 2), (inter, dim // 32), (dim, inter // 2), (dim, inter // 32),
+            (inter, dim // 2), (inter, dim // 32)]
+
+
+@pytest.fixture
+def store(hip):
+    made = []
+
+    def make(L, E, dim, inter):
+        err = C.create_string_buffer(256)
+        st = hip.lib().apus_hip_store_create(L, E, dim, inter, err, 256)
+        assert st, err.value
+        made.append(st)
+        return st
+    yield make
+    for st in made:
+        hip.lib().apus_hip_store_free(st)
+
+
+def read_expert(hip, st, layer, e, dim, inter):
+    ptrs = (C.c_void_p * 6)()
+    hip._check(hip.lib().apus_hip_store_get(st, layer, e, ptrs), "store_get")
+    out = []
+    for p, shp in zip(ptrs, shapes(dim, inter)):
+        a = np.empty(shp, np.uint8)
+        hip._check(hip.lib().apus_hip_d2h(a.ctypes.data, p, a.nbytes), "d2h")
+        out.append(a)
+    return tuple(out)
+
+
+def host_expert(oracle, seed, layer, e, E, dim, inter):
+    out = []
+    for t, shp in enumerate(shapes(dim, inter)):
+        sid = (layer * E + e) * 8 + t
+        out.append(oracle.fill_bytes(seed, sid, int(np.prod(shp)), KINDS[t]).reshape(shp))
+    return tuple(out)
+
+
+def test_store_fill_matches_host_generator(hip, oracle, store):
+    L, E, dim, inter = 2, 5, 512, 256
+    st = store(L, E, dim, inter)
+    hip._check(hip.lib().apus_hip_store_fill_random(st, 11), "fill")
+    for layer, e in ((0, 0), (1, 4), (0, 3)):
+        dev = read_expert(hip, st, layer, e, dim, inter)
+        host = host_expert(oracle, 11, layer, e, E, dim, inter)
+        for d, h in zip(dev, host):
+            assert np.array_equal(d, h)
+
+
+def test_store_put_get_roundtrip(hip, store, rng):
+    dim, inter = 256, 128
+    st = store(1, 3, dim, inter)
+    ex = moe_experts(rng, 1, dim, inter)[0]
+    W = [hip.ApusFp4W(t.ctypes.data_as(hip.u8p), s.ctypes.data_as(hip.u8p), o, k)
+         for t, s, o, k in ((ex[0], ex[1], inter, dim), (ex[2], ex[3], dim, inter),
+                            (ex[4], ex[5], inter, dim))]
+    hip._check(hip.lib().apus_hip_store_put(st, 0, 2, C.byref(W[0]), C.byref(W[1]),
+                                            C.byref(W[2])), "put")
+    back = read_expert(hip, st, 0, 2, dim, inter)
+    for a, b in zip(ex, back):
+        assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("E,dim,inter,s,topk", [(16, 512, 256, 5, 4), (32, 2048, 2048, 3, 6)])
+def test_moe_routed_dev_over_store(hip, oracle, store, rng, E, dim, inter, s, topk):
+    L, seed, layer = 2, 5, 1
+    st = store(L, E, dim, inter)
+    hip._check(hip.lib().apus_hip_store_fill_random(st, seed), "fill")
+    experts = [host_expert(oracle, seed, layer, e, E, dim, inter) for e in range(E)]
+    x = acts(rng, s, dim)
+    idx, wgt = topk_routing(rng, s, E, topk)
+    want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
+    L_ = hip.lib()
+    dx, di, dw = (hip.DevBuf.from_array(a) for a in (x, idx, wgt))
+    dy = hip.DevBuf(s * dim * 4)
+    wsp = hip.DevBuf(L_.apus_hip_moe_workspace(st, s, topk))
+    hip._check(L_.apus_hip_moe_routed_dev(st, layer, dx.ptr, di.ptr, dw.ptr, s, topk, 10.0,
+                                          dy.ptr, wsp.ptr), "moe_routed_dev")
+    got = dy.to_array(np.float32, (s, dim))
+    assert max_rel(got, want) <= 2.0 ** -7
+    host = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=777 + E)
+    assert np.array_equal(got.view(np.uint32), host.view(np.uint32))
