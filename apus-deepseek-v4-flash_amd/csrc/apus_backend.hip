@@ -18,6 +18,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
@@ -250,7 +251,7 @@ int gemm_host(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acod
 struct MoeWs {
     uint8_t *xc; float *xs;
     int32_t *pair, *tok;
-    ApusGemmEnt *e13, *e2;
+    ApusGemmEnt *e13s, *e2s, *e13l, *e2l;   /* few-row and many-row expert tables */
     float *gm, *um; uint8_t *hc; float *hs; float *eo;
     uint8_t **tab;
     size_t total;
@@ -265,7 +266,8 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
     auto take = [&](size_t n) { size_t o = off; off += align256(n); return o; };
     size_t o_xc = take((size_t)s * dim), o_xs = take((size_t)s * (dim / 128) * 4);
     size_t o_pair = take(nj * 4), o_tok = take(nj * 4);
-    size_t o_e13 = take(2 * (size_t)E * sizeof(ApusGemmEnt)), o_e2 = take((size_t)E * sizeof(ApusGemmEnt));
+    const size_t te = (size_t)E * sizeof(ApusGemmEnt);
+    size_t o_e13s = take(2 * te), o_e2s = take(te), o_e13l = take(2 * te), o_e2l = take(te);
     size_t o_g = take(nj * inter * 4), o_u = take(nj * inter * 4);
     size_t o_hc = take(nj * inter), o_hs = take(nj * (inter / 128) * 4);
     size_t o_eo = take(nj * dim * 4);
@@ -275,7 +277,8 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
         uint8_t *b = (uint8_t *)base;
         w.xc = b + o_xc; w.xs = (float *)(b + o_xs);
         w.pair = (int32_t *)(b + o_pair); w.tok = (int32_t *)(b + o_tok);
-        w.e13 = (ApusGemmEnt *)(b + o_e13); w.e2 = (ApusGemmEnt *)(b + o_e2);
+        w.e13s = (ApusGemmEnt *)(b + o_e13s); w.e2s = (ApusGemmEnt *)(b + o_e2s);
+        w.e13l = (ApusGemmEnt *)(b + o_e13l); w.e2l = (ApusGemmEnt *)(b + o_e2l);
         w.gm = (float *)(b + o_g); w.um = (float *)(b + o_u);
         w.hc = b + o_hc; w.hs = (float *)(b + o_hs); w.eo = (float *)(b + o_eo);
         w.tab = (uint8_t **)(b + o_tab);
@@ -294,20 +297,39 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
     t.w3 = tab + 4 * E; t.w3s = tab + 5 * E;
     if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, w.xc, w.xs, st), "act_quant"))
         return 1;
-    if (!launched(apus_launch_moe_route(idx, nj, topk, E, t, w.gm, w.um, w.eo, inter, dim,
-                                        w.pair, w.tok, w.e13, w.e2, st), "moe_route"))
+    /* experts with at most SMALL pairs take the few-row GEMM schedule; at
+     * most min(E, nj) experts are small and at most nj / (SMALL + 1) are
+     * large, so the launches cover only that many table slots */
+    constexpr int SMALL = 8;
+    if (!launched(apus_launch_moe_route(idx, nj, topk, E, t, w.gm, w.um, w.eo, w.pair, w.tok,
+                                        w.e13s, w.e2s, w.e13l, w.e2l, SMALL, st), "moe_route"))
         return 1;
+    const int n_small = std::min(E, nj), n_large = std::min(E, nj / (SMALL + 1));
     ApusGemmArgs a{};
-    a.acodes = w.xc; a.ascale = w.xs; a.ents = w.e13;
-    a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1; a.max_m = (2 * nj + E - 1) / E;
-    if (!launched(apus_launch_gemm(APUS_W_FP4, &a, 2 * E, st), "gemm w1/w3")) return 1;
+    a.acodes = w.xc; a.ascale = w.xs;
+    a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
+    ApusGemmArgs b{};
+    b.acodes = w.hc; b.ascale = w.hs;
+    b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int n = pass ? n_large : n_small;
+        if (!n) continue;
+        a.ents = pass ? w.e13l : w.e13s;
+        a.max_m = pass ? 0 : SMALL;
+        a.min_m = pass ? SMALL : 0;
+        if (!launched(apus_launch_gemm(APUS_W_FP4, &a, 2 * n, st), "gemm w1/w3")) return 1;
+    }
     if (!launched(apus_launch_swiglu_quant(w.gm, w.um, nj, inter, limit, w.hc, w.hs, st),
                   "swiglu_quant"))
         return 1;
-    ApusGemmArgs b{};
-    b.acodes = w.hc; b.ascale = w.hs; b.ents = w.e2;
-    b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1; b.max_m = (2 * nj + E - 1) / E;
-    if (!launched(apus_launch_gemm(APUS_W_FP4, &b, E, st), "gemm w2")) return 1;
+    for (int pass = 0; pass < 2; ++pass) {
+        const int n = pass ? n_large : n_small;
+        if (!n) continue;
+        b.ents = pass ? w.e2l : w.e2s;
+        b.max_m = pass ? 0 : SMALL;
+        b.min_m = pass ? SMALL : 0;
+        if (!launched(apus_launch_gemm(APUS_W_FP4, &b, n, st), "gemm w2")) return 1;
+    }
     if (!launched(apus_launch_moe_accum(w.eo, wgt, s, topk, dim, y, st), "moe_accum"))
         return 1;
     return 0;

@@ -564,8 +564,11 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
     /* grouped launches with K = 2048 or 4096: entries with at most 8 rows
      * take the decode schedule, larger ones the prefill schedule (two
      * launches over the same entry table, each skipping the other's entries) */
-    if (grouped && row_tiles >= 512 && (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
-        constexpr int R = 8;
+    constexpr int R = 8;
+    if (grouped && (row_tiles >= 512 || (a->max_m > 0 && a->max_m <= R)) &&
+        (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
+        const bool run_dec = !(a->min_m >= R);
+        const bool run_pre = !(a->max_m > 0 && a->max_m <= R);
         ApusGemmArgs d = *a;
         d.m_min = 0;
         d.m_max = R;
@@ -574,7 +577,8 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
         const size_t lds = (((size_t)R * (a->K + 16) + (size_t)R * (a->K / 128) + 15) & ~(size_t)15) +
                            (ks > 1 ? 256 * sizeof(float) * 4 : 0);
         dim3 gd(a->O / (16 * APUS_DEC_WAVES / ks), n_ent), bd(256);
-        if (wfmt == APUS_W_FP4) {
+        if (!run_dec) {
+        } else if (wfmt == APUS_W_FP4) {
             if (a->K == 4096) {
                 if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3, 2>), gd, bd, lds, st, d);
                 else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3, 1>), gd, bd, lds, st, d);
@@ -591,7 +595,7 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
                 else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2, 1>), gd, bd, lds, st, d);
             }
         }
-        if (a->max_m > 0 && a->max_m <= R) return hipGetLastError();
+        if (!run_pre) return hipGetLastError();
         ApusGemmArgs p = *a;
         p.m_min = R;
         p.m_max = 0;

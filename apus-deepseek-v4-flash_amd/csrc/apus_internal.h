@@ -32,8 +32,10 @@ typedef struct {
     const ApusGemmEnt *ents; /* grouped: device array; else NULL */
     ApusGemmEnt ent0;        /* the entry when ents == NULL */
     int O, K, ldo, round_out;
-    int max_m;               /* typical largest M of an entry (a performance hint
-                              * only: any M is computed; 0 = unknown) */
+    int max_m;               /* upper bound on every entry's M (0 = unknown); a
+                              * launch with max_m <= 8 runs only the few-row
+                              * schedule */
+    int min_m;               /* every entry has M = 0 or M > min_m (0 = unknown) */
     int m_min, m_max;        /* set by the launcher: a kernel computes only the
                               * entries with m_min < M <= m_max (m_max 0: no cap) */
 } ApusGemmArgs;
@@ -55,21 +57,23 @@ hipError_t apus_launch_swiglu_quant(const float *g, const float *u, int M,
                                     float *scales, hipStream_t st);
 
 /* Counting sort of the routed pairs by expert and GEMM entry tables.
- * idx [nj] (nj = s * topk) expert ids; writes pair_sorted [nj] (pair q),
- * tok_sorted [nj] (q / topk), and entry tables e13 [2E] (w1 then w3, output
- * rows in sorted order), e2 [E] (output rows = pair ids). The weight
- * pointer tables are device arrays of E pointers each. */
+ * idx [nj] (nj = s * topk) expert ids in [0, E), E <= 1024; writes
+ * pair_sorted [nj] (pair q), tok_sorted [nj] (q / topk) and two sets of
+ * entry tables: experts with 1..small_max pairs go, in expert order, to the
+ * front of e13s [2E] (w1 then w3 of each expert, output rows in sorted
+ * order) and e2s [E] (output rows = pair ids); experts with more pairs go to
+ * e13l / e2l the same way. Slots past the listed experts have M = 0. The
+ * weight pointer tables are device arrays of E pointers each. */
 typedef struct {
     const uint8_t *const *w1, *const *w1s, *const *w2, *const *w2s,
                   *const *w3, *const *w3s;
 } ApusExpertTable;
 
 hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
-                                 ApusExpertTable tab, float *g, float *u,
-                                 float *eo, int inter, int dim,
+                                 ApusExpertTable tab, float *g, float *u, float *eo,
                                  int32_t *pair_sorted, int32_t *tok_sorted,
-                                 ApusGemmEnt *e13, ApusGemmEnt *e2,
-                                 hipStream_t st);
+                                 ApusGemmEnt *e13s, ApusGemmEnt *e2s, ApusGemmEnt *e13l,
+                                 ApusGemmEnt *e2l, int small_max, hipStream_t st);
 
 /* y[t, i] = sum_j wgt[t, j] * eo[t*topk + j, i] in j order (mul, then add,
  * each rounded), starting from +0. */

@@ -92,57 +92,97 @@ hipError_t apus_launch_swiglu_quant(const float *g, const float *u, int M,
 
 /* ------------------------------------------------------------ MoE route */
 
-/* Single workgroup: histogram of expert ids, exclusive scan, placement.
- * Placement order inside an expert is whatever the LDS atomics give: each
- * output row of the grouped GEMMs depends only on its own activation row,
- * and results are written back by pair id, so the order is not observable
- * in the results. */
-__global__ __launch_bounds__(1024) void apus_moe_route_kernel(
-    const int32_t *__restrict__ idx, int nj, int topk, int E,
-    ApusExpertTable tab, float *g, float *u, float *eo, int inter, int dim,
-    int32_t *pair_sorted, int32_t *tok_sorted, ApusGemmEnt *e13,
-    ApusGemmEnt *e2) {
-    extern __shared__ int sh[];
-    int *cnt = sh, *off = sh + E, *cur = sh + 2 * E;
-    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
-    __syncthreads();
-    for (int q = threadIdx.x; q < nj; q += blockDim.x) atomicAdd(&cnt[idx[q]], 1);
+/* Exclusive prefix sum of one int per thread over the workgroup (at most 16
+ * waves); sw is 17 ints of LDS; total receives the sum of all v. */
+__device__ __forceinline__ int apus_block_scan_excl(int v, int *sw, int &total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nw = (blockDim.x + 63) >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) sw[wave] = x;
     __syncthreads();
     if (threadIdx.x == 0) {
         int run = 0;
-        for (int e = 0; e < E; ++e) { off[e] = run; cur[e] = run; run += cnt[e]; }
+        for (int w = 0; w < nw; ++w) { const int t = sw[w]; sw[w] = run; run += t; }
+        sw[16] = run;
     }
     __syncthreads();
-    for (int q = threadIdx.x; q < nj; q += blockDim.x) {
-        const int pos = atomicAdd(&cur[idx[q]], 1);
+    const int r = x - v + sw[wave];
+    total = sw[16];
+    __syncthreads();
+    return r;
+}
+
+/* Single workgroup, one thread per expert (E <= 1024): histogram of expert
+ * ids, exclusive scans, placement, entry tables. Experts with 1..small_max
+ * pairs are listed (in expert order) at the front of the small tables, the
+ * others with pairs at the front of the large tables; the remaining slots
+ * get M = 0. Placement order inside an expert is whatever the LDS atomics
+ * give: each output row of the grouped GEMMs depends only on its own
+ * activation row, and results are written back by pair id, so the order is
+ * not observable in the results. */
+__global__ __launch_bounds__(1024) void apus_moe_route_kernel(
+    const int32_t *__restrict__ idx, int nj, int topk, int E,
+    ApusExpertTable tab, float *g, float *u, float *eo,
+    int32_t *pair_sorted, int32_t *tok_sorted, ApusGemmEnt *e13s, ApusGemmEnt *e2s,
+    ApusGemmEnt *e13l, ApusGemmEnt *e2l, int small_max) {
+    __shared__ int cnt[1024], cur[1024], sw[17];
+    const int e = threadIdx.x;
+    cnt[e] = 0;
+    __syncthreads();
+    for (int q = e; q < nj; q += blockDim.x) {
+        const int id = idx[q];
+        if ((unsigned)id < (unsigned)E) atomicAdd(&cnt[id], 1);
+    }
+    __syncthreads();
+    const int c = e < E ? cnt[e] : 0;
+    int total;
+    const int o0 = apus_block_scan_excl(c, sw, total);
+    cur[e] = o0;
+    const int small = c > 0 && c <= small_max, large = c > small_max;
+    int packed_total;
+    const int packed = apus_block_scan_excl(small | (large << 16), sw, packed_total);
+    const int ns = packed_total & 0xffff, nl = packed_total >> 16;
+    for (int q = e; q < nj; q += blockDim.x) {
+        const int id = idx[q];
+        if ((unsigned)id >= (unsigned)E) continue;      /* ids outside [0, E) are dropped */
+        const int pos = atomicAdd(&cur[id], 1);
         pair_sorted[pos] = q;
         tok_sorted[pos] = q / topk;
     }
-    for (int e = threadIdx.x; e < E; e += blockDim.x) {
-        const int c = cnt[e], o0 = off[e];
-        ApusGemmEnt a;
-        a.arows = tok_sorted + o0; a.orows = nullptr; a.a0 = 0; a.o0 = o0; a.M = c; a.pad = 0;
+    if (e >= E) return;
+    ApusGemmEnt a;
+    a.arows = tok_sorted + o0; a.orows = nullptr; a.a0 = 0; a.o0 = o0; a.M = c; a.pad = 0;
+    ApusGemmEnt b;
+    b.w = tab.w2[e]; b.ws = tab.w2s[e]; b.out = eo;
+    b.arows = nullptr; b.orows = pair_sorted + o0; b.a0 = o0; b.o0 = 0; b.M = c; b.pad = 0;
+    if (small | large) {
+        const int slot = small ? (packed & 0xffff) : (packed >> 16);
+        ApusGemmEnt *t13 = small ? e13s : e13l;
         a.w = tab.w1[e]; a.ws = tab.w1s[e]; a.out = g;
-        e13[e] = a;
+        t13[2 * slot] = a;
         a.w = tab.w3[e]; a.ws = tab.w3s[e]; a.out = u;
-        e13[E + e] = a;
-        ApusGemmEnt b;
-        b.w = tab.w2[e]; b.ws = tab.w2s[e]; b.out = eo;
-        b.arows = nullptr; b.orows = pair_sorted + o0; b.a0 = o0; b.o0 = 0; b.M = c; b.pad = 0;
-        e2[e] = b;
+        t13[2 * slot + 1] = a;
+        (small ? e2s : e2l)[slot] = b;
     }
-    (void)inter; (void)dim;
+    ApusGemmEnt z{};
+    if (e >= ns) { e13s[2 * e] = z; e13s[2 * e + 1] = z; e2s[e] = z; }
+    if (e >= nl) { e13l[2 * e] = z; e13l[2 * e + 1] = z; e2l[e] = z; }
+    (void)total;
 }
 
 hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
-                                 ApusExpertTable tab, float *g, float *u,
-                                 float *eo, int inter, int dim,
+                                 ApusExpertTable tab, float *g, float *u, float *eo,
                                  int32_t *pair_sorted, int32_t *tok_sorted,
-                                 ApusGemmEnt *e13, ApusGemmEnt *e2,
-                                 hipStream_t st) {
-    hipLaunchKernelGGL(apus_moe_route_kernel, dim3(1), dim3(1024), 3 * E * sizeof(int), st,
-                       idx, nj, topk, E, tab, g, u, eo, inter, dim, pair_sorted,
-                       tok_sorted, e13, e2);
+                                 ApusGemmEnt *e13s, ApusGemmEnt *e2s, ApusGemmEnt *e13l,
+                                 ApusGemmEnt *e2l, int small_max, hipStream_t st) {
+    if (E <= 0 || E > 1024) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(apus_moe_route_kernel, dim3(1), dim3(1024), 0, st, idx, nj, topk, E,
+                       tab, g, u, eo, pair_sorted, tok_sorted, e13s, e2s, e13l, e2l, small_max);
     return hipGetLastError();
 }
 

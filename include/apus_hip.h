@@ -171,8 +171,9 @@ int apus_hip_fp8_gemm_dev(const uint8_t *w, const uint8_t *ws,
  *   out[orow(m) * ldo + o] = sum_k acodes[arow(m), k] * W[o, k]   (o < O)
  * with arow(m) = arows ? arows[m] : a0 + m and orow(m) = orows ? orows[m] :
  * o0 + m; W is MXFP4 [O, K/2] + [O, K/32] (wfmt 0) or FP8 [O, K] +
- * [ceil(O/128), K/128] (wfmt 1). max_m is a hint (typical largest M; 0 =
- * unknown). round_out: BF16-round the outputs. */
+ * [ceil(O/128), K/128] (wfmt 1). max_m is an upper bound on every entry's
+ * M, or 0 when unknown (entries with M > max_m may be left uncomputed).
+ * round_out: BF16-round the outputs. */
 typedef struct {
     const uint8_t *w, *ws;
     float *out;

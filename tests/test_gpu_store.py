@@ -103,3 +103,53 @@ def test_moe_routed_dev_over_store(hip, oracle, store, rng, E, dim, inter, s, to
     assert max_rel(got, want) <= 2.0 ** -7
     host = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=777 + E)
     assert np.array_equal(got.view(np.uint32), host.view(np.uint32))
+
+
+def _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt, seed=9):
+    """Run apus_hip_moe_routed_dev over a freshly filled one-layer store and
+    the oracle over host copies of the experts that the routing uses (the
+    others share a placeholder: the dispatch reads only routed experts)."""
+    st = store(1, E, dim, inter)
+    hip._check(hip.lib().apus_hip_store_fill_random(st, seed), "fill")
+    used = sorted(set(int(e) for e in idx.ravel()))
+    host = {e: host_expert(oracle, seed, 0, e, E, dim, inter) for e in used}
+    experts = [host.get(e, host[used[0]]) for e in range(E)]
+    want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
+    L_ = hip.lib()
+    s, topk = idx.shape
+    dx, di, dw = (hip.DevBuf.from_array(a) for a in (x, idx, wgt))
+    dy = hip.DevBuf(s * dim * 4)
+    wsp = hip.DevBuf(L_.apus_hip_moe_workspace(st, s, topk))
+    hip._check(L_.apus_hip_moe_routed_dev(st, 0, dx.ptr, di.ptr, dw.ptr, s, topk, 10.0,
+                                          dy.ptr, wsp.ptr), "moe_routed_dev")
+    return dy.to_array(np.float32, (s, dim)), want
+
+
+def test_moe_routed_dev_one_token_full_shape(hip, oracle, store, rng):
+    """One token at the model's shape (256 experts, dim 4096, inter 2048):
+    the decode path with its compacted expert tables."""
+    E, dim, inter, topk = 256, 4096, 2048, 6
+    x = acts(rng, 1, dim)
+    idx, wgt = topk_routing(rng, 1, E, topk)
+    got, want = _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
+    assert max_rel(got, want) <= 2.0 ** -7
+
+
+def test_moe_routed_dev_skewed_small_batch(hip, oracle, store, rng):
+    """16 tokens over 256 experts, two of them routed by most tokens: on
+    average under one pair per expert, but experts 0 and 1 carry more than
+    8 pairs and must take the many-row schedule."""
+    E, dim, inter, s, topk = 256, 2048, 2048, 16, 6
+    x = acts(rng, s, dim)
+    idx = np.empty((s, topk), np.int32)
+    for t in range(s):
+        rest = rng.choice(np.arange(2, E), topk - 2, replace=False)
+        idx[t] = np.r_[0, 1 if t < 12 else rng.integers(2, E), rest[:topk - 2]]
+        while len(set(idx[t])) < topk:
+            idx[t, 1] = rng.integers(2, E)
+    wgt = rng.random((s, topk)).astype(np.float32)
+    wgt /= wgt.sum(1, keepdims=True)
+    counts = np.bincount(idx.ravel(), minlength=E)
+    assert counts[0] == 16 and counts[1] >= 12 and counts.mean() < 1
+    got, want = _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
+    assert max_rel(got, want) <= 2.0 ** -7
