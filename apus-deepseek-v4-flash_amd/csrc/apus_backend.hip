@@ -202,6 +202,22 @@ int gemm_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acode
     return launched(apus_launch_gemm(wfmt, &a, 1, st), "gemm") ? 0 : 1;
 }
 
+/* fp32 x -> BF16 out linear in one launch when M <= 8 and the shape has a
+ * few-row schedule (the act quant runs in the GEMM's staging); returns -1
+ * when the shape does not qualify (the caller quantises, then multiplies) */
+int linear_fused(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x, float *out,
+                 int M, int K, int O, hipStream_t st) {
+    if (M > 8 || (K != 2048 && K != 4096) || O % 128) return -1;
+    ApusGemmArgs a{};
+    a.ents = nullptr;
+    a.ent0.w = w; a.ent0.ws = ws; a.ent0.out = out;
+    a.ent0.arows = nullptr; a.ent0.orows = nullptr;
+    a.ent0.a0 = 0; a.ent0.o0 = 0; a.ent0.M = M;
+    a.O = O; a.K = K; a.ldo = O; a.round_out = 1;
+    a.asrc = APUS_A_F32; a.ax = x;
+    return launched(apus_launch_gemm_few(wfmt, &a, 1, 8, 0, st), "linear") ? 0 : 1;
+}
+
 /* host-pointer linear: stage x, quantise, GEMM, BF16 out, copy back */
 int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
                 float *out, int M, int K, int O) {
@@ -219,8 +235,12 @@ int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
     float *dout = (float *)scratch(3, (size_t)M * O * 4);
     if (!dx || !dc || !dsc || !dout) return 1;
     if (!upload(dx, x, (size_t)M * K * 4)) return 1;
-    if (!launched(apus_launch_act_quant(dx, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
-    if (gemm_dev(wfmt, d->w, d->ws, dc, dsc, dout, M, O, K, 1, g.stream)) return 1;
+    const int f = linear_fused(wfmt, d->w, d->ws, dx, dout, M, K, O, g.stream);
+    if (f > 0) return 1;
+    if (f < 0) {
+        if (!launched(apus_launch_act_quant(dx, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
+        if (gemm_dev(wfmt, d->w, d->ws, dc, dsc, dout, M, O, K, 1, g.stream)) return 1;
+    }
     if (!download(out, dout, (size_t)M * O * 4) || !finish()) return 1;
     return 0;
 }
@@ -254,6 +274,7 @@ struct MoeWs {
     ApusGemmEnt *e13s, *e2s, *e13l, *e2l;   /* few-row and many-row expert tables */
     float *gm, *um; uint8_t *hc; float *hs; float *eo;
     uint8_t **tab;
+    unsigned *tickets;   /* one per 16 output columns of w2 */
     size_t total;
 };
 
@@ -272,6 +293,7 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
     size_t o_hc = take(nj * inter), o_hs = take(nj * (inter / 128) * 4);
     size_t o_eo = take(nj * dim * 4);
     size_t o_tab = take(6 * (size_t)E * sizeof(void *));
+    size_t o_tk = take((size_t)(dim / 16) * sizeof(unsigned));
     w.total = off;
     if (base) {
         uint8_t *b = (uint8_t *)base;
@@ -282,8 +304,19 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
         w.gm = (float *)(b + o_g); w.um = (float *)(b + o_u);
         w.hc = b + o_hc; w.hs = (float *)(b + o_hs); w.eo = (float *)(b + o_eo);
         w.tab = (uint8_t **)(b + o_tab);
+        w.tickets = (unsigned *)(b + o_tk);
     }
     return w;
+}
+
+/* routed pairs up to which the dispatch runs per pair (APUS_HIP_MOE_PAIRS
+ * overrides; 0 = always sort by expert) */
+int moe_pair_max() {
+    static const int v = [] {
+        const char *e = getenv("APUS_HIP_MOE_PAIRS");
+        return e ? atoi(e) : 32;
+    }();
+    return v;
 }
 
 /* the routed-dispatch pipeline on device data; tab = 6 device arrays of E
@@ -295,12 +328,35 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
     ApusExpertTable t;
     t.w1 = tab; t.w1s = tab + E; t.w2 = tab + 2 * E; t.w2s = tab + 3 * E;
     t.w3 = tab + 4 * E; t.w3s = tab + 5 * E;
-    if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, w.xc, w.xs, st), "act_quant"))
-        return 1;
+    /* few pairs (decode): one launch entry per routed pair and matrix, no
+     * sorting pass. w1/w3 quantise x while staging, w2 computes and
+     * quantises h = swiglu(g, u) while staging and accumulates y in
+     * (t, j) order in its last workgroup per column tile: three launches */
+    if (nj <= moe_pair_max() && (dim == 2048 || dim == 4096) &&
+        (inter == 2048 || inter == 4096)) {
+        ApusGemmArgs a{};
+        a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
+        a.asrc = APUS_A_F32; a.ax = x;
+        a.pidx = idx; a.nmat = 2; a.adiv = topk; a.pE = E;
+        a.pw[0] = t.w1; a.pws[0] = t.w1s; a.pout[0] = w.gm;
+        a.pw[1] = t.w3; a.pws[1] = t.w3s; a.pout[1] = w.um;
+        a.zero = w.tickets; a.nzero = dim / 16;
+        if (!launched(apus_launch_gemm_few(APUS_W_FP4, &a, 2 * nj, 1, 0, st), "pair w1/w3"))
+            return 1;
+        ApusGemmArgs b{};
+        b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
+        b.asrc = APUS_A_SWIGLU; b.ax = w.gm; b.au = w.um; b.limit = limit;
+        b.pidx = idx; b.nmat = 1; b.adiv = 1; b.pE = E;
+        b.pw[0] = t.w2; b.pws[0] = t.w2s; b.pout[0] = w.eo;
+        b.acc_w = wgt; b.acc_y = y; b.tickets = w.tickets; b.acc_topk = topk; b.acc_s = s;
+        return launched(apus_launch_gemm_few(APUS_W_FP4, &b, nj, 1, 0, st), "pair w2") ? 0 : 1;
+    }
     /* experts with at most SMALL pairs take the few-row GEMM schedule; at
      * most min(E, nj) experts are small and at most nj / (SMALL + 1) are
      * large, so the launches cover only that many table slots */
     constexpr int SMALL = 8;
+    if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, w.xc, w.xs, st), "act_quant"))
+        return 1;
     if (!launched(apus_launch_moe_route(idx, nj, topk, E, t, w.gm, w.um, w.eo, w.pair, w.tok,
                                         w.e13s, w.e2s, w.e13l, w.e2l, SMALL, st), "moe_route"))
         return 1;
@@ -572,6 +628,8 @@ static int linear_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const float
                       int M, int K, int O, void *workspace) {
     if (!ensure_init() || !shape_ok(M, K, O)) return 1;
     if (!workspace) { set_err("linear_dev: workspace required"); return 1; }
+    const int f = linear_fused(wfmt, w, ws, x, out, M, K, O, dev_stream());
+    if (f >= 0) return f;
     uint8_t *dc = (uint8_t *)workspace;
     float *dsc = (float *)(dc + align256((size_t)M * K));
     if (!launched(apus_launch_act_quant(x, K, nullptr, M, K, dc, dsc, dev_stream()), "act_quant")) return 1;

@@ -55,6 +55,17 @@ __device__ __forceinline__ float apus_wave_max(float v) {
     return v;
 }
 
+/* h = bf16(silu(g') * u') with g' = min(g, limit), u' = clamp(u, +-limit)
+ * when limit > 0 (c/moe.h:113-126); every step rounded as written. */
+__device__ __forceinline__ float apus_swiglu_h(float g, float u, float limit) {
+    if (limit > 0.0f) {
+        u = u > limit ? limit : (u < -limit ? -limit : u);
+        g = g > limit ? limit : g;
+    }
+    const float sig = 1.0f / (1.0f + expf(-g));
+    return apus_bf16_rne((g * sig) * u);
+}
+
 /* Workgroup barrier for LDS hand-off only: waits for this wave's LDS
  * operations, not for its outstanding global loads. __syncthreads() also
  * fences global memory, i.e. waits for every load in flight (vmcnt 0), which

@@ -271,9 +271,14 @@ __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args
  * launcher checks), so the slice loop is straight-line code with no per-lane
  * bounds tests: a divergent branch or a loop back edge around the prefetch
  * ring makes the compiler drain every outstanding load (s_waitcnt vmcnt(0)),
- * which would empty the ring each step. The workgroup's four waves share one entry; its
- * activation rows (R at a time, whole K) are staged in LDS as E4M3 codes and
- * E8M0 bytes, rows beyond the entry read row 0 and are zeroed by a select.
+ * which would empty the ring each step. The workgroup's four waves share one
+ * entry; its activation rows (R at a time, whole K) are staged in LDS as
+ * E4M3 codes and E8M0 bytes, rows beyond the entry are zeroed by a select.
+ * The staged rows are either read as codes (ASRC CODES) or quantised while
+ * staging from fp32 rows (F32: the act quant of c/attn.h:393-403; SWIGLU:
+ * h = swiglu(g, u) then its act quant, c/moe.h:113-126 and :309-314), with
+ * the same per-element steps as the standalone kernels, so the codes are
+ * identical.
  */
 #define APUS_DEC_WAVES 4
 
@@ -298,19 +303,106 @@ __device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const uint8_t
     }
 }
 
-template <int WF, int R, int NS, int PD, int KS>
+/* the entry of launch row y: table, routed pair, or the single entry */
+__device__ __forceinline__ ApusGemmEnt apus_entry_of(const ApusGemmArgs &a, int y) {
+    if (a.ents) return a.ents[y];
+    if (!a.pidx) return a.ent0;
+    ApusGemmEnt ent;
+    const int p = y / a.nmat, mat = y - p * a.nmat;
+    const int e = a.pidx[p];
+    const bool ok = (unsigned)e < (unsigned)a.pE;
+    const int ee = ok ? e : 0;
+    ent.w = (mat ? a.pw[1] : a.pw[0])[ee];
+    ent.ws = (mat ? a.pws[1] : a.pws[0])[ee];
+    ent.out = mat ? a.pout[1] : a.pout[0];
+    ent.arows = nullptr; ent.orows = nullptr;
+    ent.a0 = p / a.adiv; ent.o0 = p; ent.M = ok ? 1 : 0; ent.pad = 0;
+    return ent;
+}
+
+/* Quantise rows c0 .. c0+rows-1 of the entry into LDS (codes [R][K + 16],
+ * E8M0 bytes [R][K/128]). Eight lanes own one 128-group (16 elements each);
+ * a wave covers 8 groups per pass. */
+template <int K, int R, int ASRC>
+__device__ __forceinline__ void apus_stage_quant(const ApusGemmArgs &a, const ApusGemmEnt &ent,
+                                                 int c0, int rows, uint8_t *lcodes,
+                                                 uint8_t *lsc) {
+    constexpr int NQ = K / 128, LDK = K + 16;
+    constexpr int PASSES = (R * NQ + 31) / 32;
+    const int sub = threadIdx.x & 7;
+    const int n = rows * NQ;
+#pragma unroll
+    for (int pass = 0; pass < PASSES; ++pass) {
+        /* n is a multiple of 16, so this test is uniform over each wave */
+        const int gi = pass * 32 + (threadIdx.x >> 3);
+        if (gi < n) {
+            const int row = gi / NQ, q = gi - row * NQ;
+            const int mm = c0 + row;
+            const int ar = ent.arows ? ent.arows[mm] : ent.a0 + mm;
+            const size_t off = (size_t)ar * K + q * 128 + sub * 16;
+            float v[16];
+            if constexpr (ASRC == APUS_A_F32) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 f = *reinterpret_cast<const float4 *>(a.ax + off + 4 * i);
+                    v[4 * i] = apus_bf16_rne(f.x); v[4 * i + 1] = apus_bf16_rne(f.y);
+                    v[4 * i + 2] = apus_bf16_rne(f.z); v[4 * i + 3] = apus_bf16_rne(f.w);
+                }
+            } else {
+                float4 gg[4], uu[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    gg[i] = *reinterpret_cast<const float4 *>(a.ax + off + 4 * i);
+                    uu[i] = *reinterpret_cast<const float4 *>(a.au + off + 4 * i);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[4 * i] = apus_swiglu_h(gg[i].x, uu[i].x, a.limit);
+                    v[4 * i + 1] = apus_swiglu_h(gg[i].y, uu[i].y, a.limit);
+                    v[4 * i + 2] = apus_swiglu_h(gg[i].z, uu[i].z, a.limit);
+                    v[4 * i + 3] = apus_swiglu_h(gg[i].w, uu[i].w, a.limit);
+                }
+            }
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+            m = fmaxf(m, __shfl_xor(m, 1, 64));
+            m = fmaxf(m, __shfl_xor(m, 2, 64));
+            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            const uint32_t e = apus_act_scale_exp(m);
+            const float inv = apus_inv_pow2_from_exp(e);
+            uint32_t w4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                w4[i] = apus_e4m3_code(v[4 * i] * inv) | (apus_e4m3_code(v[4 * i + 1] * inv) << 8) |
+                        (apus_e4m3_code(v[4 * i + 2] * inv) << 16) |
+                        (apus_e4m3_code(v[4 * i + 3] * inv) << 24);
+            *reinterpret_cast<uint4 *>(lcodes + row * LDK + q * 128 + sub * 16) =
+                uint4{w4[0], w4[1], w4[2], w4[3]};
+            if (sub == 0) lsc[row * NQ + q] = (uint8_t)e;
+        }
+    }
+}
+
+template <int WF, int R, int NS, int PD, int KS, int ASRC>
 __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args) {
     extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ int last_ticket;
     constexpr int K = NS * 512, NQ = NS * 4, K16 = K / 16, LDK = K + 16;
-    constexpr int STAGE = R * K16 / 256;               /* 16-byte loads per thread */
     constexpr int NSW = NS / KS;                       /* slices per wave */
-    static_assert(NS % KS == 0 && PD <= NSW, "decode shape");
-    const ApusGemmEnt ent = args.ents[blockIdx.y];
-    if (ent.M <= args.m_min || (args.m_max > 0 && ent.M > args.m_max)) return;
+    constexpr int TPW = APUS_DEC_WAVES / KS;           /* row tiles per workgroup */
+    static_assert(NS % KS == 0 && PD <= NSW && APUS_DEC_WAVES % KS == 0, "decode shape");
+    if (args.zero && blockIdx.y == 0) {
+        for (int i = blockIdx.x * 256 + threadIdx.x; i < args.nzero; i += gridDim.x * 256)
+            args.zero[i] = 0u;
+    }
+    const ApusGemmEnt ent = apus_entry_of(args, blockIdx.y);
+    const bool active = ent.M > args.m_min && !(args.m_max > 0 && ent.M > args.m_max);
+    if (!active && !args.acc_y) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    /* KS waves share a row tile and split its K range; O % (64 / KS) == 0 */
-    const int tile = blockIdx.x * (APUS_DEC_WAVES / KS) + wave / KS;
+    /* KS waves share a row tile and split its K range */
+    const int tile = blockIdx.x * TPW + wave / KS;
     const int kpart = wave % KS;
     const int o = tile * 16 + r;
     uint8_t *lcodes = lds;
@@ -321,50 +413,59 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                                            : ent.ws + (size_t)(o >> 7) * NQ;
 
     const int sbase = kpart * NSW;
-    for (int c0 = 0; c0 < ent.M; c0 += R) {
+    for (int c0 = 0; active && c0 < ent.M; c0 += R) {
         const int rows = min(R, ent.M - c0);
         apus_lds_barrier();           /* the previous chunk's LDS reads are done */
-        /* stage: row indices, then every code/scale load, then the LDS
-         * writes (no load waits on another load's result more than once) */
-        int ridx[R];
-        if (ent.arows) {
-#pragma unroll
-            for (int j = 0; j < R; ++j) ridx[j] = ent.arows[c0 + min(j, rows - 1)];
-        } else {
-#pragma unroll
-            for (int j = 0; j < R; ++j) ridx[j] = ent.a0 + c0 + min(j, rows - 1);
-        }
-        constexpr int RPJ = 256 / K16;                   /* rows per 256 loads */
-        static_assert(RPJ >= 1 && R % RPJ == 0, "staging shape");
-        uint4 v[STAGE];
-#pragma unroll
-        for (int j = 0; j < STAGE; ++j) {
-            const int rsub = threadIdx.x / K16;         /* 0..RPJ-1 */
-            const int cc = threadIdx.x - rsub * K16;
-            int ar = ridx[j * RPJ];
-#pragma unroll
-            for (int t = 1; t < RPJ; ++t) ar = rsub == t ? ridx[j * RPJ + t] : ar;
-            v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);   /* rows past the entry
-                                                                          repeat its last row */
-        }
-        const int si = threadIdx.x % (R * NQ), srr = si / NQ;
-        int sar = ridx[0];
-#pragma unroll
-        for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
-        const float scv = args.ascale[(size_t)sar * NQ + (si - srr * NQ)];
-        /* weight prefetch ring: issued after the staging loads (so waiting
-         * for those does not wait for these) and before the LDS hand-off */
         ApusBFrag<WF> ring[PD];
+        if constexpr (ASRC == APUS_A_CODES) {
+            /* stage: row indices, then every code/scale load, then the LDS
+             * writes (no load waits on another load's result more than once) */
+            constexpr int STAGE = R * K16 / 256;       /* 16-byte loads per thread */
+            constexpr int RPJ = 256 / K16;             /* rows per 256 loads */
+            static_assert(RPJ >= 1 && R % RPJ == 0, "staging shape");
+            int ridx[R];
+            if (ent.arows) {
 #pragma unroll
-        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
+                for (int j = 0; j < R; ++j) ridx[j] = ent.arows[c0 + min(j, rows - 1)];
+            } else {
 #pragma unroll
-        for (int j = 0; j < STAGE; ++j) {
-            const int rsub = threadIdx.x / K16;
-            const int cc = threadIdx.x - rsub * K16;
-            if (j * RPJ + rsub < rows)
-                *reinterpret_cast<uint4 *>(lcodes + (j * RPJ + rsub) * LDK + cc * 16) = v[j];
+                for (int j = 0; j < R; ++j) ridx[j] = ent.a0 + c0 + min(j, rows - 1);
+            }
+            uint4 v[STAGE];
+#pragma unroll
+            for (int j = 0; j < STAGE; ++j) {
+                const int rsub = threadIdx.x / K16;         /* 0..RPJ-1 */
+                const int cc = threadIdx.x - rsub * K16;
+                int ar = ridx[j * RPJ];
+#pragma unroll
+                for (int t = 1; t < RPJ; ++t) ar = rsub == t ? ridx[j * RPJ + t] : ar;
+                v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);   /* rows past the entry
+                                                                              repeat its last row */
+            }
+            const int si = threadIdx.x % (R * NQ), srr = si / NQ;
+            int sar = ridx[0];
+#pragma unroll
+            for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
+            const float scv = args.ascale[(size_t)sar * NQ + (si - srr * NQ)];
+            /* weight prefetch ring: issued after the staging loads (so waiting
+             * for those does not wait for these) and before the LDS hand-off */
+#pragma unroll
+            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
+#pragma unroll
+            for (int j = 0; j < STAGE; ++j) {
+                const int rsub = threadIdx.x / K16;
+                const int cc = threadIdx.x - rsub * K16;
+                if (j * RPJ + rsub < rows)
+                    *reinterpret_cast<uint4 *>(lcodes + (j * RPJ + rsub) * LDK + cc * 16) = v[j];
+            }
+            if (threadIdx.x < R * NQ && srr < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv);
+        } else {
+            /* the weight ring goes first: its loads are in flight while the
+             * activation rows are read and quantised */
+#pragma unroll
+            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
+            apus_stage_quant<K, R, ASRC>(args, ent, c0, rows, lcodes, lsc);
         }
-        if (threadIdx.x < R * NQ && srr < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv);
         apus_lds_barrier();
         const bool rvalid = r < rows;
         const int rr = rvalid ? r : 0;
@@ -385,7 +486,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                                             (int)a0.w & z, (int)a1.x & z, (int)a1.y & z,
                                             (int)a1.z & z, (int)a1.w & z};
                 const int sa = asrow[q];
-                if (WF == APUS_W_FP4) {
+                if constexpr (WF == APUS_W_FP4) {
                     const apus_v4u w = cur.w[st][0];
                     const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
                     const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
@@ -416,7 +517,39 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                 if (args.round_out) val = apus_bf16_rne(val);
                 const int mm = c0 + m;
                 const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
-                ent.out[(size_t)orow * args.ldo + o] = val;
+                float *dst = ent.out + (size_t)orow * args.ldo + o;
+                if (args.acc_y) /* device-coherent store: read by another workgroup */
+                    __hip_atomic_store(dst, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else
+                    *dst = val;
+            }
+        }
+    }
+    if (args.acc_y) {
+        /* The outputs went out as device-coherent stores; once every wave
+         * has seen them complete, take a ticket. The last workgroup of the
+         * column tile reads every pair's outputs with device-coherent loads
+         * (no stale copy in its own L2), so no cache-wide fence is needed. */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last_ticket = __hip_atomic_fetch_add(&args.tickets[blockIdx.x], 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT) == gridDim.y - 1;
+        __syncthreads();
+        if (last_ticket) {
+            constexpr int TW = 16 * TPW;
+            const float *eo = args.pout[0];
+            const int topk = args.acc_topk;
+            for (int i = threadIdx.x; i < args.acc_s * TW; i += 256) {
+                const int t = i / TW, oo = blockIdx.x * TW + (i - t * TW);
+                float y = 0.0f;
+                for (int j = 0; j < topk; ++j) {
+                    const int pj = t * topk + j;
+                    const float e = __hip_atomic_load(eo + (size_t)pj * args.ldo + oo, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                    y = __fadd_rn(y, __fmul_rn(args.acc_w[pj], e));
+                }
+                args.acc_y[(size_t)t * args.ldo + oo] = y;
             }
         }
     }
@@ -556,6 +689,92 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
     }
 }
 
+namespace {
+
+template <int WF, int R, int NS, int KS, int ASRC>
+void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
+    constexpr int NSW = NS / KS, PDD = WF == APUS_W_FP4 ? 3 : 2;
+    constexpr int PD = PDD < NSW ? PDD : NSW;
+    constexpr int K = NS * 512, NQ = NS * 4;
+    const size_t lds = (((size_t)R * (K + 16) + (size_t)R * NQ + 15) & ~(size_t)15) +
+                       (KS > 1 ? 256 * sizeof(float) * 4 : 0);
+    dim3 gd(d.O / (16 * APUS_DEC_WAVES / KS), n_ent), bd(256);
+    hipLaunchKernelGGL((apus_gemm_decode_kernel<WF, R, NS, PD, KS, ASRC>), gd, bd, lds, st, d);
+}
+
+template <int WF, int R, int ASRC>
+void apus_launch_dec_k(const ApusGemmArgs &d, int n_ent, int ks, hipStream_t st) {
+    if constexpr (R == 1) {
+        /* single-row chunks always split K: with one chunk per workgroup and
+         * whole-K waves the compiler hoists every slice's weight loads and
+         * runs out of registers */
+        if (d.K == 4096) {
+            if (ks == 4) apus_launch_dec<WF, R, 8, 4, ASRC>(d, n_ent, st);
+            else apus_launch_dec<WF, R, 8, 2, ASRC>(d, n_ent, st);
+        } else {
+            if (ks == 4) apus_launch_dec<WF, R, 4, 4, ASRC>(d, n_ent, st);
+            else apus_launch_dec<WF, R, 4, 2, ASRC>(d, n_ent, st);
+        }
+        return;
+    }
+    if (d.K == 4096) {
+        if (ks == 1) apus_launch_dec<WF, R, 8, 1, ASRC>(d, n_ent, st);
+        else if (ks == 2) apus_launch_dec<WF, R, 8, 2, ASRC>(d, n_ent, st);
+        else apus_launch_dec<WF, R, 8, 4, ASRC>(d, n_ent, st);
+    } else {
+        if (ks == 1) apus_launch_dec<WF, R, 4, 1, ASRC>(d, n_ent, st);
+        else if (ks == 2) apus_launch_dec<WF, R, 4, 2, ASRC>(d, n_ent, st);
+        else apus_launch_dec<WF, R, 4, 4, ASRC>(d, n_ent, st);
+    }
+}
+
+/* waves per 16-row tile: small launches split K for more weight streams;
+ * APUS_HIP_DEC_KS (1, 2, 4) overrides */
+int apus_dec_ks(size_t row_tiles) {
+    static const int forced = [] {
+        const char *e = getenv("APUS_HIP_DEC_KS");
+        const int v = e ? atoi(e) : 0;
+        return (v == 1 || v == 2 || v == 4) ? v : 0;
+    }();
+    if (forced) return forced;
+    return row_tiles < 1024 ? 4 : row_tiles < 2048 ? 2 : 1;
+}
+
+}  // namespace
+
+hipError_t apus_launch_gemm_few(int wfmt, const ApusGemmArgs *a, int n_ent, int rows,
+                                int ks, hipStream_t st) {
+    if (n_ent <= 0) return hipSuccess;
+    if ((a->K != 2048 && a->K != 4096) || a->O % 128 || (rows != 1 && rows != 8) ||
+        (a->asrc == APUS_A_CODES && rows != 8) || (a->asrc == APUS_A_SWIGLU && wfmt != APUS_W_FP4) ||
+        (a->acc_y && (!a->pidx || a->nmat != 1 || !a->tickets)) || ks < 0 || ks > 4 || ks == 3)
+        return hipErrorInvalidValue;
+    if (!ks) ks = apus_dec_ks((size_t)n_ent * (a->O / 16));
+    const bool fp4 = wfmt == APUS_W_FP4;
+    switch (a->asrc) {
+    case APUS_A_CODES:
+        if (fp4) apus_launch_dec_k<APUS_W_FP4, 8, APUS_A_CODES>(*a, n_ent, ks, st);
+        else     apus_launch_dec_k<APUS_W_FP8, 8, APUS_A_CODES>(*a, n_ent, ks, st);
+        break;
+    case APUS_A_F32:
+        if (rows == 1) {
+            if (fp4) apus_launch_dec_k<APUS_W_FP4, 1, APUS_A_F32>(*a, n_ent, ks, st);
+            else     apus_launch_dec_k<APUS_W_FP8, 1, APUS_A_F32>(*a, n_ent, ks, st);
+        } else {
+            if (fp4) apus_launch_dec_k<APUS_W_FP4, 8, APUS_A_F32>(*a, n_ent, ks, st);
+            else     apus_launch_dec_k<APUS_W_FP8, 8, APUS_A_F32>(*a, n_ent, ks, st);
+        }
+        break;
+    case APUS_A_SWIGLU:
+        if (rows == 1) apus_launch_dec_k<APUS_W_FP4, 1, APUS_A_SWIGLU>(*a, n_ent, ks, st);
+        else           apus_launch_dec_k<APUS_W_FP4, 8, APUS_A_SWIGLU>(*a, n_ent, ks, st);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
                             hipStream_t st) {
     if (n_ent <= 0) return hipSuccess;
@@ -569,31 +788,13 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
         (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
         const bool run_dec = !(a->min_m >= R);
         const bool run_pre = !(a->max_m > 0 && a->max_m <= R);
-        ApusGemmArgs d = *a;
-        d.m_min = 0;
-        d.m_max = R;
-        /* small launches split each tile's K over 2 waves for more streams */
-        const int ks = row_tiles < 2048 ? 2 : 1;
-        const size_t lds = (((size_t)R * (a->K + 16) + (size_t)R * (a->K / 128) + 15) & ~(size_t)15) +
-                           (ks > 1 ? 256 * sizeof(float) * 4 : 0);
-        dim3 gd(a->O / (16 * APUS_DEC_WAVES / ks), n_ent), bd(256);
-        if (!run_dec) {
-        } else if (wfmt == APUS_W_FP4) {
-            if (a->K == 4096) {
-                if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3, 2>), gd, bd, lds, st, d);
-                else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 8, 3, 1>), gd, bd, lds, st, d);
-            } else {
-                if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 4, 2, 2>), gd, bd, lds, st, d);
-                else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP4, R, 4, 3, 1>), gd, bd, lds, st, d);
-            }
-        } else {
-            if (a->K == 4096) {
-                if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 8, 2, 2>), gd, bd, lds, st, d);
-                else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 8, 2, 1>), gd, bd, lds, st, d);
-            } else {
-                if (ks == 2) hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2, 2>), gd, bd, lds, st, d);
-                else         hipLaunchKernelGGL((apus_gemm_decode_kernel<APUS_W_FP8, R, 4, 2, 1>), gd, bd, lds, st, d);
-            }
+        if (run_dec) {
+            ApusGemmArgs d = *a;
+            d.m_min = 0;
+            d.m_max = R;
+            d.asrc = APUS_A_CODES;
+            const hipError_t e = apus_launch_gemm_few(wfmt, &d, n_ent, R, 0, st);
+            if (e != hipSuccess) return e;
         }
         if (!run_pre) return hipGetLastError();
         ApusGemmArgs p = *a;

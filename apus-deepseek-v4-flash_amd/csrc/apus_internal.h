@@ -38,7 +38,42 @@ typedef struct {
     int min_m;               /* every entry has M = 0 or M > min_m (0 = unknown) */
     int m_min, m_max;        /* set by the launcher: a kernel computes only the
                               * entries with m_min < M <= m_max (m_max 0: no cap) */
+    /* --- few-row schedule only (apus_launch_gemm_few) --- */
+    int asrc;                /* APUS_A_*: where the activation rows come from */
+    const float *ax, *au;    /* F32: rows of x [*, K]; SWIGLU: rows of g and u [*, K] */
+    float limit;             /* SWIGLU clamp (<= 0: none) */
+    /* pair entries (ents == NULL, pidx != NULL): launch entry y is matrix
+     * y % nmat of routed pair p = y / nmat, expert e = pidx[p] (pairs with
+     * e outside [0, pE) are skipped): W = pw[mat][e], pws[mat][e], M = 1,
+     * activation row p / adiv, output row p of pout[mat] */
+    const int32_t *pidx;
+    int nmat, adiv, pE, pad2;
+    const uint8_t *const *pw[2];
+    const uint8_t *const *pws[2];
+    float *pout[2];
+    /* fused (t, j)-ordered accumulation (pair entries, nmat 1): after every
+     * workgroup of a column tile has written its outputs, the last one adds
+     * y[t, o] = sum_j acc_w[t*acc_topk + j] * out[t*acc_topk + j, o] over
+     * t < acc_s (y row stride ldo); tickets: one counter per column tile,
+     * zero at launch */
+    const float *acc_w;
+    float *acc_y;
+    unsigned *tickets;
+    int acc_topk, acc_s;
+    unsigned *zero;          /* zeroed by workgroups of launch row 0 (the */
+    int nzero;               /* tickets of a later launch) */
 } ApusGemmArgs;
+
+enum { APUS_A_CODES = 0, APUS_A_F32 = 1, APUS_A_SWIGLU = 2 };
+
+/* The few-row schedule for every entry (each entry's M is computed in
+ * chunks of up to `rows` rows; rows 1 or 8), with the activation source,
+ * pair entries and fused accumulation of ApusGemmArgs. Needs K 2048 or
+ * 4096 and O % 128 == 0; asrc CODES needs rows 8. ks: 0 = by launch size,
+ * else 1, 2 or 4 waves per 16-row tile. Returns hipErrorInvalidValue for
+ * other shapes. */
+hipError_t apus_launch_gemm_few(int wfmt, const ApusGemmArgs *a, int n_ent, int rows,
+                                int ks, hipStream_t st);
 
 /* y[m] = A x W^T for every entry; n_ent entries (1 with ents == NULL). */
 hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,

@@ -59,18 +59,7 @@ __global__ __launch_bounds__(256) void apus_swiglu_quant_kernel(
     const size_t off = (size_t)m * N + b * 128 + lane * 2;
     const float2 gv = *reinterpret_cast<const float2 *>(gm + off);
     const float2 uv = *reinterpret_cast<const float2 *>(um + off);
-    float h[2];
-    const float ga[2] = {gv.x, gv.y}, ua[2] = {uv.x, uv.y};
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        float gg = ga[i], uu = ua[i];
-        if (limit > 0.0f) {
-            uu = uu > limit ? limit : (uu < -limit ? -limit : uu);
-            gg = gg > limit ? limit : gg;
-        }
-        const float sig = 1.0f / (1.0f + expf(-gg));
-        h[i] = apus_bf16_rne((gg * sig) * uu);
-    }
+    const float h[2] = {apus_swiglu_h(gv.x, uv.x, limit), apus_swiglu_h(gv.y, uv.y, limit)};
     /* h is bf16-valued, so the act quant's own BF16 round is the identity */
     const float amax = apus_wave_max(fmaxf(fabsf(h[0]), fabsf(h[1])));
     const uint32_t e = apus_act_scale_exp(amax);

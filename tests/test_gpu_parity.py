@@ -79,7 +79,9 @@ def _check_linear(got, want, unrounded, tag):
     assert mr <= 1e-3 + 2.0 ** -8
 
 
-@pytest.mark.parametrize("M,O,K", [(1, 2048, 4096), (4, 4096, 2048)])
+# M <= 8 with K 2048/4096 runs the one-launch path (act quant inside the
+# GEMM staging); the other shapes quantise first
+@pytest.mark.parametrize("M,O,K", [(1, 2048, 4096), (4, 4096, 2048), (8, 256, 2048), (9, 2048, 4096)])
 def test_fp4_linear(hip, oracle, rng, M, O, K):
     w, ws = fp4_weights(rng, O, K)
     x = acts(rng, M, K)
@@ -89,7 +91,7 @@ def test_fp4_linear(hip, oracle, rng, M, O, K):
     _check_linear(got, want, oracle.fp4_gemm(w, ws, c, s), f"fp4 linear M={M} O={O} K={K}")
 
 
-@pytest.mark.parametrize("M,O,K", [(1, 4096, 4096), (3, 256, 512)])
+@pytest.mark.parametrize("M,O,K", [(1, 4096, 4096), (8, 4096, 2048), (3, 256, 512), (12, 1024, 4096)])
 def test_fp8_linear(hip, oracle, rng, M, O, K):
     w, ws = fp8_weights(rng, O, K)
     x = acts(rng, M, K)
@@ -108,4 +110,18 @@ def test_fp4_gemm_m_independent(hip, oracle, rng):
     full = hip.fp4_gemm(w, ws, c, s)
     for m in (0, 7, 19):
         one = hip.fp4_gemm(w, ws, c[m:m + 1].copy(), s[m:m + 1].copy())
+        assert np.array_equal(one.view(np.uint32), full[m:m + 1].view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", ["fp4", "fp8"])
+def test_linear_rows_independent(hip, rng, fmt):
+    """Up to 8 rows: each row of a batched linear is bitwise the row computed
+    alone (one-launch path)."""
+    O, K = 1024, 4096
+    w, ws = (fp4_weights if fmt == "fp4" else fp8_weights)(rng, O, K)
+    x = acts(rng, 6, K)
+    f = hip.fp4_linear if fmt == "fp4" else hip.fp8_linear
+    full = f(w, ws, x)
+    for m in (0, 5):
+        one = f(w, ws, x[m:m + 1].copy())
         assert np.array_equal(one.view(np.uint32), full[m:m + 1].view(np.uint32))

@@ -153,3 +153,57 @@ def test_moe_routed_dev_skewed_small_batch(hip, oracle, store, rng):
     assert counts[0] == 16 and counts[1] >= 12 and counts.mean() < 1
     got, want = _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
     assert max_rel(got, want) <= 2.0 ** -7
+
+
+def test_moe_routed_dev_duplicate_ids(hip, oracle, store, rng):
+    """A token that names the same expert twice gets both pairs (each pair is
+    computed and weighted on its own, as the reference's pair loop does)."""
+    E, dim, inter, topk = 64, 2048, 2048, 6
+    x = acts(rng, 2, dim)
+    idx = np.array([[3, 3, 7, 9, 3, 11], [5, 6, 7, 8, 9, 5]], np.int32)
+    wgt = rng.random((2, topk)).astype(np.float32)
+    got, want = _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
+    assert max_rel(got, want) <= 2.0 ** -7
+
+
+def test_moe_routed_dev_graph_replays(hip, oracle, store, rng):
+    """The one-token dispatch captured in a HIP graph: every replay, with
+    other eager dispatches in between, equals the eager result bit for bit
+    (the fused accumulation's counters are re-armed by each replay)."""
+    E, dim, inter, topk, seed = 64, 4096, 2048, 6, 21
+    L_ = hip.lib()
+    st = store(1, E, dim, inter)
+    hip._check(L_.apus_hip_store_fill_random(st, seed), "fill")
+    x = acts(rng, 1, dim)
+    idx, wgt = topk_routing(rng, 1, E, topk)
+    idx2, wgt2 = topk_routing(rng, 1, E, topk)
+    dx, di, dw, di2, dw2 = (hip.DevBuf.from_array(a) for a in (x, idx, wgt, idx2, wgt2))
+    dy, dy2 = hip.DevBuf(dim * 4), hip.DevBuf(dim * 4)
+    wsp = hip.DevBuf(L_.apus_hip_moe_workspace(st, 1, topk))
+
+    def run(i, w, y):
+        hip._check(L_.apus_hip_moe_routed_dev(st, 0, dx.ptr, i.ptr, w.ptr, 1, topk, 10.0,
+                                              y.ptr, wsp.ptr), "moe_routed_dev")
+
+    run(di, dw, dy)
+    eager = dy.to_array(np.float32, (1, dim)).copy()
+    run(di2, dw2, dy2)
+    eager2 = dy2.to_array(np.float32, (1, dim)).copy()
+    used = sorted(set(int(e) for e in idx.ravel()))
+    host = {e: host_expert(oracle, seed, 0, e, E, dim, inter) for e in used}
+    want = oracle.moe_routed([host.get(e, host[used[0]]) for e in range(E)], x, idx, wgt, 10.0)
+    assert max_rel(eager, want) <= 2.0 ** -7
+    hip._check(L_.apus_hip_memset(dy.ptr, 0, dim * 4), "memset")
+    hip._check(L_.apus_hip_synchronize(), "sync")
+    hip._check(L_.apus_hip_graph_begin(), "graph_begin")
+    run(di, dw, dy)
+    hip._check(L_.apus_hip_graph_end(), "graph_end")
+    for rep in range(3):
+        hip._check(L_.apus_hip_memset(dy.ptr, 0, dim * 4), "memset")
+        hip._check(L_.apus_hip_graph_replay(1), "replay")
+        hip._check(L_.apus_hip_synchronize(), "sync")
+        got = dy.to_array(np.float32, (1, dim))
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), rep
+        run(di2, dw2, dy2)
+        got2 = dy2.to_array(np.float32, (1, dim))
+        assert np.array_equal(got2.view(np.uint32), eager2.view(np.uint32)), rep
