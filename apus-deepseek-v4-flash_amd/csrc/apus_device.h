@@ -36,8 +36,42 @@ __device__ __forceinline__ apus_v4f apus_mfma_scaled(apus_v8i a, apus_v8i b,
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, AF, BF, SA, sa, SB, sb);
 }
 
+/* Loads through global-address-space pointers. Pointers read from memory
+ * (entry tables) are generic, and a generic load is a flat load, which the
+ * hardware counts against both the vector-memory and the LDS counters: every
+ * LDS wait would then also wait for the weight prefetch ring. */
+#define APUS_GLOBAL __attribute__((address_space(1)))
+
+template <typename T>
+__device__ __forceinline__ T apus_gld(const void *p) {
+    /* raw chunks of the object's size, then a bit cast (class types cannot
+     * be copy-constructed from an address-space-qualified reference) */
+    if constexpr (sizeof(T) == 16) {
+        typedef unsigned v4 __attribute__((ext_vector_type(4)));
+        return __builtin_bit_cast(T, *(const APUS_GLOBAL v4 *)p);
+    } else if constexpr (sizeof(T) == 8) {
+        return __builtin_bit_cast(T, *(const APUS_GLOBAL unsigned long long *)p);
+    } else if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, *(const APUS_GLOBAL unsigned *)p);
+    } else if constexpr (sizeof(T) == 1) {
+        return __builtin_bit_cast(T, *(const APUS_GLOBAL unsigned char *)p);
+    } else {
+        static_assert(sizeof(T) % 8 == 0, "apus_gld size");
+        struct Raw { unsigned long long d[sizeof(T) / 8]; } r;
+#pragma unroll
+        for (unsigned i = 0; i < sizeof(T) / 8; ++i)
+            r.d[i] = ((const APUS_GLOBAL unsigned long long *)p)[i];
+        return __builtin_bit_cast(T, r);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void apus_gst(void *p, T v) {
+    *(APUS_GLOBAL T *)p = v;
+}
+
 __device__ __forceinline__ uint4 apus_ld16(const uint8_t *p) {
-    return *reinterpret_cast<const uint4 *>(p);
+    return apus_gld<uint4>(p);
 }
 
 typedef unsigned apus_v4u __attribute__((ext_vector_type(4)));
@@ -46,7 +80,7 @@ typedef unsigned apus_v4u __attribute__((ext_vector_type(4)));
  * non-temporal hint, so weight slabs do not evict the activations that
  * every workgroup re-reads */
 __device__ __forceinline__ apus_v4u apus_ld16_stream(const uint8_t *p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const apus_v4u *>(p));
+    return __builtin_nontemporal_load((const APUS_GLOBAL apus_v4u *)p);
 }
 
 __device__ __forceinline__ float apus_wave_max(float v) {

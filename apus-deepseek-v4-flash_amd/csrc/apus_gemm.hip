@@ -45,7 +45,7 @@
 template <int WF, bool GROUPED>
 __global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
     __shared__ float red[8][16][17];
-    const ApusGemmEnt ent = GROUPED ? args.ents[blockIdx.y] : args.ent0;
+    const ApusGemmEnt ent = GROUPED ? apus_gld<ApusGemmEnt>(args.ents + blockIdx.y) : args.ent0;
     if (ent.M <= 0) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nw = blockDim.x >> 6;
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
         apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
         const int m = t0 + r;
         const bool mvalid = m < ent.M;
-        const int arow = mvalid ? (ent.arows ? ent.arows[m] : ent.a0 + m) : 0;
+        const int arow = mvalid ? (ent.arows ? apus_gld<int>(ent.arows + (m)) : ent.a0 + m) : 0;
         for (int s = wave; s < nslice; s += nw) {
             apus_v8i bw[4], aw[4];
             int sbv[4], sav[4];
@@ -68,11 +68,11 @@ __global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
             apus_v4u sw4 = {0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu, 0x7f7f7f7fu};
             if (WF == APUS_W_FP4 && ovalid) {
                 if ((s + 1) * 4 <= nq) {
-                    sw4 = *reinterpret_cast<const apus_v4u *>(ent.ws + (size_t)o * (K >> 5) + s * 16);
+                    sw4 = apus_gld<apus_v4u>(ent.ws + (size_t)o * (K >> 5) + s * 16);
                 } else {
                     for (int st = 0; st < 4; ++st)
                         if (s * 4 + st < nq)
-                            sw4[st] = *reinterpret_cast<const unsigned *>(ent.ws + (size_t)o * (K >> 5) + (s * 4 + st) * 4);
+                            sw4[st] = apus_gld<unsigned>(ent.ws + (size_t)o * (K >> 5) + (s * 4 + st) * 4);
                 }
             }
 #pragma unroll
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
                         apus_v4u w0 = apus_ld16_stream(p), w1 = apus_ld16_stream(p + 64);
                         bw[st] = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
                                           (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
-                        sbv[st] = ent.ws[(size_t)(o >> 7) * nq + q];
+                        sbv[st] = apus_gld<uint8_t>(ent.ws + ((size_t)(o >> 7) * nq + q));
                     } else {
                         bw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
                         sbv[st] = 0x7f;
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
                     uint4 a0 = apus_ld16(p), a1 = apus_ld16(p + 64);
                     aw[st] = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
                                       (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-                    sav[st] = (int)apus_e8m0_of(args.ascale[(size_t)arow * nq + q]);
+                    sav[st] = (int)apus_e8m0_of(apus_gld<float>(args.ascale + ((size_t)arow * nq + q)));
                 } else {
                     aw[st] = apus_v8i{0, 0, 0, 0, 0, 0, 0, 0};
                     sav[st] = 0x7f;
@@ -131,8 +131,8 @@ __global__ __launch_bounds__(512) void apus_gemm_kernel(ApusGemmArgs args) {
                 float v = red[0][i][j];
                 for (int w = 1; w < nw; ++w) v += red[w][i][j];
                 if (args.round_out) v = apus_bf16_rne(v);
-                const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
-                ent.out[(size_t)orow * args.ldo + oo] = v;
+                const int orow = ent.orows ? apus_gld<int>(ent.orows + (mm)) : ent.o0 + mm;
+                apus_gst<float>(ent.out + ((size_t)orow * args.ldo + oo), v);
             }
         }
         __syncthreads();
@@ -174,24 +174,24 @@ __device__ __forceinline__ void apus_load_b(ApusBFrag<WF> &f, const ApusGemmEnt 
     }
     if (WF == APUS_W_FP4) {
         if (ovalid && full) {
-            f.s = *reinterpret_cast<const apus_v4u *>(ent.ws + (size_t)o * (K >> 5) + s * 16);
+            f.s = apus_gld<apus_v4u>(ent.ws + (size_t)o * (K >> 5) + s * 16);
         } else {
 #pragma unroll
             for (int st = 0; st < 4; ++st)
                 f.s[st] = (ovalid && s * 4 + st < nq)
-                    ? *reinterpret_cast<const unsigned *>(ent.ws + (size_t)o * (K >> 5) + (s * 4 + st) * 4)
+                    ? apus_gld<unsigned>(ent.ws + (size_t)o * (K >> 5) + (s * 4 + st) * 4)
                     : 0x7f7f7f7fu;
         }
     } else {
 #pragma unroll
         for (int st = 0; st < 4; ++st)
-            f.s[st] = (ovalid && s * 4 + st < nq) ? ent.ws[(size_t)(o >> 7) * nq + s * 4 + st] : 0x7fu;
+            f.s[st] = (ovalid && s * 4 + st < nq) ? apus_gld<uint8_t>(ent.ws + ((size_t)(o >> 7) * nq + s * 4 + st)) : 0x7fu;
     }
 }
 
 template <int WF, int MT>
 __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args) {
-    const ApusGemmEnt ent = args.ents[blockIdx.y];
+    const ApusGemmEnt ent = apus_gld<ApusGemmEnt>(args.ents + blockIdx.y);
     if (ent.M <= 0) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int O = args.O, K = args.K;
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args
         for (int t = 0; t < MT; ++t) {
             acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
             const int m = c0 + t * 16 + r;
-            arow[t] = m < ent.M ? (ent.arows ? ent.arows[m] : ent.a0 + m) : -1;
+            arow[t] = m < ent.M ? (ent.arows ? apus_gld<int>(ent.arows + (m)) : ent.a0 + m) : -1;
         }
         ApusBFrag<WF> cur, nxt;
         apus_load_b<WF>(cur, ent, o, ovalid, 0, nq, K, g);
@@ -231,7 +231,7 @@ __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args
                         const uint4 a0 = apus_ld16(p), a1 = apus_ld16(p + 64);
                         a = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
                                      (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-                        sa = (int)apus_e8m0_of(args.ascale[(size_t)ar * nq + q]);
+                        sa = (int)apus_e8m0_of(apus_gld<float>(args.ascale + ((size_t)ar * nq + q)));
                     }
                     if (WF == APUS_W_FP4) {
                         const apus_v4u w = cur.w[st][0];
@@ -258,8 +258,8 @@ __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args
                 if (mm < ent.M && ovalid) {
                     float v = acc[t][q];
                     if (args.round_out) v = apus_bf16_rne(v);
-                    const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
-                    ent.out[(size_t)orow * args.ldo + o] = v;
+                    const int orow = ent.orows ? apus_gld<int>(ent.orows + (mm)) : ent.o0 + mm;
+                    apus_gst<float>(ent.out + ((size_t)orow * args.ldo + o), v);
                 }
             }
         }
@@ -296,92 +296,102 @@ __device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const uint8_t
         }
     }
     if (WF == APUS_W_FP4) {
-        f.s = *reinterpret_cast<const apus_v4u *>(srow + s * 16);
+        f.s = apus_gld<apus_v4u>(srow + s * 16);
     } else {
-        const unsigned b4 = *reinterpret_cast<const unsigned *>(srow + s * 4);
+        const unsigned b4 = apus_gld<unsigned>(srow + s * 4);
         f.s = apus_v4u{b4 & 0xffu, (b4 >> 8) & 0xffu, (b4 >> 16) & 0xffu, b4 >> 24};
     }
 }
 
 /* the entry of launch row y: table, routed pair, or the single entry */
 __device__ __forceinline__ ApusGemmEnt apus_entry_of(const ApusGemmArgs &a, int y) {
-    if (a.ents) return a.ents[y];
+    if (a.ents) return apus_gld<ApusGemmEnt>(a.ents + y);
     if (!a.pidx) return a.ent0;
     ApusGemmEnt ent;
     const int p = y / a.nmat, mat = y - p * a.nmat;
-    const int e = a.pidx[p];
+    const int e = apus_gld<int>(a.pidx + p);
     const bool ok = (unsigned)e < (unsigned)a.pE;
     const int ee = ok ? e : 0;
-    ent.w = (mat ? a.pw[1] : a.pw[0])[ee];
-    ent.ws = (mat ? a.pws[1] : a.pws[0])[ee];
+    ent.w = apus_gld<const uint8_t *>((mat ? a.pw[1] : a.pw[0]) + ee);
+    ent.ws = apus_gld<const uint8_t *>((mat ? a.pws[1] : a.pws[0]) + ee);
     ent.out = mat ? a.pout[1] : a.pout[0];
     ent.arows = nullptr; ent.orows = nullptr;
     ent.a0 = p / a.adiv; ent.o0 = p; ent.M = ok ? 1 : 0; ent.pad = 0;
     return ent;
 }
 
-/* Quantise rows c0 .. c0+rows-1 of the entry into LDS (codes [R][K + 16],
- * E8M0 bytes [R][K/128]). Eight lanes own one 128-group (16 elements each);
- * a wave covers 8 groups per pass. */
-template <int K, int R, int ASRC>
-__device__ __forceinline__ void apus_stage_quant(const ApusGemmArgs &a, const ApusGemmEnt &ent,
-                                                 int c0, int rows, uint8_t *lcodes,
-                                                 uint8_t *lsc) {
-    constexpr int NQ = K / 128, LDK = K + 16;
-    constexpr int PASSES = (R * NQ + 31) / 32;
+/* Quantising staging of activation rows into LDS (codes [R][K + 16], E8M0
+ * bytes [R][K/128]). Eight lanes own one 128-group (16 elements each); a
+ * wave covers 8 groups per pass, a pass 32 groups. The loads of a pass and
+ * its quantisation are separate steps so that the first pass's loads can be
+ * issued before the weight ring (and before the entry lookup when the row
+ * is known without it). */
+template <int ASRC>
+struct ApusStageRaw {
+    float4 g[4], u[4];
+    int row, q;
+    bool ok;
+};
+
+template <int K, int ASRC>
+__device__ __forceinline__ void apus_stage_load(const ApusGemmArgs &a, const int *arows, int a0,
+                                                int c0, int rows, int pass, ApusStageRaw<ASRC> &r) {
+    constexpr int NQ = K / 128;
     const int sub = threadIdx.x & 7;
-    const int n = rows * NQ;
+    /* rows * NQ is a multiple of 16, so this test is uniform over each wave */
+    const int gi = pass * 32 + (threadIdx.x >> 3);
+    r.ok = gi < rows * NQ;
+    r.row = gi / NQ;
+    r.q = gi - r.row * NQ;
+    if (r.ok) {
+        const int mm = c0 + r.row;
+        const int ar = arows ? apus_gld<int>(arows + mm) : a0 + mm;
+        const size_t off = (size_t)ar * K + r.q * 128 + sub * 16;
 #pragma unroll
-    for (int pass = 0; pass < PASSES; ++pass) {
-        /* n is a multiple of 16, so this test is uniform over each wave */
-        const int gi = pass * 32 + (threadIdx.x >> 3);
-        if (gi < n) {
-            const int row = gi / NQ, q = gi - row * NQ;
-            const int mm = c0 + row;
-            const int ar = ent.arows ? ent.arows[mm] : ent.a0 + mm;
-            const size_t off = (size_t)ar * K + q * 128 + sub * 16;
-            float v[16];
-            if constexpr (ASRC == APUS_A_F32) {
+        for (int i = 0; i < 4; ++i) r.g[i] = apus_gld<float4>(a.ax + off + 4 * i);
+        if constexpr (ASRC == APUS_A_SWIGLU) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float4 f = *reinterpret_cast<const float4 *>(a.ax + off + 4 * i);
-                    v[4 * i] = apus_bf16_rne(f.x); v[4 * i + 1] = apus_bf16_rne(f.y);
-                    v[4 * i + 2] = apus_bf16_rne(f.z); v[4 * i + 3] = apus_bf16_rne(f.w);
-                }
-            } else {
-                float4 gg[4], uu[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    gg[i] = *reinterpret_cast<const float4 *>(a.ax + off + 4 * i);
-                    uu[i] = *reinterpret_cast<const float4 *>(a.au + off + 4 * i);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[4 * i] = apus_swiglu_h(gg[i].x, uu[i].x, a.limit);
-                    v[4 * i + 1] = apus_swiglu_h(gg[i].y, uu[i].y, a.limit);
-                    v[4 * i + 2] = apus_swiglu_h(gg[i].z, uu[i].z, a.limit);
-                    v[4 * i + 3] = apus_swiglu_h(gg[i].w, uu[i].w, a.limit);
-                }
-            }
-            float m = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
-            m = fmaxf(m, __shfl_xor(m, 1, 64));
-            m = fmaxf(m, __shfl_xor(m, 2, 64));
-            m = fmaxf(m, __shfl_xor(m, 4, 64));
-            const uint32_t e = apus_act_scale_exp(m);
-            const float inv = apus_inv_pow2_from_exp(e);
-            uint32_t w4[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                w4[i] = apus_e4m3_code(v[4 * i] * inv) | (apus_e4m3_code(v[4 * i + 1] * inv) << 8) |
-                        (apus_e4m3_code(v[4 * i + 2] * inv) << 16) |
-                        (apus_e4m3_code(v[4 * i + 3] * inv) << 24);
-            *reinterpret_cast<uint4 *>(lcodes + row * LDK + q * 128 + sub * 16) =
-                uint4{w4[0], w4[1], w4[2], w4[3]};
-            if (sub == 0) lsc[row * NQ + q] = (uint8_t)e;
+            for (int i = 0; i < 4; ++i) r.u[i] = apus_gld<float4>(a.au + off + 4 * i);
         }
     }
+}
+
+template <int K, int ASRC>
+__device__ __forceinline__ void apus_stage_quant(const ApusGemmArgs &a, const ApusStageRaw<ASRC> &r,
+                                                 uint8_t *lcodes, uint8_t *lsc) {
+    constexpr int NQ = K / 128, LDK = K + 16;
+    const int sub = threadIdx.x & 7;
+    if (!r.ok) return;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        if constexpr (ASRC == APUS_A_F32) {
+            v[4 * i] = apus_bf16_rne(r.g[i].x); v[4 * i + 1] = apus_bf16_rne(r.g[i].y);
+            v[4 * i + 2] = apus_bf16_rne(r.g[i].z); v[4 * i + 3] = apus_bf16_rne(r.g[i].w);
+        } else {
+            v[4 * i] = apus_swiglu_h(r.g[i].x, r.u[i].x, a.limit);
+            v[4 * i + 1] = apus_swiglu_h(r.g[i].y, r.u[i].y, a.limit);
+            v[4 * i + 2] = apus_swiglu_h(r.g[i].z, r.u[i].z, a.limit);
+            v[4 * i + 3] = apus_swiglu_h(r.g[i].w, r.u[i].w, a.limit);
+        }
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    const uint32_t e = apus_act_scale_exp(m);
+    const float inv = apus_inv_pow2_from_exp(e);
+    uint32_t w4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w4[i] = apus_e4m3_code(v[4 * i] * inv) | (apus_e4m3_code(v[4 * i + 1] * inv) << 8) |
+                (apus_e4m3_code(v[4 * i + 2] * inv) << 16) |
+                (apus_e4m3_code(v[4 * i + 3] * inv) << 24);
+    *reinterpret_cast<uint4 *>(lcodes + r.row * LDK + r.q * 128 + sub * 16) =
+        uint4{w4[0], w4[1], w4[2], w4[3]};
+    if (sub == 0) lsc[r.row * NQ + r.q] = (uint8_t)e;
 }
 
 template <int WF, int R, int NS, int PD, int KS, int ASRC>
@@ -395,6 +405,20 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
     if (args.zero && blockIdx.y == 0) {
         for (int i = blockIdx.x * 256 + threadIdx.x; i < args.nzero; i += gridDim.x * 256)
             args.zero[i] = 0u;
+    }
+    /* quantising staging: when the first chunk's activation rows are known
+     * without the entry (routed pair, single entry), their loads go out
+     * before the entry lookup */
+    ApusStageRaw<ASRC> raw0;
+    bool pre = false;
+    if constexpr (ASRC != APUS_A_CODES) {
+        if (!args.ents && args.pidx) {
+            apus_stage_load<K, ASRC>(args, nullptr, (blockIdx.y / args.nmat) / args.adiv, 0, 1, 0, raw0);
+            pre = true;
+        } else if (!args.ents) {
+            apus_stage_load<K, ASRC>(args, args.ent0.arows, args.ent0.a0, 0, min(R, args.ent0.M), 0, raw0);
+            pre = true;
+        }
     }
     const ApusGemmEnt ent = apus_entry_of(args, blockIdx.y);
     const bool active = ent.M > args.m_min && !(args.m_max > 0 && ent.M > args.m_max);
@@ -426,7 +450,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
             int ridx[R];
             if (ent.arows) {
 #pragma unroll
-                for (int j = 0; j < R; ++j) ridx[j] = ent.arows[c0 + min(j, rows - 1)];
+                for (int j = 0; j < R; ++j) ridx[j] = apus_gld<int>(ent.arows + (c0 + min(j, rows - 1)));
             } else {
 #pragma unroll
                 for (int j = 0; j < R; ++j) ridx[j] = ent.a0 + c0 + min(j, rows - 1);
@@ -446,7 +470,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
             int sar = ridx[0];
 #pragma unroll
             for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
-            const float scv = args.ascale[(size_t)sar * NQ + (si - srr * NQ)];
+            const float scv = apus_gld<float>(args.ascale + ((size_t)sar * NQ + (si - srr * NQ)));
             /* weight prefetch ring: issued after the staging loads (so waiting
              * for those does not wait for these) and before the LDS hand-off */
 #pragma unroll
@@ -460,11 +484,22 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
             }
             if (threadIdx.x < R * NQ && srr < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv);
         } else {
-            /* the weight ring goes first: its loads are in flight while the
-             * activation rows are read and quantised */
+            /* first pass: loads (unless issued before the entry lookup), the
+             * weight ring, then the quantisation; later passes load and
+             * quantise */
+            ApusStageRaw<ASRC> r0;
+            if (pre && c0 == 0) r0 = raw0;
+            else apus_stage_load<K, ASRC>(args, ent.arows, ent.a0, c0, rows, 0, r0);
 #pragma unroll
             for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
-            apus_stage_quant<K, R, ASRC>(args, ent, c0, rows, lcodes, lsc);
+            apus_stage_quant<K, ASRC>(args, r0, lcodes, lsc);
+            constexpr int PASSES = (R * NQ + 31) / 32;
+#pragma unroll
+            for (int pass = 1; pass < PASSES; ++pass) {
+                ApusStageRaw<ASRC> rp;
+                apus_stage_load<K, ASRC>(args, ent.arows, ent.a0, c0, rows, pass, rp);
+                apus_stage_quant<K, ASRC>(args, rp, lcodes, lsc);
+            }
         }
         apus_lds_barrier();
         const bool rvalid = r < rows;
@@ -516,12 +551,12 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                 float val = acc[q];
                 if (args.round_out) val = apus_bf16_rne(val);
                 const int mm = c0 + m;
-                const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
+                const int orow = ent.orows ? apus_gld<int>(ent.orows + (mm)) : ent.o0 + mm;
                 float *dst = ent.out + (size_t)orow * args.ldo + o;
                 if (args.acc_y) /* device-coherent store: read by another workgroup */
                     __hip_atomic_store(dst, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 else
-                    *dst = val;
+                    apus_gst<float>(dst, val);
             }
         }
     }
@@ -576,7 +611,7 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
     constexpr int CHUNKS = ROWS * 32 / 512;       /* 16-byte loads per thread per slice */
     __shared__ __align__(16) uint8_t abuf[2][ROWS * PITCH];
     __shared__ uint8_t sbuf[2][ROWS * 4];
-    const ApusGemmEnt ent = args.ents[blockIdx.y];
+    const ApusGemmEnt ent = apus_gld<ApusGemmEnt>(args.ents + blockIdx.y);
     if (ent.M <= args.m_min || (args.m_max > 0 && ent.M > args.m_max)) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -594,11 +629,11 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
         for (int j = 0; j < CHUNKS; ++j) {
             const int i = threadIdx.x + j * 512;
             const int rr = min(i >> 5, rows - 1);
-            const int ar = ent.arows ? ent.arows[c0 + rr] : ent.a0 + c0 + rr;
+            const int ar = ent.arows ? apus_gld<int>(ent.arows + (c0 + rr)) : ent.a0 + c0 + rr;
             abase[j] = args.acodes + (size_t)ar * K + (i & 31) * 16;
         }
         const int srr = min((int)((threadIdx.x % (ROWS * 4)) >> 2), rows - 1);
-        const int sar = ent.arows ? ent.arows[c0 + srr] : ent.a0 + c0 + srr;
+        const int sar = ent.arows ? apus_gld<int>(ent.arows + (c0 + srr)) : ent.a0 + c0 + srr;
         const float *sbase = args.ascale + (size_t)sar * NQ + (threadIdx.x & 3);
         uint4 v[CHUNKS];
         float sv;
@@ -680,8 +715,8 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
                         float val = acc[t][q];
                         if (args.round_out) val = apus_bf16_rne(val);
                         const int mm = c0 + m;
-                        const int orow = ent.orows ? ent.orows[mm] : ent.o0 + mm;
-                        ent.out[(size_t)orow * args.ldo + o] = val;
+                        const int orow = ent.orows ? apus_gld<int>(ent.orows + (mm)) : ent.o0 + mm;
+                        apus_gst<float>(ent.out + ((size_t)orow * args.ldo + o), val);
                     }
                 }
             }
@@ -715,9 +750,7 @@ void apus_launch_dec_k(const ApusGemmArgs &d, int n_ent, int ks, hipStream_t st)
             if (ks == 4) apus_launch_dec<WF, R, 4, 4, ASRC>(d, n_ent, st);
             else apus_launch_dec<WF, R, 4, 2, ASRC>(d, n_ent, st);
         }
-        return;
-    }
-    if (d.K == 4096) {
+    } else if (d.K == 4096) {
         if (ks == 1) apus_launch_dec<WF, R, 8, 1, ASRC>(d, n_ent, st);
         else if (ks == 2) apus_launch_dec<WF, R, 8, 2, ASRC>(d, n_ent, st);
         else apus_launch_dec<WF, R, 8, 4, ASRC>(d, n_ent, st);
