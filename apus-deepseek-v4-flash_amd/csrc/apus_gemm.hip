@@ -463,8 +463,10 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                 int ar = ridx[j * RPJ];
 #pragma unroll
                 for (int t = 1; t < RPJ; ++t) ar = rsub == t ? ridx[j * RPJ + t] : ar;
-                v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);   /* rows past the entry
-                                                                              repeat its last row */
+                /* only the entry's rows are read; the test is uniform over
+                 * each wave (a row is K16 >= 128 consecutive threads) */
+                if (j * RPJ + rsub < rows) v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);
+                else v[j] = uint4{0u, 0u, 0u, 0u};
             }
             const int si = threadIdx.x % (R * NQ), srr = si / NQ;
             int sar = ridx[0];
