@@ -726,6 +726,150 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
     }
 }
 
+/*
+ * Tile schedule (dense GEMMs with more than 8 rows, e.g. a 512-token FP8
+ * projection). A workgroup computes 64 rows (tokens) x 128 columns (weight
+ * rows) over the whole K, one accumulation chain per output in 128-group
+ * order. Four waves in a 2 x 2 arrangement own 32 tokens x 64 weight rows
+ * each (2 x 4 MFMA tiles, 8 instructions per 128-group). The 64 activation
+ * rows of each group are staged in LDS (double buffered, loaded DA groups
+ * ahead through a register ring); each wave streams its weight fragments straight into a register
+ * ring PD groups ahead. The activation loads of a step are issued before
+ * that step's weight loads, so waiting for them never waits for the ring.
+ * K = 128 * NQ is a template constant (the group loop is straight-line).
+ */
+template <int WF>
+struct ApusTileB {
+    apus_v4u w[4][WF == APUS_W_FP4 ? 1 : 2];
+    unsigned s[4];           /* FP4: the row's 4 group-scale bytes of this step */
+};
+
+template <int WF, int NQ, int PD, int DA>
+__global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) {
+    constexpr int BM = 64, BN = 128, LDA = 128 + 16;
+    constexpr int K = NQ * 128;
+    constexpr size_t RB = WF == APUS_W_FP4 ? K / 2 : K;     /* weight row bytes */
+    __shared__ __align__(16) uint8_t la[2][BM * LDA];
+    __shared__ uint8_t lsa[2][BM];
+    const ApusGemmEnt ent = args.ents ? apus_gld<ApusGemmEnt>(args.ents + blockIdx.z) : args.ent0;
+    const int m0 = blockIdx.y * BM;
+    if (m0 >= ent.M) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nbase = blockIdx.x * BN + wn * 64;
+    /* activation staging: thread t loads bytes [(t%4)*32, +32) of token row t/4 */
+    const int srow = threadIdx.x >> 2, spart = threadIdx.x & 3;
+    const int sm = m0 + srow;
+    const int sar = sm < ent.M ? (ent.arows ? apus_gld<int>(ent.arows + sm) : ent.a0 + sm)
+                               : (ent.arows ? apus_gld<int>(ent.arows) : ent.a0);
+    const uint8_t *sap = args.acodes + (size_t)sar * K + spart * 32;
+    const float *ssp = args.ascale + (size_t)sar * NQ;
+    const uint8_t *wrow = ent.w + (size_t)(nbase + r) * RB;
+    const uint8_t *wsrow = ent.ws + (WF == APUS_W_FP4 ? (size_t)(nbase + r) * (K / 32)
+                                                      : (size_t)blockIdx.x * NQ);
+    /* FP8: the 128 x 128 tile scales of this column block, all groups */
+    unsigned sb8[WF == APUS_W_FP8 ? NQ / 4 : 1];
+    if constexpr (WF == APUS_W_FP8) {
+#pragma unroll
+        for (int i = 0; i < NQ / 4; ++i) sb8[i] = apus_gld<unsigned>(wsrow + 4 * i);
+    }
+    auto load_b = [&](ApusTileB<WF> &f, int q) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint8_t *p = wrow + (size_t)i * 16 * RB;
+            if constexpr (WF == APUS_W_FP4) {
+                f.w[i][0] = apus_gld<apus_v4u>(p + q * 64 + g * 16);
+                f.s[i] = apus_gld<unsigned>(wsrow + (size_t)i * 16 * (K / 32) + 4 * q);
+            } else {
+                f.w[i][0] = apus_gld<apus_v4u>(p + q * 128 + g * 16);
+                f.w[i][1] = apus_gld<apus_v4u>(p + q * 128 + 64 + g * 16);
+            }
+        }
+    };
+    uint4 areg[DA][2];        /* activation ring: DA groups ahead */
+    float sreg[DA];
+    auto load_a = [&](int q, int slot) {
+        areg[slot][0] = apus_ld16(sap + q * 128);
+        areg[slot][1] = apus_ld16(sap + q * 128 + 16);
+        sreg[slot] = apus_gld<float>(ssp + q);    /* unconditional: no branch around a load */
+    };
+    auto store_a = [&](int q, int slot) {
+        uint8_t *d = la[q & 1] + srow * LDA + spart * 32;
+        *reinterpret_cast<uint4 *>(d) = areg[slot][0];
+        *reinterpret_cast<uint4 *>(d + 16) = areg[slot][1];
+        if (spart == 0) lsa[q & 1][srow] = (uint8_t)apus_e8m0_of(sreg[slot]);
+    };
+
+    ApusTileB<WF> ring[PD];
+#pragma unroll
+    for (int u = 0; u < DA; ++u)
+        if (u < NQ) load_a(u, u);
+#pragma unroll
+    for (int u = 0; u < PD; ++u) load_b(ring[u], u);
+    store_a(0, 0);
+    apus_lds_barrier();
+
+    apus_v4f acc[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        /* activation rows of step q + DA (slot of step q, written last step) */
+        if (q + DA < NQ) load_a(q + DA, q % DA);
+        ApusTileB<WF> &cur = ring[q % PD];
+        const uint8_t *ab = la[q & 1];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int row = wm * 32 + t * 16 + r;
+            const uint4 a0 = *reinterpret_cast<const uint4 *>(ab + row * LDA + g * 16);
+            const uint4 a1 = *reinterpret_cast<const uint4 *>(ab + row * LDA + 64 + g * 16);
+            const apus_v8i a = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                        (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+            const int sa = lsa[q & 1][row];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (WF == APUS_W_FP4) {
+                    const apus_v4u w = cur.w[i][0];
+                    const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                    const int sb = (int)((cur.s[i] >> (8 * g)) & 0xffu);
+                    acc[t][i] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[t][i], sa, sb);
+                } else {
+                    const apus_v4u w0 = cur.w[i][0], w1 = cur.w[i][1];
+                    const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                                (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                    const int sb = (int)((sb8[q >> 2] >> (8 * (q & 3))) & 0xffu);
+                    acc[t][i] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc[t][i], sa, sb);
+                }
+            }
+        }
+        if (q + PD < NQ) load_b(cur, q + PD);
+        if (q + 1 < NQ) store_a(q + 1, (q + 1) % DA);
+        apus_lds_barrier();
+    }
+    /* lane holds D[4g + j][r]: token m0 + 32 wm + 16 t + 4g + j, weight row nbase + 16 i + r */
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int mm = m0 + wm * 32 + t * 16 + 4 * g + j;
+            if (mm < ent.M) {
+                const int orow = ent.orows ? apus_gld<int>(ent.orows + mm) : ent.o0 + mm;
+                float *dst = ent.out + (size_t)orow * args.ldo + nbase + r;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float v = acc[t][i][j];
+                    if (args.round_out) v = apus_bf16_rne(v);
+                    apus_gst<float>(dst + i * 16, v);
+                }
+            }
+        }
+    }
+}
+
 namespace {
 
 template <int WF, int R, int NS, int KS, int ASRC>
@@ -842,6 +986,18 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
         } else {
             if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 8, 2, 2>), gp, bp, 0, st, p);
             else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 4, 2, 2>), gp, bp, 0, st, p);
+        }
+        return hipGetLastError();
+    }
+    /* dense GEMMs with more than 8 rows: the tile schedule */
+    if (!grouped && a->ent0.M > R && (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
+        dim3 gt(a->O / 128, (a->ent0.M + 63) / 64, 1), bt(256);
+        if (wfmt == APUS_W_FP4) {
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_tile_kernel<APUS_W_FP4, 32, 8, 6>), gt, bt, 0, st, *a);
+            else              hipLaunchKernelGGL((apus_gemm_tile_kernel<APUS_W_FP4, 16, 8, 6>), gt, bt, 0, st, *a);
+        } else {
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_tile_kernel<APUS_W_FP8, 32, 6, 6>), gt, bt, 0, st, *a);
+            else              hipLaunchKernelGGL((apus_gemm_tile_kernel<APUS_W_FP8, 16, 6, 6>), gt, bt, 0, st, *a);
         }
         return hipGetLastError();
     }

@@ -316,7 +316,9 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
                                                     dwgt.ptr + off, 1, topk, 10.0,
                                                     y.ptr + l * dim * 4, wsp.ptr), "moe")
 
+        d0 = L_.apus_hip_dispatches()
         step(0)
+        launches = L_.apus_hip_dispatches() - d0
         H.synchronize()
         H._check(L_.apus_hip_graph_begin(), "graph_begin")
         for t in range(tokens):
@@ -334,7 +336,7 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
         return {"tok_s": 1.0 / t_tok, "ms_per_token": t_tok * 1e3, "layers": L,
                 "resident_GB": (L_.apus_hip_store_bytes(store) + (dbytes + dsb) * L) / 1e9,
                 "bytes_per_token": tok_bytes, "gbs": tok_bytes / t_tok / 1e9,
-                "launches_per_token": L * 8, "fill_s": fill_s}
+                "launches_per_token": launches, "fill_s": fill_s}
     finally:
         L_.apus_hip_store_free(store)
 

@@ -102,15 +102,39 @@ def test_fp8_linear(hip, oracle, rng, M, O, K):
 
 
 def test_fp4_gemm_m_independent(hip, oracle, rng):
-    """Batched rows are bitwise equal to the same rows computed alone
-    (the reference's M-independence gate, tests/m12/README.md:331-354)."""
+    """Within a schedule, a row's result does not depend on the batch (the
+    reference's M-independence gate, tests/m12/README.md:331-354): up to 8
+    rows (split-K schedule) and more than 8 rows (tile schedule) are each
+    checked bitwise. Across the two schedules the K split differs, so the
+    bits may differ within the GEMM tolerance."""
     O, K = 256, 2048
     w, ws = fp4_weights(rng, O, K)
-    c, s = oracle.act_quant(acts(rng, 20, K))
-    full = hip.fp4_gemm(w, ws, c, s)
-    for m in (0, 7, 19):
+    c, s = oracle.act_quant(acts(rng, 40, K))
+    big = hip.fp4_gemm(w, ws, c, s)                         # tile schedule
+    mid = hip.fp4_gemm(w, ws, c[5:25].copy(), s[5:25].copy())
+    assert np.array_equal(mid.view(np.uint32), big[5:25].view(np.uint32))
+    few = hip.fp4_gemm(w, ws, c[:6].copy(), s[:6].copy())  # few-row schedule
+    for m in (0, 5):
         one = hip.fp4_gemm(w, ws, c[m:m + 1].copy(), s[m:m + 1].copy())
-        assert np.array_equal(one.view(np.uint32), full[m:m + 1].view(np.uint32))
+        assert np.array_equal(one.view(np.uint32), few[m:m + 1].view(np.uint32))
+    assert max_rel(few, big[:6]) <= 1e-3
+
+
+@pytest.mark.parametrize("fmt,M,O,K", [("fp8", 100, 256, 4096), ("fp8", 64, 384, 2048),
+                                       ("fp4", 77, 256, 4096), ("fp4", 9, 128, 2048)])
+def test_gemm_tile_schedule(hip, oracle, rng, fmt, M, O, K):
+    """More than 8 rows, K 2048/4096: the 64 x 128 tile schedule, ragged M."""
+    c, s = oracle.act_quant(acts(rng, M, K, 2.0))
+    if fmt == "fp8":
+        w, ws = fp8_weights(rng, O, K)
+        got, want = hip.fp8_gemm(w, ws, c, s), oracle.fp8_gemm(w, ws, c, s)
+        truth, esc = oracle.fp8_truth(w, ws, c, s)
+    else:
+        w, ws = fp4_weights(rng, O, K)
+        got, want = hip.fp4_gemm(w, ws, c, s), oracle.fp4_gemm(w, ws, c, s)
+        truth, esc = oracle.fp4_truth(w, ws, c, s)
+    assert max_rel(got, want) <= 1e-3
+    assert err_esc(got, truth, esc) <= 1e-4
 
 
 @pytest.mark.parametrize("fmt", ["fp4", "fp8"])
