@@ -22,6 +22,7 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libapus_hip.so")
+W_TILED = 0x100        # APUS_HIP_W_TILED: weights in the MFMA-tiled layout
 
 u8p = C.POINTER(C.c_uint8)
 f32p = C.POINTER(C.c_float)
@@ -98,6 +99,10 @@ SIGNATURES = {
     "apus_hip_fp8_gemm_dev": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int]),
     "apus_hip_gemm_grouped_dev": (C.c_int, [C.c_int, vp, C.c_int, vp, vp, C.c_int, C.c_int,
                                             C.c_int, C.c_int, C.c_int]),
+    "apus_hip_store_tiled": (C.c_int, [vp]),
+    "apus_hip_linear_dev": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
+    "apus_hip_pack_weights_dev": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int]),
+    "apus_hip_unpack_weights_dev": (C.c_int, [C.c_int, vp, vp, vp, vp, C.c_int, C.c_int]),
     "apus_hip_linear_workspace": (C.c_size_t, [C.c_int, C.c_int]),
     "apus_hip_fp4_linear_dev": (C.c_int, [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),
     "apus_hip_fp8_linear_dev": (C.c_int, [vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, vp]),

@@ -50,11 +50,14 @@ struct DenseW {        /* one cached dense weight (codes/packed + scales) */
     uint8_t *w, *ws;
     size_t wbytes, sbytes;
     uint64_t fp;
+    int wfmt, O, K;    /* the layout of a tiled copy depends on the shape */
+    bool tiled;        /* held in the MFMA-tiled layout */
 };
 
 struct ExpertW {       /* one cached routed expert, six tensors */
     uint8_t *p[6];
     size_t bytes;
+    bool tiled;
 };
 
 struct State {
@@ -155,14 +158,40 @@ uint64_t fingerprint(const uint8_t *p, size_t n) {
 
 /* dense weight cache lookup/insert, keyed by the host weight pointer (the
  * engine's weight pointers are stable, c/backend_metal.h:38-43); a hit whose
- * shape, scale pointer or sampled contents changed is re-uploaded */
-const DenseW *dense_weight(const uint8_t *w, const uint8_t *ws, size_t wbytes,
-                           size_t sbytes) {
+ * format, shape (O, K: the tiled layout depends on it), scale pointer or
+ * sampled contents changed is re-uploaded */
+/* shapes whose weights are kept in the MFMA-tiled layout (the decode,
+ * prefill and tile schedules read it) */
+bool tiled_shape(int O, int K) { return (K == 2048 || K == 4096) && O > 0 && O % 128 == 0; }
+
+/* routed experts of this shape are held MFMA-tiled (w1/w3 [inter, dim] and
+ * w2 [dim, inter] all qualify) */
+bool moe_tiled(int dim, int inter) { return tiled_shape(inter, dim) && tiled_shape(dim, inter); }
+
+/* host row-major weights -> device, MFMA-tiled when `tiled` (staged through
+ * scratch slots 4 and 5) */
+bool upload_weights(int wfmt, uint8_t *dw, uint8_t *dws, const void *w, const void *ws,
+                    size_t wbytes, size_t sbytes, int O, int K, bool tiled) {
+    if (!tiled) return upload(dw, w, wbytes) && upload(dws, ws, sbytes);
+    uint8_t *sw = (uint8_t *)scratch(4, wbytes);
+    uint8_t *ss = (uint8_t *)scratch(5, sbytes);
+    if (!sw || !ss || !upload(sw, w, wbytes) || !upload(ss, ws, sbytes)) return false;
+    if (!launched(apus_launch_pack(wfmt, sw, ss, dw, dws, O, K, 0, g.stream), "pack")) return false;
+    if (wfmt == APUS_W_FP8 && !ok(hipMemcpyAsync(dws, ss, sbytes, hipMemcpyDeviceToDevice, g.stream),
+                                  "D2D scales"))
+        return false;
+    /* the staging slots are reused by the next upload */
+    return finish();
+}
+
+const DenseW *dense_weight(int wfmt, const uint8_t *w, const uint8_t *ws, size_t wbytes,
+                           size_t sbytes, int O, int K) {
     const uint64_t fp = fingerprint(w, wbytes) ^ (fingerprint(ws, sbytes) * 31);
     auto it = g.dense.find(w);
     if (it != g.dense.end()) {
         DenseW &d = it->second;
-        if (d.host_scales == ws && d.wbytes == wbytes && d.sbytes == sbytes && d.fp == fp)
+        if (d.host_scales == ws && d.wbytes == wbytes && d.sbytes == sbytes && d.fp == fp &&
+            d.wfmt == wfmt && d.O == O && d.K == K)
             return &d;
         (void)hipStreamSynchronize(g.stream);
         (void)hipFree(d.w);
@@ -174,10 +203,14 @@ const DenseW *dense_weight(const uint8_t *w, const uint8_t *ws, size_t wbytes,
         set_err("dense weight budget exhausted (APUS_HIP_DENSE_MB)");
         return nullptr;
     }
-    DenseW d{ws, nullptr, nullptr, wbytes, sbytes, fp};
+    DenseW d{ws, nullptr, nullptr, wbytes, sbytes, fp, wfmt, O, K, false};
     if (!ok(hipMalloc(&d.w, wbytes), "hipMalloc weight")) return nullptr;
     if (!ok(hipMalloc(&d.ws, sbytes), "hipMalloc scales")) { hipFree(d.w); return nullptr; }
-    if (!upload(d.w, w, wbytes) || !upload(d.ws, ws, sbytes)) return nullptr;
+    d.tiled = tiled_shape(O, K);
+    if (!upload_weights(wfmt, d.w, d.ws, w, ws, wbytes, sbytes, O, K, d.tiled)) {
+        hipFree(d.w); hipFree(d.ws);
+        return nullptr;
+    }
     g.bytes_uploaded += wbytes + sbytes;
     g.bytes_resident += wbytes + sbytes;
     return &(g.dense[w] = d);
@@ -191,9 +224,12 @@ bool shape_ok(int M, int K, int O) {
     return true;
 }
 
+/* wfmt may carry APUS_HIP_W_TILED */
 int gemm_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
              const float *as, float *out, int M, int O, int K, int round_out, hipStream_t st) {
     ApusGemmArgs a{};
+    a.wtiled = (wfmt & APUS_HIP_W_TILED) ? 1 : 0;
+    wfmt &= ~APUS_HIP_W_TILED;
     a.acodes = acodes; a.ascale = as; a.ents = nullptr;
     a.ent0.w = w; a.ent0.ws = ws; a.ent0.out = out;
     a.ent0.arows = nullptr; a.ent0.orows = nullptr;
@@ -209,6 +245,8 @@ int linear_fused(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x, 
                  int M, int K, int O, hipStream_t st) {
     if (M > 8 || (K != 2048 && K != 4096) || O % 128) return -1;
     ApusGemmArgs a{};
+    a.wtiled = (wfmt & APUS_HIP_W_TILED) ? 1 : 0;
+    wfmt &= ~APUS_HIP_W_TILED;
     a.ents = nullptr;
     a.ent0.w = w; a.ent0.ws = ws; a.ent0.out = out;
     a.ent0.arows = nullptr; a.ent0.orows = nullptr;
@@ -226,8 +264,9 @@ int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
     const size_t wbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 2 : (size_t)O * K;
     const size_t sbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 32
                                              : (size_t)((O + 127) / 128) * (K / 128);
-    const DenseW *d = dense_weight(w, ws, wbytes, sbytes);
+    const DenseW *d = dense_weight(wfmt, w, ws, wbytes, sbytes, O, K);
     if (!d) return 1;
+    const int wf = wfmt | (d->tiled ? APUS_HIP_W_TILED : 0);
     const size_t nab = K / 128;
     float *dx = (float *)scratch(0, (size_t)M * K * 4);
     uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
@@ -235,11 +274,11 @@ int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
     float *dout = (float *)scratch(3, (size_t)M * O * 4);
     if (!dx || !dc || !dsc || !dout) return 1;
     if (!upload(dx, x, (size_t)M * K * 4)) return 1;
-    const int f = linear_fused(wfmt, d->w, d->ws, dx, dout, M, K, O, g.stream);
+    const int f = linear_fused(wf, d->w, d->ws, dx, dout, M, K, O, g.stream);
     if (f > 0) return 1;
     if (f < 0) {
         if (!launched(apus_launch_act_quant(dx, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
-        if (gemm_dev(wfmt, d->w, d->ws, dc, dsc, dout, M, O, K, 1, g.stream)) return 1;
+        if (gemm_dev(wf, d->w, d->ws, dc, dsc, dout, M, O, K, 1, g.stream)) return 1;
     }
     if (!download(out, dout, (size_t)M * O * 4) || !finish()) return 1;
     return 0;
@@ -323,7 +362,7 @@ int moe_pair_max() {
  * pointers (w1, w1s, w2, w2s, w3, w3s) */
 int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
                  const float *x, const int32_t *idx, const float *wgt, int s,
-                 int topk, float *y, const MoeWs &w, hipStream_t st) {
+                 int topk, float *y, const MoeWs &w, bool wtiled, hipStream_t st) {
     const int nj = s * topk;
     ApusExpertTable t;
     t.w1 = tab; t.w1s = tab + E; t.w2 = tab + 2 * E; t.w2s = tab + 3 * E;
@@ -335,6 +374,7 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
     if (nj <= moe_pair_max() && (dim == 2048 || dim == 4096) &&
         (inter == 2048 || inter == 4096)) {
         ApusGemmArgs a{};
+        a.wtiled = wtiled;
         a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
         a.asrc = APUS_A_F32; a.ax = x;
         a.pidx = idx; a.nmat = 2; a.adiv = topk; a.pE = E;
@@ -344,6 +384,7 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         if (!launched(apus_launch_gemm_few(APUS_W_FP4, &a, 2 * nj, 1, 0, st), "pair w1/w3"))
             return 1;
         ApusGemmArgs b{};
+        b.wtiled = wtiled;
         b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
         b.asrc = APUS_A_SWIGLU; b.ax = w.gm; b.au = w.um; b.limit = limit;
         b.pidx = idx; b.nmat = 1; b.adiv = 1; b.pE = E;
@@ -362,9 +403,11 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         return 1;
     const int n_small = std::min(E, nj), n_large = std::min(E, nj / (SMALL + 1));
     ApusGemmArgs a{};
+    a.wtiled = wtiled;
     a.acodes = w.xc; a.ascale = w.xs;
     a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
     ApusGemmArgs b{};
+    b.wtiled = wtiled;
     b.acodes = w.hc; b.ascale = w.hs;
     b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
     for (int pass = 0; pass < 2; ++pass) {
@@ -397,6 +440,7 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
 
 struct ApusHipStore {
     int L, E, dim, inter;
+    bool tiled;            /* expert matrices held MFMA-tiled */
     size_t sz[6];          /* bytes of w1, w1s, w2, w2s, w3, w3s */
     size_t expert_bytes;   /* 256-aligned slab per expert */
     std::vector<uint8_t *> layer_base;   /* one allocation per layer */
@@ -500,9 +544,12 @@ int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent, const ui
     if (!upload(dc, acodes, rows * K) || !upload(dsc, as, rows * nab * 4)) return 1;
     std::vector<ApusGemmEnt> he(n_ent);
     size_t orow = 0;
+    bool tiled = false;     /* same (O, K) for every entry: all tiled or none */
     for (size_t i = 0; i < n_ent; i++) {
-        const DenseW *d = dense_weight(ents[i].w, ents[i].ws, O * K / 2, O * K / 32);
+        const DenseW *d = dense_weight(APUS_W_FP4, ents[i].w, ents[i].ws, O * K / 2, O * K / 32,
+                                       (int)O, (int)K);
         if (!d) return 1;
+        tiled = d->tiled;
         he[i] = ApusGemmEnt{d->w, d->ws, dout, nullptr, nullptr, (int32_t)ents[i].m0,
                             (int32_t)orow, (int32_t)ents[i].M, 0};
         orow += ents[i].M;
@@ -511,6 +558,7 @@ int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent, const ui
     ApusGemmArgs a{};
     a.acodes = dc; a.ascale = dsc; a.ents = dents;
     a.O = (int)O; a.K = (int)K; a.ldo = (int)O; a.round_out = 0; a.max_m = (int)max_m;
+    a.wtiled = tiled ? 1 : 0;
     if (!launched(apus_launch_gemm(APUS_W_FP4, &a, (int)n_ent, g.stream), "grouped gemm")) return 1;
     orow = 0;
     for (size_t i = 0; i < n_ent; i++) {
@@ -562,8 +610,18 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
             size_t off = 0;
             for (int i = 0; i < 6; i++) {
                 ew.p[i] = base + off;
-                if (!upload(ew.p[i], src[i], sz[i])) return 1;
                 off += align256(sz[i]);
+            }
+            /* w1, w3: [inter, dim]; w2: [dim, inter] */
+            const int mo[3] = {inter, dim, inter}, mk[3] = {dim, inter, dim};
+            ew.tiled = moe_tiled(dim, inter);
+            for (int m = 0; m < 3; m++) {
+                if (!upload_weights(APUS_W_FP4, ew.p[2 * m], ew.p[2 * m + 1], src[2 * m],
+                                    src[2 * m + 1], sz[2 * m], sz[2 * m + 1], mo[m], mk[m],
+                                    ew.tiled)) {
+                    hipFree(base);
+                    return 1;
+                }
             }
             ew.bytes = tot;
             g.bytes_uploaded += tot;
@@ -584,7 +642,10 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
         !upload(dx, x, (size_t)s * dim * 4) || !upload(didx, idx, (size_t)nj * 4) ||
         !upload(dwgt, wgt, (size_t)nj * 4))
         return 1;
-    if (moe_pipeline(E, dim, inter, w->limit, mw.tab, dx, didx, dwgt, s, topk, dy, mw, g.stream)) return 1;
+    const bool etiled = moe_tiled(dim, inter);
+    if (moe_pipeline(E, dim, inter, w->limit, mw.tab, dx, didx, dwgt, s, topk, dy, mw, etiled,
+                     g.stream))
+        return 1;
     if (!download(y, dy, (size_t)s * dim * 4) || !finish()) return 1;
     return 0;
 }
@@ -599,25 +660,54 @@ int apus_hip_act_quant_dev(const float *x, int M, int K, uint8_t *codes, float *
 int apus_hip_fp4_gemm_dev(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
                           const float *as, float *out, int M, int O, int K, int round_out) {
     if (!ensure_init() || !shape_ok(M, K, O)) return 1;
-    return gemm_dev(APUS_W_FP4, w, ws, acodes, as, out, M, O, K, round_out, dev_stream());
+    return gemm_dev(APUS_W_FP4 | (round_out & APUS_HIP_W_TILED), w, ws, acodes, as, out, M, O, K,
+                    round_out & 1, dev_stream());
 }
 
 int apus_hip_fp8_gemm_dev(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
                           const float *as, float *out, int M, int O, int K, int round_out) {
     if (!ensure_init() || !shape_ok(M, K, O)) return 1;
-    return gemm_dev(APUS_W_FP8, w, ws, acodes, as, out, M, O, K, round_out, dev_stream());
+    return gemm_dev(APUS_W_FP8 | (round_out & APUS_HIP_W_TILED), w, ws, acodes, as, out, M, O, K,
+                    round_out & 1, dev_stream());
 }
 
 int apus_hip_gemm_grouped_dev(int wfmt, const ApusHipGemmEnt *ents, int n_ent,
                               const uint8_t *acodes, const float *as, int O, int K, int ldo,
                               int round_out, int max_m) {
     if (!ensure_init() || !shape_ok(1, K, O)) return 1;
-    if (wfmt != APUS_W_FP4 && wfmt != APUS_W_FP8) { set_err("gemm_grouped_dev: bad format"); return 1; }
+    const int fmt = wfmt & ~APUS_HIP_W_TILED;
+    const bool tiled = (wfmt & APUS_HIP_W_TILED) != 0;
+    if (fmt != APUS_W_FP4 && fmt != APUS_W_FP8) { set_err("gemm_grouped_dev: bad format"); return 1; }
+    if (tiled && ((K != 2048 && K != 4096) || O % 128)) {
+        set_err("gemm_grouped_dev: tiled weights need K 2048/4096 and O %% 128 == 0");
+        return 1;
+    }
     static_assert(sizeof(ApusHipGemmEnt) == sizeof(ApusGemmEnt), "entry layout");
     ApusGemmArgs a{};
     a.acodes = acodes; a.ascale = as; a.ents = reinterpret_cast<const ApusGemmEnt *>(ents);
     a.O = O; a.K = K; a.ldo = ldo; a.round_out = round_out; a.max_m = max_m;
-    return launched(apus_launch_gemm(wfmt, &a, n_ent, dev_stream()), "gemm_grouped_dev") ? 0 : 1;
+    a.wtiled = tiled ? 1 : 0;
+    return launched(apus_launch_gemm(fmt, &a, n_ent, dev_stream()), "gemm_grouped_dev") ? 0 : 1;
+}
+
+static int pack_dev(int wfmt, const uint8_t *w, const uint8_t *ws, uint8_t *tw, uint8_t *tws,
+                    int O, int K, int unpack) {
+    if (!ensure_init()) return 1;
+    if ((wfmt != APUS_W_FP4 && wfmt != APUS_W_FP8) || O <= 0 || O % 16 || K <= 0 || K % 512) {
+        set_err("pack_weights: needs wfmt 0/1, O %% 16 == 0, K %% 512 == 0");
+        return 1;
+    }
+    return launched(apus_launch_pack(wfmt, w, ws, tw, tws, O, K, unpack, dev_stream()), "pack") ? 0 : 1;
+}
+
+int apus_hip_pack_weights_dev(int wfmt, const uint8_t *w, const uint8_t *ws, uint8_t *tw,
+                              uint8_t *tws, int O, int K) {
+    return pack_dev(wfmt, w, ws, tw, tws, O, K, 0);
+}
+
+int apus_hip_unpack_weights_dev(int wfmt, const uint8_t *tw, const uint8_t *tws, uint8_t *w,
+                                uint8_t *ws, int O, int K) {
+    return pack_dev(wfmt, tw, tws, w, ws, O, K, 1);
 }
 
 size_t apus_hip_linear_workspace(int M, int K) {
@@ -627,6 +717,12 @@ size_t apus_hip_linear_workspace(int M, int K) {
 static int linear_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x, float *out,
                       int M, int K, int O, void *workspace) {
     if (!ensure_init() || !shape_ok(M, K, O)) return 1;
+    const int fmt = wfmt & ~APUS_HIP_W_TILED;
+    if ((fmt != APUS_W_FP4 && fmt != APUS_W_FP8) ||
+        ((wfmt & APUS_HIP_W_TILED) && !tiled_shape(O, K))) {
+        set_err("linear_dev: bad format, or tiled weights with K not 2048/4096 or O %% 128 != 0");
+        return 1;
+    }
     if (!workspace) { set_err("linear_dev: workspace required"); return 1; }
     const int f = linear_fused(wfmt, w, ws, x, out, M, K, O, dev_stream());
     if (f >= 0) return f;
@@ -634,6 +730,11 @@ static int linear_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const float
     float *dsc = (float *)(dc + align256((size_t)M * K));
     if (!launched(apus_launch_act_quant(x, K, nullptr, M, K, dc, dsc, dev_stream()), "act_quant")) return 1;
     return gemm_dev(wfmt, w, ws, dc, dsc, out, M, O, K, 1, dev_stream());
+}
+
+int apus_hip_linear_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x, float *out,
+                        int M, int K, int O, void *workspace) {
+    return linear_dev(wfmt, w, ws, x, out, M, K, O, workspace);
 }
 
 int apus_hip_fp4_linear_dev(const uint8_t *w, const uint8_t *ws, const float *x, float *out,
@@ -658,6 +759,7 @@ ApusHipStore *apus_hip_store_create(int n_layers, int E, int dim, int inter, cha
     }
     ApusHipStore *st = new ApusHipStore();
     st->L = n_layers; st->E = E; st->dim = dim; st->inter = inter;
+    st->tiled = moe_tiled(dim, inter);
     const size_t sz[6] = {(size_t)inter * dim / 2, (size_t)inter * dim / 32,
                           (size_t)dim * inter / 2, (size_t)dim * inter / 32,
                           (size_t)inter * dim / 2, (size_t)inter * dim / 32};
@@ -711,16 +813,34 @@ uint64_t apus_hip_store_bytes(const ApusHipStore *st) {
 
 int apus_hip_store_fill_random(ApusHipStore *st, uint64_t seed) {
     if (!st) return 1;
+    std::lock_guard<std::mutex> lk(g_mu);
     static const int kinds[6] = {0, 1, 0, 1, 0, 1};
+    const int mo[3] = {st->inter, st->dim, st->inter}, mk[3] = {st->dim, st->inter, st->dim};
+    /* tiled stores: each matrix is generated row-major into staging (stream
+     * ordered, so the staging is reused) and packed into place */
+    uint8_t *sw = st->tiled ? (uint8_t *)scratch(4, st->sz[0] > st->sz[2] ? st->sz[0] : st->sz[2]) : nullptr;
+    uint8_t *ss = st->tiled ? (uint8_t *)scratch(5, st->sz[1] > st->sz[3] ? st->sz[1] : st->sz[3]) : nullptr;
+    if (st->tiled && (!sw || !ss)) return 1;
     for (int l = 0; l < st->L; l++)
         for (int e = 0; e < st->E; e++) {
+            uint8_t *p[6];
             size_t off = 0;
             for (int i = 0; i < 6; i++) {
-                uint8_t *p = st->layer_base[l] + st->expert_bytes * e + off;
-                const uint64_t sid = ((uint64_t)l * st->E + e) * 8 + i;
-                if (!launched(apus_launch_fill(p, st->sz[i], seed, sid, 0, kinds[i], g.stream), "fill"))
-                    return 1;
+                p[i] = st->layer_base[l] + st->expert_bytes * e + off;
                 off += align256(st->sz[i]);
+            }
+            for (int m = 0; m < 3; m++) {
+                for (int h = 0; h < 2; h++) {
+                    const int i = 2 * m + h;
+                    const uint64_t sid = ((uint64_t)l * st->E + e) * 8 + i;
+                    uint8_t *dst = st->tiled ? (h ? ss : sw) : p[i];
+                    if (!launched(apus_launch_fill(dst, st->sz[i], seed, sid, 0, kinds[i], g.stream), "fill"))
+                        return 1;
+                }
+                if (st->tiled &&
+                    !launched(apus_launch_pack(APUS_W_FP4, sw, ss, p[2 * m], p[2 * m + 1], mo[m], mk[m], 0,
+                                               g.stream), "pack"))
+                    return 1;
             }
         }
     return finish() ? 0 : 1;
@@ -729,13 +849,20 @@ int apus_hip_store_fill_random(ApusHipStore *st, uint64_t seed) {
 int apus_hip_store_put(ApusHipStore *st, int layer, int eid, const ApusFp4W *w1,
                        const ApusFp4W *w2, const ApusFp4W *w3) {
     if (!st || layer < 0 || layer >= st->L || eid < 0 || eid >= st->E) return 1;
+    std::lock_guard<std::mutex> lk(g_mu);
     const void *src[6] = {w1->packed, w1->scales, w2->packed, w2->scales, w3->packed, w3->scales};
+    const int mo[3] = {st->inter, st->dim, st->inter}, mk[3] = {st->dim, st->inter, st->dim};
+    uint8_t *p[6];
     size_t off = 0;
     for (int i = 0; i < 6; i++) {
-        uint8_t *p = st->layer_base[layer] + st->expert_bytes * eid + off;
-        if (!upload(p, src[i], st->sz[i])) return 1;
-        g.bytes_uploaded += st->sz[i];
+        p[i] = st->layer_base[layer] + st->expert_bytes * eid + off;
         off += align256(st->sz[i]);
+    }
+    for (int m = 0; m < 3; m++) {
+        if (!upload_weights(APUS_W_FP4, p[2 * m], p[2 * m + 1], src[2 * m], src[2 * m + 1],
+                            st->sz[2 * m], st->sz[2 * m + 1], mo[m], mk[m], st->tiled))
+            return 1;
+        g.bytes_uploaded += st->sz[2 * m] + st->sz[2 * m + 1];
     }
     return finish() ? 0 : 1;
 }
@@ -749,6 +876,8 @@ int apus_hip_store_get(const ApusHipStore *st, int layer, int eid, const uint8_t
     }
     return 0;
 }
+
+int apus_hip_store_tiled(const ApusHipStore *st) { return st && st->tiled ? 1 : 0; }
 
 size_t apus_hip_moe_workspace(const ApusHipStore *st, int s, int topk) {
     if (!st) return 0;
@@ -764,7 +893,7 @@ int apus_hip_moe_routed_dev(const ApusHipStore *st, int layer, const float *x, c
     }
     MoeWs mw = moe_carve(workspace, s, topk, st->E, st->dim, st->inter);
     return moe_pipeline(st->E, st->dim, st->inter, limit, st->layer_tab[layer], x, idx, wgt, s,
-                        topk, y, mw, dev_stream());
+                        topk, y, mw, st->tiled, dev_stream());
 }
 
 /* --------------------------------------------------------------- helpers */

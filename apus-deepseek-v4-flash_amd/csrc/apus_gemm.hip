@@ -282,23 +282,53 @@ __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args
  */
 #define APUS_DEC_WAVES 4
 
+/* The weight stream of one lane of a 16-row tile: the address of its
+ * 16 bytes of 128-group 0 and the distance between consecutive groups (qs)
+ * and, for FP4, between the 16-byte scale runs of consecutive 512-slices
+ * (ss). Row-major weights ([O, K/2] or [O, K]): 16 rows x 64 bytes per load.
+ * MFMA-tiled weights (launch flag wtiled): for each 16-row tile and
+ * 128-group the 64 lanes' pieces are stored back to back, so a load reads
+ * 1 KB contiguously; FP4 scales are [O/16][K/512][16 rows][16 bytes]. FP8
+ * takes its second 16-byte piece of a group at qs / 2 in both layouts. */
+struct ApusWLane {
+    const uint8_t *w, *s;
+    uint32_t qs, ss;
+};
+
 template <int WF>
-__device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const uint8_t *wrow,
-                                                 const uint8_t *srow, int s, int g) {
+__device__ __forceinline__ ApusWLane apus_wlane(const ApusGemmEnt &ent, bool tiled, int o, int lane,
+                                                int K) {
+    const int NQ = K >> 7, NS = K >> 9;
+    ApusWLane l;
+    if constexpr (WF == APUS_W_FP4) {
+        if (tiled) {
+            l.w = ent.w + ((size_t)(o >> 4) * NQ * 64 + lane) * 16; l.qs = 1024;
+            l.s = ent.ws + ((size_t)(o >> 4) * NS * 16 + (o & 15)) * 16; l.ss = 256;
+        } else {
+            l.w = ent.w + (size_t)o * (K >> 1) + (lane >> 4) * 16; l.qs = 64;
+            l.s = ent.ws + (size_t)o * (K >> 5); l.ss = 16;
+        }
+    } else {
+        if (tiled) { l.w = ent.w + ((size_t)(o >> 4) * NQ * 128 + lane) * 16; l.qs = 2048; }
+        else       { l.w = ent.w + (size_t)o * K + (lane >> 4) * 16; l.qs = 128; }
+        l.s = ent.ws + (size_t)(o >> 7) * NQ; l.ss = 4;
+    }
+    return l;
+}
+
+/* the four groups of 512-slice s of a lane's weight stream */
+template <int WF>
+__device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const ApusWLane &l, int s) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-        const int q = s * 4 + st;
-        if (WF == APUS_W_FP4) {
-            f.w[st][0] = apus_ld16_stream(wrow + q * 64 + g * 16);
-        } else {
-            f.w[st][0] = apus_ld16_stream(wrow + q * 128 + g * 16);
-            f.w[st][1] = apus_ld16_stream(wrow + q * 128 + 64 + g * 16);
-        }
+        const uint8_t *p = l.w + (size_t)(s * 4 + st) * l.qs;
+        f.w[st][0] = apus_ld16_stream(p);
+        if constexpr (WF == APUS_W_FP8) f.w[st][1] = apus_ld16_stream(p + (l.qs >> 1));
     }
-    if (WF == APUS_W_FP4) {
-        f.s = apus_gld<apus_v4u>(srow + s * 16);
+    if constexpr (WF == APUS_W_FP4) {
+        f.s = apus_gld<apus_v4u>(l.s + (size_t)s * l.ss);
     } else {
-        const unsigned b4 = apus_gld<unsigned>(srow + s * 4);
+        const unsigned b4 = apus_gld<unsigned>(l.s + s * 4);
         f.s = apus_v4u{b4 & 0xffu, (b4 >> 8) & 0xffu, (b4 >> 16) & 0xffu, b4 >> 24};
     }
 }
@@ -432,9 +462,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
     uint8_t *lcodes = lds;
     uint8_t *lsc = lds + R * LDK;
     apus_v4f *lred = reinterpret_cast<apus_v4f *>(lds + ((R * LDK + R * NQ + 15) & ~15));
-    const uint8_t *wrow = ent.w + (size_t)o * (WF == APUS_W_FP4 ? (K >> 1) : K);
-    const uint8_t *srow = WF == APUS_W_FP4 ? ent.ws + (size_t)o * (K >> 5)
-                                           : ent.ws + (size_t)(o >> 7) * NQ;
+    const ApusWLane wl = apus_wlane<WF>(ent, args.wtiled, o, lane, K);
 
     const int sbase = kpart * NSW;
     for (int c0 = 0; active && c0 < ent.M; c0 += R) {
@@ -476,7 +504,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
             /* weight prefetch ring: issued after the staging loads (so waiting
              * for those does not wait for these) and before the LDS hand-off */
 #pragma unroll
-            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
+            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, sbase + u);
 #pragma unroll
             for (int j = 0; j < STAGE; ++j) {
                 const int rsub = threadIdx.x / K16;
@@ -493,7 +521,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
             if (pre && c0 == 0) r0 = raw0;
             else apus_stage_load<K, ASRC>(args, ent.arows, ent.a0, c0, rows, 0, r0);
 #pragma unroll
-            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, sbase + u, g);
+            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, sbase + u);
             apus_stage_quant<K, ASRC>(args, r0, lcodes, lsc);
             constexpr int PASSES = (R * NQ + 31) / 32;
 #pragma unroll
@@ -535,7 +563,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                     acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, sa, (int)cur.s[st]);
                 }
             }
-            if (si + PD < NSW) apus_load_b_full<WF>(cur, wrow, srow, s + PD, g);
+            if (si + PD < NSW) apus_load_b_full<WF>(cur, wl, s + PD);
         }
         if (KS > 1) {
             /* the K parts of a tile meet in LDS; part 0 adds them in part order */
@@ -618,9 +646,7 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int o = (blockIdx.x * APUS_PRE_WAVES + wave) * 16 + r;   /* O % 128 == 0 */
-    const uint8_t *wrow = ent.w + (size_t)o * (WF == APUS_W_FP4 ? (K >> 1) : K);
-    const uint8_t *srow = WF == APUS_W_FP4 ? ent.ws + (size_t)o * (K >> 5)
-                                           : ent.ws + (size_t)(o >> 7) * NQ;
+    const ApusWLane wl = apus_wlane<WF>(ent, args.wtiled, o, lane, K);
 
     for (int c0 = 0; c0 < ent.M; c0 += ROWS) {
         const int rows = min(ROWS, ent.M - c0);
@@ -661,7 +687,7 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
         for (int t = 0; t < TT; ++t) acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
         ApusBFrag<WF> ring[PD];
 #pragma unroll
-        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wrow, srow, u, g);
+        for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, u);
         apus_lds_barrier();
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
@@ -703,7 +729,7 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
                     asm volatile("" : "+v"(acc[t]) :: "memory");
                 }
             }
-            if (s + PD < NS) apus_load_b_full<WF>(cur, wrow, srow, s + PD, g);
+            if (s + PD < NS) apus_load_b_full<WF>(cur, wl, s + PD);
             if (s + 1 < NS) APUS_PRE_STORE((s + 1) & 1);
             apus_lds_barrier();
         }
@@ -765,9 +791,13 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
                                : (ent.arows ? apus_gld<int>(ent.arows) : ent.a0);
     const uint8_t *sap = args.acodes + (size_t)sar * K + spart * 32;
     const float *ssp = args.ascale + (size_t)sar * NQ;
-    const uint8_t *wrow = ent.w + (size_t)(nbase + r) * RB;
-    const uint8_t *wsrow = ent.ws + (WF == APUS_W_FP4 ? (size_t)(nbase + r) * (K / 32)
-                                                      : (size_t)blockIdx.x * NQ);
+    /* lane stream of the first of the wave's four 16-row tiles; the others
+     * follow at tstride (weights) and sstride (FP4 scales) */
+    const bool tiled = args.wtiled;
+    const ApusWLane wl = apus_wlane<WF>(ent, tiled, nbase + r, lane, K);
+    const size_t tstride = tiled ? (size_t)NQ * 16 * 64 * (WF == APUS_W_FP4 ? 1 : 2) : 16 * RB;
+    const size_t sstride = tiled ? (size_t)(K / 512) * 256 : 16 * (K / 32);
+    const uint8_t *wsrow = ent.ws + (size_t)blockIdx.x * NQ;     /* FP8 tile scales */
     /* FP8: the 128 x 128 tile scales of this column block, all groups */
     unsigned sb8[WF == APUS_W_FP8 ? NQ / 4 : 1];
     if constexpr (WF == APUS_W_FP8) {
@@ -777,13 +807,13 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
     auto load_b = [&](ApusTileB<WF> &f, int q) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint8_t *p = wrow + (size_t)i * 16 * RB;
+            const uint8_t *p = wl.w + i * tstride + (size_t)q * wl.qs;
             if constexpr (WF == APUS_W_FP4) {
-                f.w[i][0] = apus_gld<apus_v4u>(p + q * 64 + g * 16);
-                f.s[i] = apus_gld<unsigned>(wsrow + (size_t)i * 16 * (K / 32) + 4 * q);
+                f.w[i][0] = apus_gld<apus_v4u>(p);
+                f.s[i] = apus_gld<unsigned>(wl.s + i * sstride + (q >> 2) * wl.ss + (q & 3) * 4);
             } else {
-                f.w[i][0] = apus_gld<apus_v4u>(p + q * 128 + g * 16);
-                f.w[i][1] = apus_gld<apus_v4u>(p + q * 128 + 64 + g * 16);
+                f.w[i][0] = apus_gld<apus_v4u>(p);
+                f.w[i][1] = apus_gld<apus_v4u>(p + (wl.qs >> 1));
             }
         }
     };
@@ -959,11 +989,20 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
     if (n_ent <= 0) return hipSuccess;
     const bool grouped = a->ents != nullptr;
     const size_t row_tiles = (size_t)n_ent * ((a->O + 15) / 16);
+    constexpr int R = 8;
+    if (a->wtiled) {
+        /* tiled weights: only the decode, prefill and tile schedules read them */
+        if ((a->K != 2048 && a->K != 4096) || a->O % 128) return hipErrorInvalidValue;
+        if (!grouped && a->ent0.M <= R) {
+            ApusGemmArgs d = *a;
+            d.asrc = APUS_A_CODES;
+            return apus_launch_gemm_few(wfmt, &d, 1, R, 0, st);
+        }
+    }
     /* grouped launches with K = 2048 or 4096: entries with at most 8 rows
      * take the decode schedule, larger ones the prefill schedule (two
      * launches over the same entry table, each skipping the other's entries) */
-    constexpr int R = 8;
-    if (grouped && (row_tiles >= 512 || (a->max_m > 0 && a->max_m <= R)) &&
+    if (grouped && (row_tiles >= 512 || (a->max_m > 0 && a->max_m <= R) || a->wtiled) &&
         (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
         const bool run_dec = !(a->min_m >= R);
         const bool run_pre = !(a->max_m > 0 && a->max_m <= R);

@@ -32,6 +32,8 @@ typedef struct {
     const ApusGemmEnt *ents; /* grouped: device array; else NULL */
     ApusGemmEnt ent0;        /* the entry when ents == NULL */
     int O, K, ldo, round_out;
+    int wtiled;              /* every W (and FP4 scale) in the MFMA-tiled layout of
+                              * apus_launch_pack: K 2048 or 4096, O % 128 == 0 */
     int max_m;               /* upper bound on every entry's M (0 = unknown); a
                               * launch with max_m <= 8 runs only the few-row
                               * schedule */
@@ -109,6 +111,13 @@ hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
                                  int32_t *pair_sorted, int32_t *tok_sorted,
                                  ApusGemmEnt *e13s, ApusGemmEnt *e2s, ApusGemmEnt *e13l,
                                  ApusGemmEnt *e2l, int small_max, hipStream_t st);
+
+/* Row-major <-> MFMA-tiled weights (unpack = 0: w, ws -> tw, tws). FP4
+ * moves the weights and the per-32 scales, FP8 the weights only (its
+ * 128 x 128 tile scales keep their layout). O % 16 == 0, K % 512 == 0;
+ * source and destination must not overlap. */
+hipError_t apus_launch_pack(int wfmt, const uint8_t *w, const uint8_t *ws, uint8_t *tw,
+                            uint8_t *tws, int O, int K, int unpack, hipStream_t st);
 
 /* y[t, i] = sum_j wgt[t, j] * eo[t*topk + j, i] in j order (mul, then add,
  * each rounded), starting from +0. */

@@ -265,6 +265,57 @@ hipError_t apus_launch_fill(uint8_t *dst, size_t n, uint64_t seed,
     return hipGetLastError();
 }
 
+/* ------------------------------------------------- MFMA-tiled weight layout */
+
+/* One thread per 16-byte piece of the tiled layout: FP4 weights
+ * [O/16][K/128][64 lanes][16 B], FP8 weights [O/16][K/128][2][64 lanes][16 B]
+ * (lane = r + 16 g holds bytes [16 g, +16) of the group's first or second
+ * 64-byte half of row 16 t + r), then FP4 scales [O/16][K/512][16 rows][16 B].
+ * unpack != 0 runs the map backwards. */
+__global__ __launch_bounds__(256) void apus_pack_kernel(
+    const uint8_t *__restrict__ src, const uint8_t *__restrict__ ssrc, uint8_t *__restrict__ dst,
+    uint8_t *__restrict__ sdst, int fp8, int O, int K, int unpack) {
+    const size_t c = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const int NQ = K >> 7, NS = K >> 9;
+    const size_t rb = fp8 ? (size_t)K : (size_t)K / 2;
+    const size_t nw = (size_t)O * rb / 16;                   /* weight pieces */
+    const size_t ns = fp8 ? 0 : (size_t)O * (K / 32) / 16;   /* FP4 scale pieces */
+    if (c < nw) {
+        const int lane = (int)(c & 63);
+        size_t rest = c >> 6;
+        int h = 0;
+        if (fp8) { h = (int)(rest & 1); rest >>= 1; }
+        const int q = (int)(rest % NQ);
+        const size_t t = rest / NQ;
+        const size_t o = t * 16 + (lane & 15);
+        const size_t rm = o * rb + (fp8 ? (size_t)q * 128 + h * 64 : (size_t)q * 64) + (lane >> 4) * 16;
+        const size_t tm = c * 16;
+        if (unpack) *reinterpret_cast<uint4 *>(dst + rm) = *reinterpret_cast<const uint4 *>(src + tm);
+        else        *reinterpret_cast<uint4 *>(dst + tm) = *reinterpret_cast<const uint4 *>(src + rm);
+    } else if (c < nw + ns) {
+        const size_t d = c - nw;
+        const int r = (int)(d & 15);
+        const size_t rest = d >> 4;
+        const int sl = (int)(rest % NS);
+        const size_t t = rest / NS;
+        const size_t rm = (t * 16 + r) * (size_t)(K / 32) + sl * 16;
+        const size_t tm = d * 16;
+        if (unpack) *reinterpret_cast<uint4 *>(sdst + rm) = *reinterpret_cast<const uint4 *>(ssrc + tm);
+        else        *reinterpret_cast<uint4 *>(sdst + tm) = *reinterpret_cast<const uint4 *>(ssrc + rm);
+    }
+}
+
+hipError_t apus_launch_pack(int wfmt, const uint8_t *w, const uint8_t *ws, uint8_t *tw,
+                            uint8_t *tws, int O, int K, int unpack, hipStream_t st) {
+    if (O <= 0 || O % 16 || K <= 0 || K % 512) return hipErrorInvalidValue;
+    const bool fp8 = wfmt == APUS_W_FP8;
+    const size_t rb = fp8 ? (size_t)K : (size_t)K / 2;
+    const size_t n = (size_t)O * rb / 16 + (fp8 ? 0 : (size_t)O * (K / 32) / 16);
+    hipLaunchKernelGGL(apus_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       w, ws, tw, tws, fp8 ? 1 : 0, O, K, unpack);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------------ bf16 round */
 
 __global__ __launch_bounds__(256) void apus_bf16_round_kernel(float *v, size_t n) {

@@ -122,7 +122,18 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12):
     dents = dev.alloc(C.sizeof(ents))
     H._check(L.apus_hip_h2d(dents.ptr, C.addressof(ents), C.sizeof(ents)), "h2d ents")
     esz = C.sizeof(H.ApusHipGemmEnt)
-    assert copies % group == 0 or True
+    # the same copies in the MFMA-tiled resident layout
+    tw = dev.alloc(wbytes * copies)
+    tws = dev.alloc(sbytes * copies)
+    for c in range(copies):
+        H._check(L.apus_hip_pack_weights_dev(0, w.ptr + c * wbytes, ws.ptr + c * sbytes,
+                                             tw.ptr + c * wbytes, tws.ptr + c * sbytes, O, K), "pack")
+    tents = (H.ApusHipGemmEnt * copies)()
+    for c in range(copies):
+        tents[c] = H.ApusHipGemmEnt(tw.ptr + c * wbytes, tws.ptr + c * sbytes, out.ptr + c * O * 4,
+                                    None, None, 0, 0, 1, 0)
+    dtents = dev.alloc(C.sizeof(tents))
+    H._check(L.apus_hip_h2d(dtents.ptr, C.addressof(tents), C.sizeof(tents)), "h2d tents")
 
     def gemv(i):
         c = i % copies
@@ -134,6 +145,11 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12):
         H._check(L.apus_hip_gemm_grouped_dev(0, dents.ptr + c0 * esz, group, codes.ptr, scales.ptr,
                                              O, K, O, 0, 1), "grouped gemv")
 
+    def grouped_tiled(j):
+        c0 = (j * group) % (copies - copies % group)
+        H._check(L.apus_hip_gemm_grouped_dev(0 | H.W_TILED, dtents.ptr + c0 * esz, group, codes.ptr,
+                                             scales.ptr, O, K, O, 0, 1), "grouped gemv tiled")
+
     def linear(i):
         c = i % copies
         H._check(L.apus_hip_fp4_linear_dev(w.ptr + c * wbytes, ws.ptr + c * sbytes, dx.ptr,
@@ -142,9 +158,11 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12):
     for i in range(warmup):
         gemv(i)
         grouped(i)
+        grouped_tiled(i)
     H.synchronize()
     launches = max(1, steps // group)
     ms_group = timed_graph(H, grouped, launches)
+    ms_tiled = timed_graph(H, grouped_tiled, launches)
     ms_serial = timed_graph(H, gemv, steps)
     ms_eager = timed_eager(H, gemv, steps)
     ms_lin = timed_graph(H, linear, steps)
@@ -171,6 +189,8 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12):
         "ms_total": ms_group, "ms_per_step": ms_group / gsteps, "bytes": gemv_bytes,
         "gbs": gemv_bytes * gsteps / (ms_group * 1e-3) / 1e9,
         "launch_us": ms_group / launches * 1e3, "launch_bytes": gemv_bytes * group,
+        "tiled_gbs": gemv_bytes * gsteps / (ms_tiled * 1e-3) / 1e9,
+        "tiled_launch_us": ms_tiled / launches * 1e3,
         "serial_us": ms_serial / steps * 1e3,
         "serial_gbs": gemv_bytes * steps / (ms_serial * 1e-3) / 1e9,
         "lanes_gbs": gemv_bytes * steps / (ms_lanes * 1e-3) / 1e9,

@@ -153,12 +153,17 @@ int apus_hip_fp8_gemm(const uint8_t *w, const uint8_t *ws,
                       const uint8_t *acodes, const float *as, float *out,
                       int M, int O, int K);
 
+/* weight-layout flag of the device entry points: MFMA-tiled weights */
+#define APUS_HIP_W_TILED 0x100
+
 /* ---- device-pointer entry points (asynchronous on the backend stream) ----
  * Same semantics as the host versions; all pointers are device pointers.
  * They exist for callers that keep activations in HBM between layers and
  * for measurement with inputs already resident. */
 int apus_hip_act_quant_dev(const float *x, int M, int K, uint8_t *codes,
                            float *scales);
+/* round_out: bit 0 BF16-rounds the outputs; | APUS_HIP_W_TILED for weights
+ * in the MFMA-tiled layout (K 2048/4096, O % 128 == 0). */
 int apus_hip_fp4_gemm_dev(const uint8_t *w, const uint8_t *ws,
                           const uint8_t *acodes, const float *as, float *out,
                           int M, int O, int K, int round_out);
@@ -173,7 +178,9 @@ int apus_hip_fp8_gemm_dev(const uint8_t *w, const uint8_t *ws,
  * o0 + m; W is MXFP4 [O, K/2] + [O, K/32] (wfmt 0) or FP8 [O, K] +
  * [ceil(O/128), K/128] (wfmt 1). max_m is an upper bound on every entry's
  * M, or 0 when unknown (entries with M > max_m may be left uncomputed).
- * round_out: BF16-round the outputs. */
+ * round_out: BF16-round the outputs. wfmt | APUS_HIP_W_TILED: every W (and
+ * FP4 scale array) is in the MFMA-tiled layout of apus_hip_pack_weights_dev
+ * (then K must be 2048 or 4096 and O % 128 == 0). */
 typedef struct {
     const uint8_t *w, *ws;
     float *out;
@@ -183,6 +190,18 @@ typedef struct {
 int apus_hip_gemm_grouped_dev(int wfmt, const ApusHipGemmEnt *ents, int n_ent,
                               const uint8_t *acodes, const float *as, int O, int K,
                               int ldo, int round_out, int max_m);
+/* Row-major <-> MFMA-tiled weights, device to device (no counterpart in the
+ * reference: a resident-weight layout of this backend). The tiled layout
+ * stores, for each 16-row tile and 128-wide K group, the 16-byte pieces in
+ * matrix-core lane order, so the GEMM streams them with contiguous 1 KB
+ * loads. wfmt 0 (MXFP4): weights [O, K/2] and scales [O, K/32] both move;
+ * wfmt 1 (FP8): the weights move, the 128 x 128 tile scales keep their
+ * layout (ws/tws unused). O % 16 == 0, K % 512 == 0, no overlap. Async on
+ * the backend stream. */
+int apus_hip_pack_weights_dev(int wfmt, const uint8_t *w, const uint8_t *ws, uint8_t *tw,
+                              uint8_t *tws, int O, int K);
+int apus_hip_unpack_weights_dev(int wfmt, const uint8_t *tw, const uint8_t *tws, uint8_t *w,
+                                uint8_t *ws, int O, int K);
 /* Linear = act quant + GEMM (+ BF16 out) with a caller workspace of
  * apus_hip_linear_workspace(M, K) bytes. */
 size_t apus_hip_linear_workspace(int M, int K);
@@ -192,13 +211,20 @@ int apus_hip_fp4_linear_dev(const uint8_t *w, const uint8_t *ws,
 int apus_hip_fp8_linear_dev(const uint8_t *w, const uint8_t *ws,
                             const float *x, float *out, int M, int K, int O,
                             void *workspace);
+/* Either format: wfmt 0 (MXFP4) or 1 (FP8), | APUS_HIP_W_TILED for weights
+ * in the MFMA-tiled layout (K 2048/4096, O % 128 == 0). */
+int apus_hip_linear_dev(int wfmt, const uint8_t *w, const uint8_t *ws,
+                        const float *x, float *out, int M, int K, int O,
+                        void *workspace);
 
 /* ---- HBM-resident expert store (replaces the NVMe/RAM tiers of
  * c/cache.h for the routed experts; keyed by (layer, expert id)) ---- */
 typedef struct ApusHipStore ApusHipStore;
 /* Reserve n_layers x E experts of shape gate/up [inter, dim], down
- * [dim, inter] (MXFP4), laid out as one slab per expert in HBM. Returns
- * NULL (err filled) when HBM cannot hold it. */
+ * [dim, inter] (MXFP4), laid out as one slab per expert in HBM. When dim
+ * and inter are 2048 or 4096 the matrices are held in the MFMA-tiled layout
+ * of apus_hip_pack_weights_dev (apus_hip_store_tiled returns 1); otherwise
+ * row-major. Returns NULL (err filled) when HBM cannot hold it. */
 ApusHipStore *apus_hip_store_create(int n_layers, int E, int dim, int inter,
                                     char *err, size_t errcap);
 void     apus_hip_store_free(ApusHipStore *st);
@@ -208,13 +234,18 @@ uint64_t apus_hip_store_bytes(const ApusHipStore *st);
  * (layer, e) uses stream id ((layer * E + e) * 8 + t), t = 0..5 for
  * w1, w1s, w2, w2s, w3, w3s. */
 int      apus_hip_store_fill_random(ApusHipStore *st, uint64_t seed);
-/* Upload one expert from host memory (layout of c/st.h ApusFp4W). */
+/* Upload one expert from host memory (row-major, c/st.h ApusFp4W); packed
+ * into the store's layout. */
 int      apus_hip_store_put(ApusHipStore *st, int layer, int eid,
                             const ApusFp4W *w1, const ApusFp4W *w2,
                             const ApusFp4W *w3);
-/* Device pointers of one expert's six tensors (w1, w1s, w2, w2s, w3, w3s). */
+/* Device pointers of one expert's six tensors (w1, w1s, w2, w2s, w3, w3s),
+ * in the store's layout (apus_hip_unpack_weights_dev turns a tiled matrix
+ * back into the row-major form of c/st.h). */
 int      apus_hip_store_get(const ApusHipStore *st, int layer, int eid,
                             const uint8_t *ptrs[6]);
+/* 1 when the store holds its matrices MFMA-tiled. */
+int      apus_hip_store_tiled(const ApusHipStore *st);
 /* Workspace bytes for apus_hip_moe_routed_dev with s tokens x topk. */
 size_t   apus_hip_moe_workspace(const ApusHipStore *st, int s, int topk);
 /* Routed dispatch of one layer with everything in HBM: x [s, dim] f32,

@@ -149,3 +149,18 @@ def test_linear_rows_independent(hip, rng, fmt):
     for m in (0, 5):
         one = f(w, ws, x[m:m + 1].copy())
         assert np.array_equal(one.view(np.uint32), full[m:m + 1].view(np.uint32))
+
+
+def test_dense_cache_same_bytes_other_shape(hip, oracle, rng):
+    """The dense weight cache is keyed by host pointer; the same buffer
+    reused as a different (O, K) of equal size must not hit the copy laid out
+    for the first shape (resident copies are MFMA-tiled per shape)."""
+    w, ws = fp4_weights(rng, 2048, 4096)
+    x1 = acts(rng, 1, 4096)
+    got1 = hip.fp4_linear(w, ws, x1)
+    assert max_rel(got1, oracle.fp4_linear(w, ws, x1)) <= 1e-3 + 2.0 ** -8
+    w2, ws2 = w.reshape(4096, 1024), ws.reshape(4096, 64)      # same memory
+    assert w2.ctypes.data == w.ctypes.data and ws2.ctypes.data == ws.ctypes.data
+    x2 = acts(rng, 3, 2048)
+    got2 = hip.fp4_linear(w2, ws2, x2)
+    assert max_rel(got2, oracle.fp4_linear(w2, ws2, x2)) <= 1e-3 + 2.0 ** -8

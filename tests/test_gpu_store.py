@@ -41,12 +41,26 @@ def store(hip):
 
 
 def read_expert(hip, st, layer, e, dim, inter):
+    """The six tensors of an expert, row-major (unpacked when the store holds
+    them MFMA-tiled)."""
+    L = hip.lib()
     ptrs = (C.c_void_p * 6)()
-    hip._check(hip.lib().apus_hip_store_get(st, layer, e, ptrs), "store_get")
+    hip._check(L.apus_hip_store_get(st, layer, e, ptrs), "store_get")
+    shp = shapes(dim, inter)
+    srcs = list(ptrs)
+    tmp = []
+    if L.apus_hip_store_tiled(st):
+        for m, (O, K) in enumerate(((inter, dim), (dim, inter), (inter, dim))):
+            bw, bs = hip.DevBuf(int(np.prod(shp[2 * m]))), hip.DevBuf(int(np.prod(shp[2 * m + 1])))
+            hip._check(L.apus_hip_unpack_weights_dev(0, srcs[2 * m], srcs[2 * m + 1], bw.ptr, bs.ptr,
+                                                     O, K), "unpack")
+            srcs[2 * m], srcs[2 * m + 1] = bw.ptr, bs.ptr
+            tmp += [bw, bs]
+        hip._check(L.apus_hip_synchronize(), "sync")
     out = []
-    for p, shp in zip(ptrs, shapes(dim, inter)):
-        a = np.empty(shp, np.uint8)
-        hip._check(hip.lib().apus_hip_d2h(a.ctypes.data, p, a.nbytes), "d2h")
+    for p, sh in zip(srcs, shp):
+        a = np.empty(sh, np.uint8)
+        hip._check(L.apus_hip_d2h(a.ctypes.data, p, a.nbytes), "d2h")
         out.append(a)
     return tuple(out)
 
@@ -66,6 +80,20 @@ def test_store_fill_matches_host_generator(hip, oracle, store):
     for layer, e in ((0, 0), (1, 4), (0, 3)):
         dev = read_expert(hip, st, layer, e, dim, inter)
         host = host_expert(oracle, 11, layer, e, E, dim, inter)
+        for d, h in zip(dev, host):
+            assert np.array_equal(d, h)
+
+
+def test_store_fill_tiled_matches_host_generator(hip, oracle, store):
+    """dim, inter in {2048, 4096}: the store holds MFMA-tiled matrices whose
+    row-major form is the host generator's."""
+    L_, E, dim, inter = 1, 3, 2048, 4096
+    st = store(L_, E, dim, inter)
+    assert hip.lib().apus_hip_store_tiled(st) == 1
+    hip._check(hip.lib().apus_hip_store_fill_random(st, 12), "fill")
+    for e in (0, 2):
+        dev = read_expert(hip, st, 0, e, dim, inter)
+        host = host_expert(oracle, 12, 0, e, E, dim, inter)
         for d, h in zip(dev, host):
             assert np.array_equal(d, h)
 
