@@ -91,7 +91,7 @@ def timed_eager(H, launch, steps):
 
 # ------------------------------------------------------------------ config 0
 
-def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12):
+def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12, extras=True):
     """Config 0. A step is one M=1 expert GEMV (W [O, K] MXFP4) on its own weight
     copy (256 copies, 1.1 GB in rotation, so no cache level holds them).
     Measured three ways:
@@ -99,7 +99,10 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12):
                 (the decode MoE issues exactly this: gate+up of one token's 6
                 routed experts = 12 such GEMVs per launch) -> `value`;
       serial  : one launch per step, serialized on one stream (kernel duration);
-      lanes   : one launch per step, round-robin on 4 concurrent streams."""
+      lanes   : one launch per step, round-robin on 4 concurrent streams.
+    The grouped launch runs on MFMA-tiled weights (the layout the backend keeps
+    resident) for `value`; with extras, also on row-major weights. Without
+    extras only the tiled grouped launch runs (for a profile of that kernel)."""
     import ctypes as C
     L = H.lib()
     wbytes, sbytes = O * K // 2, O * K // 32
@@ -156,13 +159,23 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12):
                                            out.ptr + c * O * 4, 1, K, O, ws_lin.ptr), "linear")
 
     for i in range(warmup):
-        gemv(i)
-        grouped(i)
         grouped_tiled(i)
+        if extras:
+            gemv(i)
+            grouped(i)
     H.synchronize()
     launches = max(1, steps // group)
-    ms_group = timed_graph(H, grouped, launches)
     ms_tiled = timed_graph(H, grouped_tiled, launches)
+    gemv_bytes = wbytes + sbytes + K + (K // 128) * 4 + O * 4
+    gsteps = launches * group
+    res = {"steps_timed": gsteps, "group": group, "launches": launches, "bytes": gemv_bytes,
+           "launch_bytes": gemv_bytes * group, "flops": 2 * O * K,
+           "tiled_gbs": gemv_bytes * gsteps / (ms_tiled * 1e-3) / 1e9,
+           "tiled_launch_us": ms_tiled / launches * 1e3,
+           "tiled_ms_per_step": ms_tiled / gsteps}
+    if not extras:
+        return res
+    ms_group = timed_graph(H, grouped, launches)
     ms_serial = timed_graph(H, gemv, steps)
     ms_eager = timed_eager(H, gemv, steps)
     ms_lin = timed_graph(H, linear, steps)
@@ -179,26 +192,20 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12):
 
     ms_lanes = timed_graph(H, gemv_lanes, steps)
     # algorithmic bytes of one GEMV: weights + group scales + E4M3 codes + fp32
-    # act scales + fp32 outputs
-    gemv_bytes = wbytes + sbytes + K + (K // 128) * 4 + O * 4
-    # the linear additionally reads x in fp32 (it quantises in a separate launch)
+    # act scales + fp32 outputs; the linear reads x in fp32 instead of codes
     lin_bytes = wbytes + sbytes + K * 4 + O * 4
-    gsteps = launches * group
-    return {
-        "steps_timed": gsteps, "group": group, "launches": launches,
-        "ms_total": ms_group, "ms_per_step": ms_group / gsteps, "bytes": gemv_bytes,
+    res.update({
+        "ms_total": ms_group, "ms_per_step": ms_group / gsteps,
         "gbs": gemv_bytes * gsteps / (ms_group * 1e-3) / 1e9,
-        "launch_us": ms_group / launches * 1e3, "launch_bytes": gemv_bytes * group,
-        "tiled_gbs": gemv_bytes * gsteps / (ms_tiled * 1e-3) / 1e9,
-        "tiled_launch_us": ms_tiled / launches * 1e3,
+        "launch_us": ms_group / launches * 1e3,
         "serial_us": ms_serial / steps * 1e3,
         "serial_gbs": gemv_bytes * steps / (ms_serial * 1e-3) / 1e9,
         "lanes_gbs": gemv_bytes * steps / (ms_lanes * 1e-3) / 1e9,
         "eager_gbs": gemv_bytes * steps / (ms_eager * 1e-3) / 1e9,
         "linear_gbs": lin_bytes * steps / (ms_lin * 1e-3) / 1e9,
         "linear_us": ms_lin / steps * 1e3,
-        "flops": 2 * O * K,
-    }
+    })
+    return res
 
 
 # ------------------------------------------------------------------ config 1
@@ -210,6 +217,12 @@ def bench_fp8(H, dev, steps, O=4096, K=4096, copies=40):
     ws = dev.alloc(sbytes * copies)
     H._check(L.apus_hip_fill_random(w.ptr, wbytes * copies, 1, 1, 2), "fill w8")
     H._check(L.apus_hip_fill_random(ws.ptr, sbytes * copies, 1, 2, 3), "fill ws8")
+    # resident layout: MFMA-tiled (FP8 tile scales keep their layout)
+    tw = dev.alloc(wbytes * copies)
+    for c in range(copies):
+        H._check(L.apus_hip_pack_weights_dev(1, w.ptr + c * wbytes, None, tw.ptr + c * wbytes, None,
+                                             O, K), "pack w8")
+    w = tw
     res = {}
     for M in (1, 512):
         x = np.random.default_rng(1).standard_normal((M, K)).astype(np.float32)
@@ -222,7 +235,7 @@ def bench_fp8(H, dev, steps, O=4096, K=4096, copies=40):
             c = i % copies
             H._check(L.apus_hip_fp8_gemm_dev(w.ptr + c * wbytes, ws.ptr + c * sbytes, codes.ptr,
                                              scales.ptr, out.ptr + (i % 2) * M * O * 4, M, O, K,
-                                             0), "fp8 gemm")
+                                             H.W_TILED), "fp8 gemm")
 
         n = steps if M == 1 else max(10, steps // 10)
         for i in range(3):
@@ -308,6 +321,10 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
         wds = dev.alloc(dsb * L)
         H._check(L_.apus_hip_fill_random(wd.ptr, dbytes * L, 44, 1 << 40, 2), "fill fp8")
         H._check(L_.apus_hip_fill_random(wds.ptr, dsb * L, 44, (1 << 40) + 1, 3), "fill fp8 s")
+        wdt = dev.alloc(dbytes * L)            # resident layout: MFMA-tiled
+        for l in range(L):
+            H._check(L_.apus_hip_pack_weights_dev(1, wd.ptr + l * dbytes, None, wdt.ptr + l * dbytes,
+                                                  None, dim, dim), "pack fp8")
         H.synchronize()
         fill_s = time.perf_counter() - t0
         log(f"[bench] config 4: resident in {fill_s:.1f} s")
@@ -329,8 +346,8 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
 
         def step(t):
             for l in range(L):
-                H._check(L_.apus_hip_fp8_linear_dev(wd.ptr + l * dbytes, wds.ptr + l * dsb, dx.ptr,
-                                                    hd.ptr, 1, dim, dim, wlin.ptr), "fp8 linear")
+                H._check(L_.apus_hip_linear_dev(1 | H.W_TILED, wdt.ptr + l * dbytes, wds.ptr + l * dsb,
+                                                dx.ptr, hd.ptr, 1, dim, dim, wlin.ptr), "fp8 linear")
                 off = (t * L + l) * per
                 H._check(L_.apus_hip_moe_routed_dev(store, l, dx.ptr, didx.ptr + off,
                                                     dwgt.ptr + off, 1, topk, 10.0,
@@ -432,13 +449,15 @@ def main():
     g = None
     if want("gemv"):
         log(f"[bench] config 0 MXFP4 GEMV: {args.warmup} warmup, {args.steps} timed steps")
-        g = bench_fp4_gemv(H, dev, args.steps, args.warmup)
-        extras["config0_single_launch_serial_GBs"] = round(g["serial_gbs"], 1)
-        extras["config0_single_launch_us"] = round(g["serial_us"], 3)
-        extras["config0_single_launch_4lanes_GBs"] = round(g["lanes_gbs"], 1)
-        extras["config0_linear_GBs"] = round(g["linear_gbs"], 1)
-        extras["config0_linear_us"] = round(g["linear_us"], 3)
-        extras["config0_eager_launch_GBs"] = round(g["eager_gbs"], 1)
+        g = bench_fp4_gemv(H, dev, args.steps, args.warmup, extras=not args.skip_extras)
+        if not args.skip_extras:
+            extras["config0_rowmajor_grouped_GBs"] = round(g["gbs"], 1)
+            extras["config0_single_launch_serial_GBs"] = round(g["serial_gbs"], 1)
+            extras["config0_single_launch_us"] = round(g["serial_us"], 3)
+            extras["config0_single_launch_4lanes_GBs"] = round(g["lanes_gbs"], 1)
+            extras["config0_linear_GBs"] = round(g["linear_gbs"], 1)
+            extras["config0_linear_us"] = round(g["linear_us"], 3)
+            extras["config0_eager_launch_GBs"] = round(g["eager_gbs"], 1)
     if not args.skip_extras and want("fp8"):
         log("[bench] config 1 FP8 GEMV/GEMM")
         f8 = bench_fp8(H, dev, min(args.steps, 512))
@@ -501,12 +520,12 @@ def main():
         return
     line = {
         "metric": METRIC,
-        "value": round(g["gbs"], 2),
+        "value": round(g["tiled_gbs"], 2),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": g["steps_timed"],
         "warmup": args.warmup,
-        "ms_per_step": g["ms_per_step"],
+        "ms_per_step": g["tiled_ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -516,18 +535,21 @@ def main():
         "config": {"workload": "config 0: MXFP4 expert GEMV O=2048 K=4096 M=1 (one step = one "
                                "GEMV on its own HBM-resident weight copy, 256 copies in "
                                f"rotation), {g['group']} steps per grouped launch as the decode "
-                               "MoE issues them (gate+up of one token's 6 routed experts)",
+                               "MoE issues them (gate+up of one token's 6 routed experts); "
+                               "weights in the MFMA-tiled layout the backend's caches and "
+                               "expert store keep them in",
                    "group": g["group"], "launches": g["launches"],
-                   "hbm_frac": round(g["gbs"] / HBM_PEAK_GBS, 4)},
+                   "hbm_frac": round(g["tiled_gbs"] / HBM_PEAK_GBS, 4),
+                   },
         # the dominant kernel is the grouped GEMM launch; launches are
         # serialized on one stream, so per-launch time = kernel duration plus
         # the graph's inter-kernel gap (compare rocprofv3's average)
         "roofline": {"bound": "hbm",
-                     "achieved": round(g["launch_bytes"] / (g["launch_us"] * 1e-6) / 1e9, 2),
+                     "achieved": round(g["launch_bytes"] / (g["tiled_launch_us"] * 1e-6) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(g["launch_bytes"] / (g["launch_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "kernel": "apus_gemm_decode_kernel (grouped, 12 GEMVs)",
-                     "launch_us": round(g["launch_us"], 3), "bytes_per_launch": g["launch_bytes"],
+                     "frac": round(g["launch_bytes"] / (g["tiled_launch_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "kernel": "apus_gemm_decode_kernel (grouped, 12 GEMVs, tiled weights)",
+                     "launch_us": round(g["tiled_launch_us"], 3), "bytes_per_launch": g["launch_bytes"],
                      "traffic": CONFIG0_TRAFFIC_BYTES},
         "cpu_baseline": cpu,
         "extras": extras,
