@@ -36,7 +36,7 @@ METRIC = "MXFP4 expert GEMV GB/s (%HBM peak) @M=1; MoE grouped-GEMM TFLOP/s @512
 # HBM bytes per grouped 12-GEMV launch measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (FETCH scaled x2.0 from a 256 MiB copy calibration); command and
 # counts in profiles/config0_mxfp4_gemv_m1.txt. Re-measure when the kernel changes.
-CONFIG0_TRAFFIC_BYTES = 56300452
+CONFIG0_TRAFFIC_BYTES = 53728315
 
 
 def log(*a):
@@ -429,6 +429,8 @@ def main():
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list: gemv,fp8,decode,prefill,full")
+    ap.add_argument("--full-layers", type=int, default=43,
+                    help="config 4: resident MoE layers (43 fill ~148 GB)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -494,7 +496,7 @@ def main():
         H.lib().apus_hip_store_free(store)
     if not args.skip_extras and want("full"):
         log("[bench] config 4 full-footprint decode")
-        f = bench_full_footprint(H, dev)
+        f = bench_full_footprint(H, dev, L=args.full_layers)
         extras.update({"config4_tok_s": round(f["tok_s"], 1),
                        "config4_ms_per_token": round(f["ms_per_token"], 3),
                        "config4_GBs": round(f["gbs"], 1),
