@@ -360,19 +360,59 @@ int moe_pair_max() {
 
 /* the routed-dispatch pipeline on device data; tab = 6 device arrays of E
  * pointers (w1, w1s, w2, w2s, w3, w3s) */
+/* regularly spaced expert slabs (an expert store layer): tensor i of expert
+ * e at base + e * stride + off[i], i = w1, w1s, w2, w2s, w3, w3s */
+struct MoeSlab {
+    const uint8_t *base;
+    size_t stride, off[6];
+};
+
 int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
                  const float *x, const int32_t *idx, const float *wgt, int s,
-                 int topk, float *y, const MoeWs &w, bool wtiled, hipStream_t st) {
+                 int topk, float *y, const MoeWs &w, bool wtiled, const MoeSlab *slab,
+                 hipStream_t st) {
     const int nj = s * topk;
     ApusExpertTable t;
     t.w1 = tab; t.w1s = tab + E; t.w2 = tab + 2 * E; t.w2s = tab + 3 * E;
     t.w3 = tab + 4 * E; t.w3s = tab + 5 * E;
-    /* few pairs (decode): one launch entry per routed pair and matrix, no
-     * sorting pass. w1/w3 quantise x while staging, w2 computes and
-     * quantises h = swiglu(g, u) while staging and accumulates y in
-     * (t, j) order in its last workgroup per column tile: three launches */
-    if (nj <= moe_pair_max() && (dim == 2048 || dim == 4096) &&
-        (inter == 2048 || inter == 4096)) {
+    const bool pair_shape = nj <= moe_pair_max() && (dim == 2048 || dim == 4096) &&
+                            (inter == 2048 || inter == 4096);
+    /* few pairs (decode), topk 6 or 8: two launches, no sorting pass. w1/w3
+     * per (16 rows, pair) with SwiGLU in the epilogue -> h rows; w2 per 16
+     * output columns over each token's pairs, accumulating y in (t, j) order
+     * inside the workgroup */
+    if (pair_shape && (topk == 6 || topk == 8)) {
+        ApusGemmArgs a{};
+        a.wtiled = wtiled;
+        a.O = inter; a.K = dim; a.ldo = inter;
+        a.ax = x; a.limit = limit;
+        a.pidx = idx; a.adiv = topk; a.pE = E;
+        a.pw[0] = t.w1; a.pws[0] = t.w1s; a.pw[1] = t.w3; a.pws[1] = t.w3s;
+        if (slab) {
+            a.pbase = slab->base; a.pstride = slab->stride;
+            a.pwoff[0] = slab->off[0]; a.psoff[0] = slab->off[1];
+            a.pwoff[1] = slab->off[4]; a.psoff[1] = slab->off[5];
+        }
+        a.pout[0] = w.gm;                           /* h rows [nj, inter] */
+        if (!launched(apus_launch_moe_pair13(&a, nj, st), "pair w1/w3")) return 1;
+        ApusGemmArgs b{};
+        b.wtiled = wtiled;
+        b.O = dim; b.K = inter; b.ldo = dim;
+        b.ax = w.gm;
+        b.pidx = idx; b.pE = E;
+        b.pw[0] = t.w2; b.pws[0] = t.w2s;
+        if (slab) {
+            b.pbase = slab->base; b.pstride = slab->stride;
+            b.pwoff[0] = slab->off[2]; b.psoff[0] = slab->off[3];
+        }
+        b.acc_w = wgt; b.acc_y = y; b.acc_topk = topk; b.acc_s = s;
+        return launched(apus_launch_moe_pair2(&b, st), "pair w2") ? 0 : 1;
+    }
+    /* few pairs, other topk: one launch entry per routed pair and matrix.
+     * w1/w3 quantise x while staging, w2 computes and quantises h = swiglu(g,
+     * u) while staging and accumulates y in (t, j) order in its last
+     * workgroup per column tile: two launches */
+    if (pair_shape) {
         ApusGemmArgs a{};
         a.wtiled = wtiled;
         a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
@@ -644,7 +684,7 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
         return 1;
     const bool etiled = moe_tiled(dim, inter);
     if (moe_pipeline(E, dim, inter, w->limit, mw.tab, dx, didx, dwgt, s, topk, dy, mw, etiled,
-                     g.stream))
+                     nullptr, g.stream))
         return 1;
     if (!download(y, dy, (size_t)s * dim * 4) || !finish()) return 1;
     return 0;
@@ -892,8 +932,11 @@ int apus_hip_moe_routed_dev(const ApusHipStore *st, int layer, const float *x, c
         return 1;
     }
     MoeWs mw = moe_carve(workspace, s, topk, st->E, st->dim, st->inter);
+    MoeSlab slab{st->layer_base[layer], st->expert_bytes, {}};
+    size_t off = 0;
+    for (int i = 0; i < 6; i++) { slab.off[i] = off; off += align256(st->sz[i]); }
     return moe_pipeline(st->E, st->dim, st->inter, limit, st->layer_tab[layer], x, idx, wgt, s,
-                        topk, y, mw, st->tiled, dev_stream());
+                        topk, y, mw, st->tiled, &slab, dev_stream());
 }
 
 /* --------------------------------------------------------------- helpers */

@@ -333,6 +333,20 @@ __device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const ApusWLa
     }
 }
 
+/* weights of matrix slot `mat` of expert e: computed from a regular slab
+ * layout, or read from the pointer tables */
+__device__ __forceinline__ void apus_expert_ptrs(const ApusGemmArgs &a, int mat, int e,
+                                                 const uint8_t *&w, const uint8_t *&ws) {
+    if (a.pbase) {
+        const uint8_t *b = a.pbase + (size_t)e * a.pstride;
+        w = b + (mat ? a.pwoff[1] : a.pwoff[0]);
+        ws = b + (mat ? a.psoff[1] : a.psoff[0]);
+    } else {
+        w = apus_gld<const uint8_t *>((mat ? a.pw[1] : a.pw[0]) + e);
+        ws = apus_gld<const uint8_t *>((mat ? a.pws[1] : a.pws[0]) + e);
+    }
+}
+
 /* the entry of launch row y: table, routed pair, or the single entry */
 __device__ __forceinline__ ApusGemmEnt apus_entry_of(const ApusGemmArgs &a, int y) {
     if (a.ents) return apus_gld<ApusGemmEnt>(a.ents + y);
@@ -342,8 +356,7 @@ __device__ __forceinline__ ApusGemmEnt apus_entry_of(const ApusGemmArgs &a, int 
     const int e = apus_gld<int>(a.pidx + p);
     const bool ok = (unsigned)e < (unsigned)a.pE;
     const int ee = ok ? e : 0;
-    ent.w = apus_gld<const uint8_t *>((mat ? a.pw[1] : a.pw[0]) + ee);
-    ent.ws = apus_gld<const uint8_t *>((mat ? a.pws[1] : a.pws[0]) + ee);
+    apus_expert_ptrs(a, mat, ee, ent.w, ent.ws);
     ent.out = mat ? a.pout[1] : a.pout[0];
     ent.arows = nullptr; ent.orows = nullptr;
     ent.a0 = p / a.adiv; ent.o0 = p; ent.M = ok ? 1 : 0; ent.pad = 0;
@@ -898,6 +911,202 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
             }
         }
     }
+}
+
+/*
+ * One-token MoE dispatch kernels (few routed pairs, MXFP4 experts).
+ *
+ * w1/w3 (apus_moe_pair13_kernel): a workgroup owns 16 rows of inter for one
+ * pair. Waves 0-1 run w1, waves 2-3 w3, each pair of waves splitting K in
+ * halves (added in part order, as the few-row schedule with 2 K parts); the
+ * pair's x row is quantised once while staging. The epilogue meets g and u
+ * in LDS and writes h = swiglu(bf16 g, bf16 u) (c/moe.h:113-126, :198-209).
+ *
+ * w2 (apus_moe_pair2_kernel): a workgroup owns 16 columns of dim and, token by
+ * token, multiplies the token's NP = topk staged h rows against their experts'
+ * weights; the 4 waves split K in quarters and their partial sums meet in LDS
+ * (added in part order), then y[t, o] = sum_j wgt * bf16(eo_j) in j order
+ * (c/moe.h:148-158, :447-449). The weight ring runs across the pairs, so the
+ * whole tile's weights are in flight at once; nothing leaves the workgroup but y.
+ */
+template <int NS>
+__global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args) {
+    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16, NSW = NS / 2;
+    constexpr int PD = NSW < 3 ? NSW : 3;
+    __shared__ __align__(16) uint8_t lcodes[LDK];
+    __shared__ uint8_t lsc[NQ];
+    __shared__ apus_v4f lred[2][64];
+    __shared__ float lu[16];
+    if (args.zero && blockIdx.y == 0) {
+        for (int i = blockIdx.x * 256 + threadIdx.x; i < args.nzero; i += gridDim.x * 256)
+            args.zero[i] = 0u;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int mat = wave >> 1, kpart = wave & 1;
+    const int p = blockIdx.y;
+    const int o = blockIdx.x * 16 + r;
+    /* the pair's x row: its loads go out first */
+    ApusStageRaw<APUS_A_F32> raw;
+    apus_stage_load<K, APUS_A_F32>(args, nullptr, p / args.adiv, 0, 1, 0, raw);
+    const int e = apus_gld<int>(args.pidx + p);
+    const bool ok = (unsigned)e < (unsigned)args.pE;
+    ApusGemmEnt ent;
+    apus_expert_ptrs(args, mat, ok ? e : 0, ent.w, ent.ws);
+    const ApusWLane wl = apus_wlane<APUS_W_FP4>(ent, args.wtiled, o, lane, K);
+    const int sbase = kpart * NSW;
+    ApusBFrag<APUS_W_FP4> ring[PD];
+#pragma unroll
+    for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl, sbase + u);
+    apus_stage_quant<K, APUS_A_F32>(args, raw, lcodes, lsc);
+    apus_lds_barrier();
+    /* A row 0 is the pair's x; the other 15 rows are zero */
+    const int z = r == 0 ? -1 : 0;
+    const uint8_t *arow = lcodes + g * 16;
+    apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int si = 0; si < NSW; ++si) {
+        const int s = sbase + si;
+        ApusBFrag<APUS_W_FP4> &cur = ring[si % PD];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int q = s * 4 + st;
+            const uint4 a0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
+            const uint4 a1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+            const apus_v8i a = apus_v8i{(int)a0.x & z, (int)a0.y & z, (int)a0.z & z, (int)a0.w & z,
+                                        (int)a1.x & z, (int)a1.y & z, (int)a1.z & z, (int)a1.w & z};
+            const apus_v4u w = cur.w[st][0];
+            const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+            const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+            acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, (int)lsc[q], sb);
+        }
+        if (si + PD < NSW) apus_load_b_full<APUS_W_FP4>(cur, wl, s + PD);
+    }
+    if (kpart == 1) lred[mat][lane] = acc;
+    __syncthreads();
+    if (kpart == 0) acc += lred[mat][lane];
+    /* lane (g 0, r) holds D[0][r]: this pair, inter column o */
+    if (wave == 2 && g == 0) lu[r] = apus_bf16_rne(acc[0]);
+    __syncthreads();
+    if (wave == 0 && g == 0) {
+        const float h = ok ? apus_swiglu_h(apus_bf16_rne(acc[0]), lu[r], args.limit) : 0.0f;
+        apus_gst<float>(args.pout[0] + (size_t)p * args.O + o, h);
+    }
+}
+
+template <int NS, int NP>
+__global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) {
+    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16, KS = 4, NSW = NS / KS;
+    constexpr int STEPS = NP * NSW, PD = STEPS < 6 ? STEPS : (NSW == 1 ? 6 : 4);
+    static_assert(NS % KS == 0 && NP <= 8, "pair2 shape");
+    __shared__ __align__(16) uint8_t lcodes[NP * LDK];
+    __shared__ uint8_t lsc[NP * NQ];
+    __shared__ float lred[KS][NP][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int kpart = wave;
+    const int o = blockIdx.x * 16 + r;
+    const int sbase = kpart * NSW;
+    for (int t = 0; t < args.acc_s; ++t) {
+        const int p0 = t * NP;
+        apus_lds_barrier();                 /* the previous token's LDS readers are done */
+        /* the token's NP h rows: first pass's loads before the expert lookups */
+        ApusStageRaw<APUS_A_F32> raw0;
+        apus_stage_load<K, APUS_A_F32>(args, nullptr, p0, 0, NP, 0, raw0);
+        ApusWLane wl[NP];
+        bool okj[NP];
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            const int e = apus_gld<int>(args.pidx + p0 + j);
+            okj[j] = (unsigned)e < (unsigned)args.pE;
+            ApusGemmEnt ent;
+            apus_expert_ptrs(args, 0, okj[j] ? e : 0, ent.w, ent.ws);
+            wl[j] = apus_wlane<APUS_W_FP4>(ent, args.wtiled, o, lane, K);
+        }
+        ApusBFrag<APUS_W_FP4> ring[PD];
+#pragma unroll
+        for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl[u / NSW], sbase + u % NSW);
+        apus_stage_quant<K, APUS_A_F32>(args, raw0, lcodes, lsc);
+        constexpr int PASSES = (NP * NQ + 31) / 32;
+#pragma unroll
+        for (int pass = 1; pass < PASSES; ++pass) {
+            ApusStageRaw<APUS_A_F32> rp;
+            apus_stage_load<K, APUS_A_F32>(args, nullptr, p0, 0, NP, pass, rp);
+            apus_stage_quant<K, APUS_A_F32>(args, rp, lcodes, lsc);
+        }
+        apus_lds_barrier();
+        apus_v4f acc[NP];
+#pragma unroll
+        for (int j = 0; j < NP; ++j) acc[j] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int stp = 0; stp < STEPS; ++stp) {
+            const int j = stp / NSW, s = sbase + stp % NSW;
+            ApusBFrag<APUS_W_FP4> &cur = ring[stp % PD];
+            /* A row j is pair j's h; the other rows are zero */
+            const int z = r == j ? -1 : 0;
+            const uint8_t *arow = lcodes + j * LDK + g * 16;
+            const uint8_t *asr = lsc + j * NQ;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int q = s * 4 + st;
+                const uint4 a0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
+                const uint4 a1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+                const apus_v8i a = apus_v8i{(int)a0.x & z, (int)a0.y & z, (int)a0.z & z, (int)a0.w & z,
+                                            (int)a1.x & z, (int)a1.y & z, (int)a1.z & z, (int)a1.w & z};
+                const apus_v4u w = cur.w[st][0];
+                const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                acc[j] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[j], (int)asr[q], sb);
+            }
+            if (stp + PD < STEPS)
+                apus_load_b_full<APUS_W_FP4>(cur, wl[(stp + PD) / NSW], sbase + (stp + PD) % NSW);
+        }
+        /* pair j's result sits in D[j][r]: lane (g = j / 4, r), element j % 4.
+         * Every lane stores (the reader picks the right lane): a store under a
+         * lane-dependent condition would be the only consumer of the MFMA
+         * results, and the compiler then sinks the MFMAs into the narrowed-EXEC
+         * region, where a matrix instruction does not see the inactive lanes */
+#pragma unroll
+        for (int j = 0; j < NP; ++j) lred[kpart][j][lane] = acc[j][j & 3];
+        __syncthreads();
+        if (threadIdx.x < 16) {
+            float y = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NP; ++j) {
+                const int src = (j >> 2) * 16 + threadIdx.x;
+                float eo = lred[0][j][src];
+#pragma unroll
+                for (int kp = 1; kp < KS; ++kp) eo += lred[kp][j][src];
+                eo = okj[j] ? apus_bf16_rne(eo) : 0.0f;
+                y = __fadd_rn(y, __fmul_rn(apus_gld<float>(args.acc_w + p0 + j), eo));
+            }
+            apus_gst<float>(args.acc_y + (size_t)t * args.ldo + blockIdx.x * 16 + threadIdx.x, y);
+        }
+    }
+}
+
+hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t st) {
+    if (npairs <= 0) return hipSuccess;
+    if ((a->K != 2048 && a->K != 4096) || a->O % 16) return hipErrorInvalidValue;
+    dim3 grid(a->O / 16, npairs), block(256);
+    if (a->K == 4096) hipLaunchKernelGGL(apus_moe_pair13_kernel<8>, grid, block, 0, st, *a);
+    else              hipLaunchKernelGGL(apus_moe_pair13_kernel<4>, grid, block, 0, st, *a);
+    return hipGetLastError();
+}
+
+hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
+    if (a->acc_s <= 0) return hipSuccess;
+    if ((a->K != 2048 && a->K != 4096) || a->O % 16 || (a->acc_topk != 6 && a->acc_topk != 8))
+        return hipErrorInvalidValue;
+    dim3 grid(a->O / 16), block(256);
+    if (a->K == 4096) {
+        if (a->acc_topk == 6) hipLaunchKernelGGL((apus_moe_pair2_kernel<8, 6>), grid, block, 0, st, *a);
+        else                  hipLaunchKernelGGL((apus_moe_pair2_kernel<8, 8>), grid, block, 0, st, *a);
+    } else {
+        if (a->acc_topk == 6) hipLaunchKernelGGL((apus_moe_pair2_kernel<4, 6>), grid, block, 0, st, *a);
+        else                  hipLaunchKernelGGL((apus_moe_pair2_kernel<4, 8>), grid, block, 0, st, *a);
+    }
+    return hipGetLastError();
 }
 
 namespace {

@@ -53,6 +53,11 @@ typedef struct {
     const uint8_t *const *pw[2];
     const uint8_t *const *pws[2];
     float *pout[2];
+    /* regularly spaced expert slabs (an expert store layer): when pbase is
+     * set, W = pbase + e * pstride + pwoff[mat] and scales at psoff[mat]
+     * instead of the pointer tables (one dependent load fewer) */
+    const uint8_t *pbase;
+    size_t pstride, pwoff[2], psoff[2];
     /* fused (t, j)-ordered accumulation (pair entries, nmat 1): after every
      * workgroup of a column tile has written its outputs, the last one adds
      * y[t, o] = sum_j acc_w[t*acc_topk + j] * out[t*acc_topk + j, o] over
@@ -67,6 +72,19 @@ typedef struct {
 } ApusGemmArgs;
 
 enum { APUS_A_CODES = 0, APUS_A_F32 = 1, APUS_A_SWIGLU = 2 };
+
+/* One-token-chunk MoE dispatch for few routed pairs (decode), MXFP4 experts
+ * with dim and inter in {2048, 4096}, topk 6 or 8, in two launches:
+ *  w1/w3: one workgroup per (16 rows of inter, pair): h = swiglu(bf16(w1 x),
+ *         bf16(w3 x)) written as fp32 rows of pout[0] [s*topk, inter]; x rows
+ *         quantised while staging; zero, nzero cleared.
+ *  w2:    one workgroup per 16 columns of dim, looping over the tokens and
+ *         their topk pairs: y[t] = sum_j acc_w[t*topk+j] * bf16(w2_j h_j).
+ * Fields used: ax (x or h), pidx, pE, adiv (= topk), pw/pws or pbase/pstride/
+ * pwoff/psoff, limit, acc_w/acc_y/acc_s/acc_topk, O, K, ldo, wtiled.
+ * Returns hipErrorInvalidValue for other shapes. */
+hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t st);
+hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st);
 
 /* The few-row schedule for every entry (each entry's M is computed in
  * chunks of up to `rows` rows; rows 1 or 8), with the activation source,
