@@ -1146,8 +1146,11 @@ void apus_launch_dec_k(const ApusGemmArgs &d, int n_ent, int ks, hipStream_t st)
     }
 }
 
-/* waves per 16-row tile: small launches split K for more weight streams;
- * APUS_HIP_DEC_KS (1, 2, 4) overrides */
+/* waves per 16-row tile: the smallest K split that still gives about one
+ * wave per SIMD (1024 on 256 CUs); measured on gfx950, whole-K waves stream
+ * best once there are enough of them (12 x 2048-row GEMVs: KS 1 10.8 us, KS 2
+ * 13.2 us) and small launches need the split (one 4096-row FP8 GEMV: KS 4
+ * 6.3 us, KS 1 8.8 us). APUS_HIP_DEC_KS (1, 2, 4) overrides. */
 int apus_dec_ks(size_t row_tiles) {
     static const int forced = [] {
         const char *e = getenv("APUS_HIP_DEC_KS");
@@ -1155,7 +1158,7 @@ int apus_dec_ks(size_t row_tiles) {
         return (v == 1 || v == 2 || v == 4) ? v : 0;
     }();
     if (forced) return forced;
-    return row_tiles < 1024 ? 4 : row_tiles < 2048 ? 2 : 1;
+    return row_tiles >= 1024 ? 1 : row_tiles >= 512 ? 2 : 4;
 }
 
 }  // namespace
