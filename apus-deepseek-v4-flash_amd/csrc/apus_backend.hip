@@ -57,6 +57,7 @@ struct DenseW {        /* one cached dense weight (codes/packed + scales) */
 struct ExpertW {       /* one cached routed expert, six tensors */
     uint8_t *p[6];
     size_t bytes;
+    int dim, inter;    /* a (layer, id) reused with another shape is re-uploaded */
     bool tiled;
 };
 
@@ -631,6 +632,13 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
         if (tab[e]) continue;
         const uint64_t key = ((uint64_t)(uint32_t)w->layer_id << 32) | (uint32_t)e;
         auto it = g.experts.find(key);
+        if (it != g.experts.end() && (it->second.dim != dim || it->second.inter != inter)) {
+            (void)hipStreamSynchronize(g.stream);
+            (void)hipFree(it->second.p[0]);
+            g.bytes_resident -= it->second.bytes;
+            g.experts.erase(it);
+            it = g.experts.end();
+        }
         if (it == g.experts.end()) {
             ApusFp4W r1, r2, r3;
             if (w->hook_resolve) {
@@ -654,6 +662,8 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
             }
             /* w1, w3: [inter, dim]; w2: [dim, inter] */
             const int mo[3] = {inter, dim, inter}, mk[3] = {dim, inter, dim};
+            ew.dim = dim;
+            ew.inter = inter;
             ew.tiled = moe_tiled(dim, inter);
             for (int m = 0; m < 3; m++) {
                 if (!upload_weights(APUS_W_FP4, ew.p[2 * m], ew.p[2 * m + 1], src[2 * m],

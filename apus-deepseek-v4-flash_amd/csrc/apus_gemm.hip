@@ -916,11 +916,11 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
 /*
  * One-token MoE dispatch kernels (few routed pairs, MXFP4 experts).
  *
- * w1/w3 (apus_moe_pair13_kernel): a workgroup owns 16 rows of inter for one
- * pair. Waves 0-1 run w1, waves 2-3 w3, each pair of waves splitting K in
- * halves (added in part order, as the few-row schedule with 2 K parts); the
- * pair's x row is quantised once while staging. The epilogue meets g and u
- * in LDS and writes h = swiglu(bf16 g, bf16 u) (c/moe.h:113-126, :198-209).
+ * w1/w3 (apus_moe_pair13_kernel): a workgroup owns 32 rows of inter for one
+ * pair; each wave streams one 16-row tile of w1 or w3 over the whole K (one
+ * accumulation chain, as the few-row schedule without a K split); the pair's
+ * x row is quantised once while staging. The epilogue meets g and u in LDS
+ * and writes h = swiglu(bf16 g, bf16 u) (c/moe.h:113-126, :198-209).
  *
  * w2 (apus_moe_pair2_kernel): a workgroup owns 16 columns of dim and, token by
  * token, multiplies the token's NP = topk staged h rows against their experts'
@@ -931,21 +931,21 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
  */
 template <int NS>
 __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args) {
-    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16, NSW = NS / 2;
-    constexpr int PD = NSW < 3 ? NSW : 3;
+    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16;
+    constexpr int PD = 3;
     __shared__ __align__(16) uint8_t lcodes[LDK];
     __shared__ uint8_t lsc[NQ];
-    __shared__ apus_v4f lred[2][64];
-    __shared__ float lu[16];
+    __shared__ float lgu[2][2][64];            /* [mat][tile][lane] */
     if (args.zero && blockIdx.y == 0) {
         for (int i = blockIdx.x * 256 + threadIdx.x; i < args.nzero; i += gridDim.x * 256)
             args.zero[i] = 0u;
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int mat = wave >> 1, kpart = wave & 1;
+    /* wave = 2 * tile + mat: two 16-row tiles of inter, w1 and w3 each, whole K */
+    const int mat = wave & 1, tile = wave >> 1;
     const int p = blockIdx.y;
-    const int o = blockIdx.x * 16 + r;
+    const int o = blockIdx.x * 32 + tile * 16 + r;
     /* the pair's x row: its loads go out first */
     ApusStageRaw<APUS_A_F32> raw;
     apus_stage_load<K, APUS_A_F32>(args, nullptr, p / args.adiv, 0, 1, 0, raw);
@@ -954,10 +954,9 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
     ApusGemmEnt ent;
     apus_expert_ptrs(args, mat, ok ? e : 0, ent.w, ent.ws);
     const ApusWLane wl = apus_wlane<APUS_W_FP4>(ent, args.wtiled, o, lane, K);
-    const int sbase = kpart * NSW;
     ApusBFrag<APUS_W_FP4> ring[PD];
 #pragma unroll
-    for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl, sbase + u);
+    for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl, u);
     apus_stage_quant<K, APUS_A_F32>(args, raw, lcodes, lsc);
     apus_lds_barrier();
     /* A row 0 is the pair's x; the other 15 rows are zero */
@@ -965,9 +964,8 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
     const uint8_t *arow = lcodes + g * 16;
     apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int si = 0; si < NSW; ++si) {
-        const int s = sbase + si;
-        ApusBFrag<APUS_W_FP4> &cur = ring[si % PD];
+    for (int s = 0; s < NS; ++s) {
+        ApusBFrag<APUS_W_FP4> &cur = ring[s % PD];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             const int q = s * 4 + st;
@@ -980,17 +978,18 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
             const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
             acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, (int)lsc[q], sb);
         }
-        if (si + PD < NSW) apus_load_b_full<APUS_W_FP4>(cur, wl, s + PD);
+        if (s + PD < NS) apus_load_b_full<APUS_W_FP4>(cur, wl, s + PD);
     }
-    if (kpart == 1) lred[mat][lane] = acc;
+    /* lane (g 0, r) holds D[0][r]: this pair, inter column o. Every lane
+     * stores its element (a lane-dependent store as the only consumer of the
+     * MFMA results would pull them into a narrowed EXEC); 32 threads then
+     * pick the g == 0 lanes of the w1 and w3 waves */
+    lgu[mat][tile][lane] = apus_bf16_rne(acc[0]);
     __syncthreads();
-    if (kpart == 0) acc += lred[mat][lane];
-    /* lane (g 0, r) holds D[0][r]: this pair, inter column o */
-    if (wave == 2 && g == 0) lu[r] = apus_bf16_rne(acc[0]);
-    __syncthreads();
-    if (wave == 0 && g == 0) {
-        const float h = ok ? apus_swiglu_h(apus_bf16_rne(acc[0]), lu[r], args.limit) : 0.0f;
-        apus_gst<float>(args.pout[0] + (size_t)p * args.O + o, h);
+    if (threadIdx.x < 32) {
+        const int t = threadIdx.x >> 4, rr = threadIdx.x & 15;
+        const float h = ok ? apus_swiglu_h(lgu[0][t][rr], lgu[1][t][rr], args.limit) : 0.0f;
+        apus_gst<float>(args.pout[0] + (size_t)p * args.O + blockIdx.x * 32 + t * 16 + rr, h);
     }
 }
 
@@ -1087,8 +1086,8 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
 
 hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t st) {
     if (npairs <= 0) return hipSuccess;
-    if ((a->K != 2048 && a->K != 4096) || a->O % 16) return hipErrorInvalidValue;
-    dim3 grid(a->O / 16, npairs), block(256);
+    if ((a->K != 2048 && a->K != 4096) || a->O % 32) return hipErrorInvalidValue;
+    dim3 grid(a->O / 32, npairs), block(256);
     if (a->K == 4096) hipLaunchKernelGGL(apus_moe_pair13_kernel<8>, grid, block, 0, st, *a);
     else              hipLaunchKernelGGL(apus_moe_pair13_kernel<4>, grid, block, 0, st, *a);
     return hipGetLastError();

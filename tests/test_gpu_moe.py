@@ -176,3 +176,16 @@ def test_grouped_dev_schedules(hip, oracle, rng, wfmt, K, Ms):
             want = f(w, ws, c[m0:m0 + M].copy(), s[m0:m0 + M].copy())
             assert max_rel(outs[i], want) <= 1e-3, (i, M)
         m0 += M
+
+
+def test_moe_routed_same_layer_id_other_shape(hip, oracle, rng):
+    """The expert cache is keyed by (layer_id, expert id); a layer id reused
+    with another shape must not return the experts cached for the first one."""
+    E, topk = 16, 6
+    for dim, inter in ((4096, 2048), (2048, 4096)):
+        experts = moe_experts(rng, E, dim, inter)
+        x = acts(rng, 1, dim)
+        idx, wgt = topk_routing(rng, 1, E, topk)
+        want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
+        got = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=4242)
+        assert max_rel(got, want) <= 2.0 ** -7, (dim, inter)
