@@ -315,10 +315,15 @@ struct MoeWs {
     float *gm, *um; uint8_t *hc; float *hs; float *eo;
     uint8_t **tab;
     unsigned *tickets;   /* one per 16 output columns of w2 */
+    int2 *items13, *items2;   /* many-row work lists */
+    int n_items;
     size_t total;
 };
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+/* experts with at most this many routed pairs take the few-row schedule */
+constexpr int MOE_SMALL = 8;
 
 MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
     MoeWs w{};
@@ -334,6 +339,9 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
     size_t o_eo = take(nj * dim * 4);
     size_t o_tab = take(6 * (size_t)E * sizeof(void *));
     size_t o_tk = take((size_t)(dim / 16) * sizeof(unsigned));
+    const int n_items = apus_moe_items_bound((int)nj, E, MOE_SMALL);
+    size_t o_i13 = take(2 * (size_t)n_items * sizeof(int2)), o_i2 = take((size_t)n_items * sizeof(int2));
+    w.n_items = n_items;
     w.total = off;
     if (base) {
         uint8_t *b = (uint8_t *)base;
@@ -345,6 +353,8 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
         w.hc = b + o_hc; w.hs = (float *)(b + o_hs); w.eo = (float *)(b + o_eo);
         w.tab = (uint8_t **)(b + o_tab);
         w.tickets = (unsigned *)(b + o_tk);
+        w.items13 = (int2 *)(b + o_i13);
+        w.items2 = (int2 *)(b + o_i2);
     }
     return w;
 }
@@ -436,11 +446,12 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
     /* experts with at most SMALL pairs take the few-row GEMM schedule; at
      * most min(E, nj) experts are small and at most nj / (SMALL + 1) are
      * large, so the launches cover only that many table slots */
-    constexpr int SMALL = 8;
+    constexpr int SMALL = MOE_SMALL;
     if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, w.xc, w.xs, st), "act_quant"))
         return 1;
     if (!launched(apus_launch_moe_route(idx, nj, topk, E, t, w.gm, w.um, w.eo, w.pair, w.tok,
-                                        w.e13s, w.e2s, w.e13l, w.e2l, SMALL, st), "moe_route"))
+                                        w.e13s, w.e2s, w.e13l, w.e2l, SMALL, w.items13, w.items2,
+                                        w.n_items, st), "moe_route"))
         return 1;
     const int n_small = std::min(E, nj), n_large = std::min(E, nj / (SMALL + 1));
     ApusGemmArgs a{};
@@ -451,13 +462,19 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
     b.wtiled = wtiled;
     b.acodes = w.hc; b.ascale = w.hs;
     b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
+    /* the many-row entries run from the route kernel's work list (one
+     * APUS_PREFILL_ROWS-row chunk per launch row, balanced) where the
+     * many-row schedule applies */
+    const bool use_items = (dim == 2048 || dim == 4096) && (inter == 2048 || inter == 4096);
     for (int pass = 0; pass < 2; ++pass) {
         const int n = pass ? n_large : n_small;
         if (!n) continue;
         a.ents = pass ? w.e13l : w.e13s;
         a.max_m = pass ? 0 : SMALL;
         a.min_m = pass ? SMALL : 0;
-        if (!launched(apus_launch_gemm(APUS_W_FP4, &a, 2 * n, st), "gemm w1/w3")) return 1;
+        a.items = pass && use_items ? w.items13 : nullptr;
+        const int rows = pass && use_items ? 2 * w.n_items : 2 * n;
+        if (!launched(apus_launch_gemm(APUS_W_FP4, &a, rows, st), "gemm w1/w3")) return 1;
     }
     if (!launched(apus_launch_swiglu_quant(w.gm, w.um, nj, inter, limit, w.hc, w.hs, st),
                   "swiglu_quant"))
@@ -468,7 +485,9 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         b.ents = pass ? w.e2l : w.e2s;
         b.max_m = pass ? 0 : SMALL;
         b.min_m = pass ? SMALL : 0;
-        if (!launched(apus_launch_gemm(APUS_W_FP4, &b, n, st), "gemm w2")) return 1;
+        b.items = pass && use_items ? w.items2 : nullptr;
+        const int rows = pass && use_items ? w.n_items : n;
+        if (!launched(apus_launch_gemm(APUS_W_FP4, &b, rows, st), "gemm w2")) return 1;
     }
     if (!launched(apus_launch_moe_accum(w.eo, wgt, s, topk, dim, y, st), "moe_accum"))
         return 1;

@@ -652,16 +652,24 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
     constexpr int ROWS = 16 * TT;                 /* activation rows per chunk */
     constexpr int PITCH = 512 + 16;               /* LDS bytes per row per slice */
     constexpr int CHUNKS = ROWS * 32 / 512;       /* 16-byte loads per thread per slice */
+    static_assert(WF != APUS_W_FP4 || ROWS == APUS_PREFILL_ROWS, "work-list chunk");
     __shared__ __align__(16) uint8_t abuf[2][ROWS * PITCH];
     __shared__ uint8_t sbuf[2][ROWS * 4];
-    const ApusGemmEnt ent = apus_gld<ApusGemmEnt>(args.ents + blockIdx.y);
+    /* launch row = entry, or one work-list item (entry, first row) */
+    int eidx = blockIdx.y, cfirst = 0, cstep = ROWS;
+    if (args.items) {
+        const int2 it = apus_gld<int2>(args.items + blockIdx.y);
+        if (it.x < 0) return;
+        eidx = it.x; cfirst = it.y; cstep = 1 << 30;
+    }
+    const ApusGemmEnt ent = apus_gld<ApusGemmEnt>(args.ents + eidx);
     if (ent.M <= args.m_min || (args.m_max > 0 && ent.M > args.m_max)) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int o = (blockIdx.x * APUS_PRE_WAVES + wave) * 16 + r;   /* O % 128 == 0 */
     const ApusWLane wl = apus_wlane<WF>(ent, args.wtiled, o, lane, K);
 
-    for (int c0 = 0; c0 < ent.M; c0 += ROWS) {
+    for (int c0 = cfirst; c0 < ent.M; c0 += cstep) {
         const int rows = min(ROWS, ent.M - c0);
         /* the activation rows this thread stages (rows past the entry repeat
          * its last row; their outputs are never stored) */
@@ -1201,6 +1209,7 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
     const bool grouped = a->ents != nullptr;
     const size_t row_tiles = (size_t)n_ent * ((a->O + 15) / 16);
     constexpr int R = 8;
+    if (a->items && (wfmt != APUS_W_FP4 || !grouped)) return hipErrorInvalidValue;
     if (a->wtiled) {
         /* tiled weights: only the decode, prefill and tile schedules read them */
         if ((a->K != 2048 && a->K != 4096) || a->O % 128) return hipErrorInvalidValue;
@@ -1229,6 +1238,7 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
         ApusGemmArgs p = *a;
         p.m_min = R;
         p.m_max = 0;
+        /* with a work list, n_ent counts its items */
         dim3 gp(a->O / (16 * APUS_PRE_WAVES), n_ent), bp(512);
         if (wfmt == APUS_W_FP4) {
             if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, 4, 2>), gp, bp, 0, st, p);

@@ -69,9 +69,16 @@ typedef struct {
     int acc_topk, acc_s;
     unsigned *zero;          /* zeroed by workgroups of launch row 0 (the */
     int nzero;               /* tickets of a later launch) */
+    /* many-row schedule work list (optional): launch row y computes rows
+     * [c0, c0 + 64) of entry items[y].x, c0 = items[y].y; x < 0: nothing */
+    const int2 *items;
 } ApusGemmArgs;
 
 enum { APUS_A_CODES = 0, APUS_A_F32 = 1, APUS_A_SWIGLU = 2 };
+
+/* rows (tokens) per chunk of the many-row (prefill) schedule for MXFP4
+ * weights: one work-list item */
+#define APUS_PREFILL_ROWS 64
 
 /* One-token-chunk MoE dispatch for few routed pairs (decode), MXFP4 experts
  * with dim and inter in {2048, 4096}, topk 6 or 8, in two launches:
@@ -117,8 +124,10 @@ hipError_t apus_launch_swiglu_quant(const float *g, const float *u, int M,
  * entry tables: experts with 1..small_max pairs go, in expert order, to the
  * front of e13s [2E] (w1 then w3 of each expert, output rows in sorted
  * order) and e2s [E] (output rows = pair ids); experts with more pairs go to
- * e13l / e2l the same way. Slots past the listed experts have M = 0. The
- * weight pointer tables are device arrays of E pointers each. */
+ * e13l / e2l the same way. Slots past the listed experts have M = 0.
+ * items13 [2 n_items] / items2 [n_items] list (entry, first row) of every
+ * APUS_PREFILL_ROWS-row chunk of the many-row entries (x = -1 past the end).
+ * The weight pointer tables are device arrays of E pointers each. */
 typedef struct {
     const uint8_t *const *w1, *const *w1s, *const *w2, *const *w2s,
                   *const *w3, *const *w3s;
@@ -128,7 +137,14 @@ hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
                                  ApusExpertTable tab, float *g, float *u, float *eo,
                                  int32_t *pair_sorted, int32_t *tok_sorted,
                                  ApusGemmEnt *e13s, ApusGemmEnt *e2s, ApusGemmEnt *e13l,
-                                 ApusGemmEnt *e2l, int small_max, hipStream_t st);
+                                 ApusGemmEnt *e2l, int small_max, int2 *items13, int2 *items2,
+                                 int n_items, hipStream_t st);
+
+/* work-list bound per matrix for the many-row experts of nj pairs */
+static inline int apus_moe_items_bound(int nj, int E, int small_max) {
+    const int nl = (nj / (small_max + 1)) < E ? nj / (small_max + 1) : E;
+    return nj / APUS_PREFILL_ROWS + nl;
+}
 
 /* Row-major <-> MFMA-tiled weights (unpack = 0: w, ws -> tw, tws). FP4
  * moves the weights and the per-32 scales, FP8 the weights only (its

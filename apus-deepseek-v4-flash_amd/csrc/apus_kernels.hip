@@ -118,7 +118,8 @@ __global__ __launch_bounds__(1024) void apus_moe_route_kernel(
     const int32_t *__restrict__ idx, int nj, int topk, int E,
     ApusExpertTable tab, float *g, float *u, float *eo,
     int32_t *pair_sorted, int32_t *tok_sorted, ApusGemmEnt *e13s, ApusGemmEnt *e2s,
-    ApusGemmEnt *e13l, ApusGemmEnt *e2l, int small_max) {
+    ApusGemmEnt *e13l, ApusGemmEnt *e2l, int small_max, int2 *items13, int2 *items2,
+    int n_items) {
     __shared__ int cnt[1024], cur[1024], sw[17];
     const int e = threadIdx.x;
     cnt[e] = 0;
@@ -136,12 +137,23 @@ __global__ __launch_bounds__(1024) void apus_moe_route_kernel(
     int packed_total;
     const int packed = apus_block_scan_excl(small | (large << 16), sw, packed_total);
     const int ns = packed_total & 0xffff, nl = packed_total >> 16;
+    /* work list of the many-row entries: one item per APUS_PREFILL_ROWS rows */
+    const int nchunk = large ? (c + APUS_PREFILL_ROWS - 1) / APUS_PREFILL_ROWS : 0;
+    int total_chunks;
+    const int cbase = apus_block_scan_excl(nchunk, sw, total_chunks);
     for (int q = e; q < nj; q += blockDim.x) {
         const int id = idx[q];
         if ((unsigned)id >= (unsigned)E) continue;      /* ids outside [0, E) are dropped */
         const int pos = atomicAdd(&cur[id], 1);
         pair_sorted[pos] = q;
         tok_sorted[pos] = q / topk;
+    }
+    if (items2) {
+        for (int i = total_chunks + threadIdx.x; i < n_items; i += blockDim.x) {
+            items2[i] = int2{-1, 0};
+            items13[2 * i] = int2{-1, 0};
+            items13[2 * i + 1] = int2{-1, 0};
+        }
     }
     if (e >= E) return;
     ApusGemmEnt a;
@@ -161,6 +173,15 @@ __global__ __launch_bounds__(1024) void apus_moe_route_kernel(
     ApusGemmEnt z{};
     if (e >= ns) { e13s[2 * e] = z; e13s[2 * e + 1] = z; e2s[e] = z; }
     if (e >= nl) { e13l[2 * e] = z; e13l[2 * e + 1] = z; e2l[e] = z; }
+    if (items2) {
+        const int slot = packed >> 16;
+        for (int k = 0; k < nchunk && cbase + k < n_items; ++k) {
+            const int c0 = k * APUS_PREFILL_ROWS;
+            items2[cbase + k] = int2{slot, c0};
+            items13[2 * (cbase + k)] = int2{2 * slot, c0};
+            items13[2 * (cbase + k) + 1] = int2{2 * slot + 1, c0};
+        }
+    }
     (void)total;
 }
 
@@ -168,10 +189,12 @@ hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
                                  ApusExpertTable tab, float *g, float *u, float *eo,
                                  int32_t *pair_sorted, int32_t *tok_sorted,
                                  ApusGemmEnt *e13s, ApusGemmEnt *e2s, ApusGemmEnt *e13l,
-                                 ApusGemmEnt *e2l, int small_max, hipStream_t st) {
+                                 ApusGemmEnt *e2l, int small_max, int2 *items13, int2 *items2,
+                                 int n_items, hipStream_t st) {
     if (E <= 0 || E > 1024) return hipErrorInvalidValue;
     hipLaunchKernelGGL(apus_moe_route_kernel, dim3(1), dim3(1024), 0, st, idx, nj, topk, E,
-                       tab, g, u, eo, pair_sorted, tok_sorted, e13s, e2s, e13l, e2l, small_max);
+                       tab, g, u, eo, pair_sorted, tok_sorted, e13s, e2s, e13l, e2l, small_max,
+                       items13, items2, n_items);
     return hipGetLastError();
 }
 
