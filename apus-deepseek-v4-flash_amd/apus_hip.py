@@ -77,6 +77,19 @@ class ApusHipHooks(C.Structure):
     _fields_ = [(n, vp) for n in HOOK_FIELDS]
 
 
+class ApusHipMoeLayer(C.Structure):
+    """Router and shared-expert weights of one MoE layer (device pointers)."""
+    _fields_ = [("gate_w", vp), ("gate_bias", vp), ("tid2eid", vp), ("hash", C.c_int),
+                ("route_scale", C.c_float), ("limit", C.c_float),
+                ("sw1", vp), ("sw1s", vp), ("sw2", vp), ("sw2s", vp), ("sw3", vp), ("sw3s", vp),
+                ("shared_tiled", C.c_int)]
+
+
+class ApusHipMoeInterm(C.Structure):
+    """Optional device outputs of apus_hip_moe_forward_dev (c/moe.h:64-71)."""
+    _fields_ = [("router_scores", vp), ("router_idx", vp), ("router_w", vp),
+                ("moe_routed", vp), ("moe_shared", vp)]
+
 # entry point -> (restype, argtypes); exactly the declarations of include/apus_hip.h
 SIGNATURES = {
     "apus_hip_enable": (C.c_int, [C.c_char_p, C.c_size_t]),
@@ -116,6 +129,10 @@ SIGNATURES = {
     "apus_hip_moe_workspace": (C.c_size_t, [vp, C.c_int, C.c_int]),
     "apus_hip_moe_routed_dev": (C.c_int, [vp, C.c_int, vp, vp, vp, C.c_int, C.c_int, C.c_float,
                                           vp, vp]),
+    "apus_hip_moe_forward_workspace": (C.c_size_t, [vp, C.c_int, C.c_int]),
+    "apus_hip_moe_forward_dev": (C.c_int, [vp, C.c_int, C.POINTER(ApusHipMoeLayer), vp, vp,
+                                           C.c_int, C.c_int, vp, C.POINTER(ApusHipMoeInterm),
+                                           vp]),
     "apus_hip_malloc": (vp, [C.c_size_t]),
     "apus_hip_free": (C.c_int, [vp]),
     "apus_hip_h2d": (C.c_int, [vp, vp, C.c_size_t]),

@@ -1093,6 +1093,97 @@ int apus_hip_device_info(char *name, size_t cap, int *cus) {
     return 0;
 }
 
+/* ---- whole MoE sublayer (c/moe.h:369-595) ---- */
+
+namespace {
+struct MoeFwdWs {
+    void *routed;                  /* apus_hip_moe_workspace bytes */
+    float *sp, *sel, *wgt, *y, *sh, *g, *u, *hs;
+    int32_t *idx;
+    uint8_t *hc;
+    void *lin;                     /* linear workspace for the shared expert */
+    size_t total;
+};
+
+MoeFwdWs moe_fwd_carve(void *base, const ApusHipStore *st, int s, int topk) {
+    MoeFwdWs w{};
+    const size_t E = st->E, dim = st->dim, inter = st->inter, ss = s;
+    size_t off = 0;
+    auto take = [&](size_t n) { size_t o = off; off += align256(n); return o; };
+    size_t o_r = take(moe_carve(nullptr, s, topk, st->E, st->dim, st->inter).total);
+    size_t o_sp = take(ss * E * 4), o_sel = take(ss * E * 4);
+    size_t o_idx = take(ss * topk * 4), o_wgt = take(ss * topk * 4);
+    size_t o_y = take(ss * dim * 4), o_sh = take(ss * dim * 4);
+    size_t o_g = take(ss * inter * 4), o_u = take(ss * inter * 4);
+    size_t o_hc = take(ss * inter), o_hs = take(ss * (inter / 128) * 4);
+    size_t o_lin = take(align256(ss * dim) + align256(ss * (dim / 128) * 4));
+    w.total = off;
+    if (base) {
+        uint8_t *b = (uint8_t *)base;
+        w.routed = b + o_r;
+        w.sp = (float *)(b + o_sp); w.sel = (float *)(b + o_sel);
+        w.idx = (int32_t *)(b + o_idx); w.wgt = (float *)(b + o_wgt);
+        w.y = (float *)(b + o_y); w.sh = (float *)(b + o_sh);
+        w.g = (float *)(b + o_g); w.u = (float *)(b + o_u);
+        w.hc = b + o_hc; w.hs = (float *)(b + o_hs);
+        w.lin = b + o_lin;
+    }
+    return w;
+}
+}  // namespace
+
+size_t apus_hip_moe_forward_workspace(const ApusHipStore *st, int s, int topk) {
+    if (!st || s <= 0 || topk <= 0) return 0;
+    return moe_fwd_carve(nullptr, st, s, topk).total;
+}
+
+int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoeLayer *ml,
+                             const float *x, const int64_t *ids, int s, int topk, float *out,
+                             const ApusHipMoeInterm *interm, void *workspace) {
+    if (!st || !ml || layer < 0 || layer >= st->L || s <= 0 || topk <= 0 || topk > 16 ||
+        topk > st->E || !workspace || !ml->gate_w || (ml->hash && (!ml->tid2eid || !ids)) ||
+        (!ml->hash && !ml->gate_bias) || st->dim % 256 || !ml->sw1 || !ml->sw2 || !ml->sw3) {
+        set_err("moe_forward_dev: bad arguments");
+        return 1;
+    }
+    if (!ensure_init()) return 1;
+    const int E = st->E, dim = st->dim, inter = st->inter;
+    hipStream_t sm = dev_stream();
+    MoeFwdWs w = moe_fwd_carve(workspace, st, s, topk);
+    /* router: scores, selection, weights */
+    if (!launched(apus_launch_router(ml->gate_w, ml->hash ? nullptr : ml->gate_bias, x, s, dim, E,
+                                     w.sp, ml->hash ? nullptr : w.sel, sm), "router") ||
+        !launched(apus_launch_topk(ml->hash ? nullptr : w.sel, w.sp, s, E, topk,
+                                   ml->hash ? ml->tid2eid : nullptr, ml->hash ? ids : nullptr,
+                                   ml->route_scale, w.idx, w.wgt, sm), "topk"))
+        return 1;
+    /* routed experts */
+    if (apus_hip_moe_routed_dev(st, layer, x, w.idx, w.wgt, s, topk, ml->limit, w.y, w.routed))
+        return 1;
+    /* shared expert (FP8; BF16-rounded linears, SwiGLU, c/moe.h:570-585) */
+    const int f8 = APUS_W_FP8 | (ml->shared_tiled ? APUS_HIP_W_TILED : 0);
+    if (apus_hip_linear_dev(f8, ml->sw1, ml->sw1s, x, w.g, s, dim, inter, w.lin) ||
+        apus_hip_linear_dev(f8, ml->sw3, ml->sw3s, x, w.u, s, dim, inter, w.lin))
+        return 1;
+    if (!launched(apus_launch_swiglu_quant(w.g, w.u, s, inter, ml->limit, w.hc, w.hs, sm),
+                  "shared swiglu"))
+        return 1;
+    if (gemm_dev(f8, ml->sw2, ml->sw2s, w.hc, w.hs, w.sh, s, dim, inter, 1, sm)) return 1;
+    if (!launched(apus_launch_add_bf16(w.y, w.sh, out, (size_t)s * dim, sm), "add")) return 1;
+    if (interm) {
+        const struct { void *dst; const void *src; size_t n; } cp[5] = {
+            {interm->router_scores, w.sp, (size_t)s * E * 4},
+            {interm->router_idx, w.idx, (size_t)s * topk * 4},
+            {interm->router_w, w.wgt, (size_t)s * topk * 4},
+            {interm->moe_routed, w.y, (size_t)s * dim * 4},
+            {interm->moe_shared, w.sh, (size_t)s * dim * 4}};
+        for (const auto &c : cp)
+            if (c.dst && !ok(hipMemcpyAsync(c.dst, c.src, c.n, hipMemcpyDeviceToDevice, sm), "D2D"))
+                return 1;
+    }
+    return 0;
+}
+
 float apus_hip_host_bf16_round(float x) { return apus_bf16_rne(x); }
 uint8_t apus_hip_host_e4m3_quant(float x) { return (uint8_t)apus_e4m3_code(x); }
 float apus_hip_host_act_scale(float amax) { return apus_pow2_from_exp(apus_act_scale_exp(amax)); }

@@ -153,6 +153,16 @@ static inline int apus_moe_items_bound(int nj, int E, int small_max) {
 hipError_t apus_launch_pack(int wfmt, const uint8_t *w, const uint8_t *ws, uint8_t *tw,
                             uint8_t *tws, int O, int K, int unpack, hipStream_t st);
 
+/* Router of one MoE layer (c/moe.h:352-410): scores, selection, weights. */
+hipError_t apus_launch_router(const float *gate_w, const float *bias, const float *x, int s,
+                              int dim, int E, float *sp, float *biased, hipStream_t st);
+hipError_t apus_launch_topk(const float *sel, const float *sp, int s, int E, int topk,
+                            const int64_t *tid2eid, const int64_t *ids, float route_scale,
+                            int32_t *idx, float *wgt, hipStream_t st);
+/* out = bf16(a + b) */
+hipError_t apus_launch_add_bf16(const float *a, const float *b, float *out, size_t n,
+                                hipStream_t st);
+
 /* y[t, i] = sum_j wgt[t, j] * eo[t*topk + j, i] in j order (mul, then add,
  * each rounded), starting from +0. */
 hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,

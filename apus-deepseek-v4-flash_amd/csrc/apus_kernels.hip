@@ -198,6 +198,131 @@ hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
     return hipGetLastError();
 }
 
+/* ---------------------------------------------------------------- router */
+
+/* Router scores (c/moe.h:352-367): sp[t, e] = sqrt(softplus(gate_w[e] . x[t]))
+ * and, with a bias, biased = sp + bias[e] for the selection. One wave per
+ * (token, expert): each lane takes a strided quarter-row of float4s, then a
+ * fixed xor-shuffle tree; the fp32 sum order differs from the reference's
+ * sequential dot (and expf/log1pf come from ROCm's libm), so scores match
+ * within fp32 rounding, not bitwise. dim % 256 == 0. */
+__global__ __launch_bounds__(256) void apus_router_kernel(
+    const float *__restrict__ gate_w, const float *__restrict__ bias,
+    const float *__restrict__ x, int dim, int E, float *__restrict__ sp,
+    float *__restrict__ biased) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int t = blockIdx.y;
+    if (e >= E) return;
+    const float *xr = x + (size_t)t * dim, *wr = gate_w + (size_t)e * dim;
+    float acc = 0.0f;
+    for (int k = lane * 4; k < dim; k += 256) {
+        const float4 a = *reinterpret_cast<const float4 *>(xr + k);
+        const float4 b = *reinterpret_cast<const float4 *>(wr + k);
+        acc = acc + a.x * b.x;
+        acc = acc + a.y * b.y;
+        acc = acc + a.z * b.z;
+        acc = acc + a.w * b.w;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
+    if (lane == 0) {
+        const float v = acc > 20.0f ? acc : log1pf(expf(acc));
+        const float r = sqrtf(v);
+        sp[(size_t)t * E + e] = r;
+        if (biased) biased[(size_t)t * E + e] = r + bias[e];
+    }
+}
+
+hipError_t apus_launch_router(const float *gate_w, const float *bias, const float *x, int s,
+                              int dim, int E, float *sp, float *biased, hipStream_t st) {
+    if (s <= 0) return hipSuccess;
+    if (dim % 256 || E <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(apus_router_kernel, dim3((E + 3) / 4, s), dim3(256), 0, st, gate_w, bias, x,
+                       dim, E, sp, biased);
+    return hipGetLastError();
+}
+
+/* Expert choice and weights of one token per wave (c/moe.h:384-410): the
+ * stable descending top-k of the selection scores (strict greater-than: the
+ * lowest index wins among equal scores, each index at most once,
+ * c/attn.h:668-686), or the hash table's row for the token's id; then
+ * wgt[j] = sp[idx[j]] / sum_j sp[idx[j]] * route_scale with the sum in j
+ * order. E <= 1024, topk <= 16. */
+__global__ __launch_bounds__(64) void apus_topk_kernel(
+    const float *__restrict__ sel, const float *__restrict__ sp, int E, int topk,
+    const int64_t *__restrict__ tid2eid, const int64_t *__restrict__ ids, float route_scale,
+    int32_t *__restrict__ idx, float *__restrict__ wgt) {
+    const int t = blockIdx.x, lane = threadIdx.x;
+    __shared__ int32_t chosen[16];
+    if (tid2eid) {
+        if (lane < topk) chosen[lane] = (int32_t)tid2eid[ids[t] * topk + lane];
+    } else {
+        float v[16];
+        unsigned used = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int e = lane + 64 * i;
+            v[i] = e < E ? sel[(size_t)t * E + e] : 0.0f;
+        }
+        for (int j = 0; j < topk; ++j) {
+            /* lane-local best among unused (lowest index first), then the
+             * wave's: larger value wins, equal values keep the lower index */
+            float bv = 0.0f;
+            int bi = -1;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int e = lane + 64 * i;
+                if (e < E && !(used & (1u << i)) && (bi < 0 || v[i] > bv)) { bv = v[i]; bi = e; }
+            }
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                const float ov = __shfl_xor(bv, off, 64);
+                const int oi = __shfl_xor(bi, off, 64);
+                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) chosen[j] = bi;
+            if ((bi & 63) == lane) used |= 1u << (bi >> 6);
+        }
+    }
+    __syncthreads();
+    if (lane == 0) {
+        float sum = 0.0f;
+        float w[16];
+        for (int j = 0; j < topk; ++j) { w[j] = sp[(size_t)t * E + chosen[j]]; sum += w[j]; }
+        for (int j = 0; j < topk; ++j) {
+            idx[t * topk + j] = chosen[j];
+            wgt[t * topk + j] = w[j] / sum * route_scale;
+        }
+    }
+}
+
+hipError_t apus_launch_topk(const float *sel, const float *sp, int s, int E, int topk,
+                            const int64_t *tid2eid, const int64_t *ids, float route_scale,
+                            int32_t *idx, float *wgt, hipStream_t st) {
+    if (s <= 0) return hipSuccess;
+    if (E <= 0 || E > 1024 || topk <= 0 || topk > 16 || topk > E) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(apus_topk_kernel, dim3(s), dim3(64), 0, st, sel, sp, E, topk, tid2eid, ids,
+                       route_scale, idx, wgt);
+    return hipGetLastError();
+}
+
+/* out = bf16(a + b), elementwise (c/moe.h:588-589) */
+__global__ __launch_bounds__(256) void apus_add_bf16_kernel(const float *__restrict__ a,
+                                                            const float *__restrict__ b,
+                                                            float *__restrict__ out, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = apus_bf16_rne(a[i] + b[i]);
+}
+
+hipError_t apus_launch_add_bf16(const float *a, const float *b, float *out, size_t n,
+                                hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(apus_add_bf16_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       a, b, out, n);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------------- MoE accumulate */
 
 __global__ __launch_bounds__(256) void apus_moe_accum_kernel(

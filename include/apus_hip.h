@@ -255,6 +255,39 @@ int      apus_hip_moe_routed_dev(const ApusHipStore *st, int layer,
                                  const float *wgt, int s, int topk,
                                  float limit, float *y, void *workspace);
 
+/* The whole MoE sublayer of one layer on the device (c/moe.h:369-595,
+ * apus_moe_forward): router scores sqrt(softplus(gate_w x)) (c/moe.h:352-367),
+ * expert choice by stable top-k of the scores plus gate_bias or by the hash
+ * table (tid2eid[ids[t]]), weights sp / sum * route_scale, routed experts from
+ * the store, the FP8 shared expert, and out = bf16(routed + shared). All
+ * pointers are device pointers; asynchronous. Router scores agree with the
+ * CPU's within fp32 rounding (different summation order, ROCm libm), so a
+ * near-tie at the top-k boundary can choose differently. */
+typedef struct {
+    const float *gate_w;      /* [E, dim] fp32 */
+    const float *gate_bias;   /* [E] selection bias (routing by scores) */
+    const int64_t *tid2eid;   /* [*, topk] expert ids per token id (hash != 0) */
+    int hash;
+    float route_scale, limit;
+    /* shared expert, FP8-E4M3 with 128 x 128 E8M0 tile scales:
+     * w1, w3 [inter, dim], w2 [dim, inter] */
+    const uint8_t *sw1, *sw1s, *sw2, *sw2s, *sw3, *sw3s;
+    int shared_tiled;         /* shared weights in the MFMA-tiled layout */
+} ApusHipMoeLayer;
+/* Optional intermediates (c/moe.h:64-71 ApusMoeInterm); NULL members skipped. */
+typedef struct {
+    float *router_scores;     /* [s, E] */
+    int32_t *router_idx;      /* [s, topk] */
+    float *router_w;          /* [s, topk] */
+    float *moe_routed;        /* [s, dim] */
+    float *moe_shared;        /* [s, dim] */
+} ApusHipMoeInterm;
+size_t   apus_hip_moe_forward_workspace(const ApusHipStore *st, int s, int topk);
+int      apus_hip_moe_forward_dev(const ApusHipStore *st, int layer,
+                                  const ApusHipMoeLayer *ml, const float *x,
+                                  const int64_t *ids, int s, int topk, float *out,
+                                  const ApusHipMoeInterm *interm, void *workspace);
+
 /* ---- device memory and timing helpers (tests and benchmarks) ---- */
 void *apus_hip_malloc(size_t bytes);
 int   apus_hip_free(void *p);

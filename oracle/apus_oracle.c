@@ -267,6 +267,100 @@ void orc_moe_routed(const uint8_t *const *w1, const uint8_t *const *w1s,
     free(g); free(u); free(h); free(eo);
 }
 
+/* ------------------------------------------------------------ router */
+
+/* torch softplus, beta 1, threshold 20 (c/moe.h:97-100) */
+static float orc_softplus(float v) { return v > 20.0f ? v : log1pf(expf(v)); }
+
+void orc_router(const float *gate_w, const float *gate_bias, const float *x,
+                int s, int dim, int E, int topk, float route_scale, int hash,
+                const int64_t *tid2eid, const int64_t *ids, float *sp,
+                int32_t *idx, float *wgt) {
+    /* scores: strict k-order fp32 dots, products rounded then added
+     * (apus_dot_f32_scalar, c/attn.h:460-465, via apus_f32_linear), then
+     * sqrt(softplus) (c/moe.h:360-361) */
+    for (int t = 0; t < s; t++)
+        for (int e = 0; e < E; e++) {
+            const float *a = x + (size_t)t * dim, *b = gate_w + (size_t)e * dim;
+            float dot = 0.0f;
+            for (int k = 0; k < dim; k++) {
+                float p = a[k] * b[k];
+                dot = dot + p;
+            }
+            sp[(size_t)t * E + e] = sqrtf(orc_softplus(dot));
+        }
+    for (int t = 0; t < s; t++) {
+        int32_t *it = idx + (size_t)t * topk;
+        const float *row = sp + (size_t)t * E;
+        if (hash) {
+            for (int j = 0; j < topk; j++) it[j] = (int32_t)tid2eid[ids[t] * topk + j];
+        } else {
+            /* selection on sp + bias (c/moe.h:362-363): stable descending
+             * top-k, strict greater-than, lowest index among equals
+             * (c/attn.h:668-686) */
+            char used[1024] = {0};
+            for (int j = 0; j < topk; j++) {
+                int best = -1;
+                float bv = 0.0f;
+                for (int e = 0; e < E; e++) {
+                    if (used[e]) continue;
+                    float v = row[e] + gate_bias[e];
+                    if (best < 0 || v > bv) { best = e; bv = v; }
+                }
+                it[j] = best;
+                used[best] = 1;
+            }
+        }
+        /* weights from the unbiased scores, normalised, times route_scale
+         * (c/moe.h:401-410) */
+        float *wt = wgt + (size_t)t * topk, sum = 0.0f;
+        for (int j = 0; j < topk; j++) { wt[j] = row[it[j]]; sum += wt[j]; }
+        for (int j = 0; j < topk; j++) wt[j] = wt[j] / sum * route_scale;
+    }
+}
+
+void orc_moe_forward(const float *gate_w, const float *gate_bias, int hash,
+                     const int64_t *tid2eid, const int64_t *ids,
+                     float route_scale, float limit,
+                     const uint8_t *const *w1, const uint8_t *const *w1s,
+                     const uint8_t *const *w2, const uint8_t *const *w2s,
+                     const uint8_t *const *w3, const uint8_t *const *w3s,
+                     const uint8_t *sw1, const uint8_t *sw1s,
+                     const uint8_t *sw2, const uint8_t *sw2s,
+                     const uint8_t *sw3, const uint8_t *sw3s,
+                     int E, int topk, int dim, int inter, const float *x, int s,
+                     float *out, float *routed, float *shared, float *sp_out,
+                     int32_t *idx_out, float *wgt_out) {
+    float *sp = malloc((size_t)s * E * sizeof(float));
+    int32_t *idx = malloc((size_t)s * topk * sizeof(int32_t));
+    float *wgt = malloc((size_t)s * topk * sizeof(float));
+    float *y = malloc((size_t)s * dim * sizeof(float));
+    float *sh = malloc((size_t)s * dim * sizeof(float));
+    float *g = malloc((size_t)inter * sizeof(float));
+    float *u = malloc((size_t)inter * sizeof(float));
+    float *h = malloc((size_t)inter * sizeof(float));
+    orc_router(gate_w, gate_bias, x, s, dim, E, topk, route_scale, hash, tid2eid, ids,
+               sp, idx, wgt);
+    orc_moe_routed(w1, w1s, w2, w2s, w3, w3s, dim, inter, limit, x, idx, wgt, s, topk, y);
+    /* shared expert: FP8 linears with BF16 outputs and SwiGLU per row
+     * (c/moe.h:570-585, apus_expert kind 1 c/moe.h:333-350) */
+    for (int t = 0; t < s; t++) {
+        const float *xt = x + (size_t)t * dim;
+        orc_fp8_linear(sw1, sw1s, xt, g, 1, (size_t)dim, (size_t)inter);
+        orc_fp8_linear(sw3, sw3s, xt, u, 1, (size_t)dim, (size_t)inter);
+        orc_swiglu(g, u, h, (size_t)inter, limit);
+        orc_fp8_linear(sw2, sw2s, h, sh + (size_t)t * dim, 1, (size_t)inter, (size_t)dim);
+    }
+    /* out = bf16(routed + shared) (c/moe.h:588-589) */
+    for (size_t i = 0; i < (size_t)s * dim; i++) out[i] = orc_bf16_round(y[i] + sh[i]);
+    if (routed) memcpy(routed, y, (size_t)s * dim * sizeof(float));
+    if (shared) memcpy(shared, sh, (size_t)s * dim * sizeof(float));
+    if (sp_out) memcpy(sp_out, sp, (size_t)s * E * sizeof(float));
+    if (idx_out) memcpy(idx_out, idx, (size_t)s * topk * sizeof(int32_t));
+    if (wgt_out) memcpy(wgt_out, wgt, (size_t)s * topk * sizeof(float));
+    free(sp); free(idx); free(wgt); free(y); free(sh); free(g); free(u); free(h);
+}
+
 /* ------------------------------------------------------------ f64 truth */
 
 void orc_fp4_truth_f64(const uint8_t *w, const uint8_t *ws,

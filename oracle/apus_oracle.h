@@ -99,6 +99,30 @@ void    orc_moe_routed(const uint8_t *const *w1, const uint8_t *const *w1s,
  * (tests/m3/test_fp4.c:75-100, tests/m4a/README.md:78-83):
  *   fp4: esc = sum_kb |dot_kb * sa * sb|
  *   fp8: esc = sum_kb (sum_i |a_i w_i|) * sa * sb */
+/* c/moe.h:352-367 apus_router_score + the routing of apus_moe_forward
+ * (c/moe.h:378-413, top-k c/attn.h:668-686, softplus c/moe.h:97-100).
+ * gate_w [E, dim] fp32; gate_bias [E] (unused with hash); hash: ids [s] and
+ * tid2eid [*, topk] pick the experts. Out: sp [s, E] = sqrt(softplus(gate x)),
+ * idx [s, topk], wgt [s, topk] = sp[idx] / sum * route_scale. */
+void    orc_router(const float *gate_w, const float *gate_bias, const float *x,
+                   int s, int dim, int E, int topk, float route_scale, int hash,
+                   const int64_t *tid2eid, const int64_t *ids, float *sp,
+                   int32_t *idx, float *wgt);
+/* c/moe.h:369-595 apus_moe_forward: router, routed experts (MXFP4), FP8
+ * shared expert (kind 1 of apus_expert / the batched s > 1 form, identical
+ * per row), out = bf16(routed + shared). routed/shared/sp/idx/wgt optional. */
+void    orc_moe_forward(const float *gate_w, const float *gate_bias, int hash,
+                        const int64_t *tid2eid, const int64_t *ids,
+                        float route_scale, float limit,
+                        const uint8_t *const *w1, const uint8_t *const *w1s,
+                        const uint8_t *const *w2, const uint8_t *const *w2s,
+                        const uint8_t *const *w3, const uint8_t *const *w3s,
+                        const uint8_t *sw1, const uint8_t *sw1s,
+                        const uint8_t *sw2, const uint8_t *sw2s,
+                        const uint8_t *sw3, const uint8_t *sw3s,
+                        int E, int topk, int dim, int inter, const float *x, int s,
+                        float *out, float *routed, float *shared, float *sp,
+                        int32_t *idx, float *wgt);
 void    orc_fp4_truth_f64(const uint8_t *w, const uint8_t *ws,
                           const uint8_t *acodes, const float *as,
                           double *out, double *esc,

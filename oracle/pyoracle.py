@@ -22,6 +22,7 @@ u8p = C.POINTER(C.c_uint8)
 f32p = C.POINTER(C.c_float)
 f64p = C.POINTER(C.c_double)
 i32p = C.POINTER(C.c_int32)
+i64p = C.POINTER(C.c_int64)
 u8pp = C.POINTER(u8p)
 
 
@@ -57,6 +58,9 @@ class Oracle:
                                            C.POINTER(C.c_uint32)]),
             "orc_hash64": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
             "orc_fill_bytes": (None, [C.c_uint64, C.c_uint64, C.c_uint64, u8p, sz, C.c_int]),
+            "orc_moe_forward": (None, [f32p, f32p, C.c_int, i64p, i64p, C.c_float, C.c_float]
+                                + [u8pp] * 6 + [u8p] * 6 + [C.c_int] * 4
+                                + [f32p, C.c_int, f32p, f32p, f32p, f32p, i32p, f32p]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -160,6 +164,23 @@ class Oracle:
                               _p(wgt, f32p), s, topk, _p(y, f32p))
         return y
 
+    def moe_forward(self, cfg, experts, shared, x):
+        """orc_moe_forward: (out, routed, shared, sp, idx, wgt)."""
+        keep, tabs, gw, gb, t2e, ids, sh, x, ptr, i64 = _moe_args(cfg, experts, shared, x)
+        s, dim = x.shape
+        E, topk = cfg["E"], cfg["topk"]
+        res = [np.empty((s, dim), np.float32) for _ in range(3)]
+        sp = np.empty((s, E), np.float32)
+        idx = np.empty((s, topk), np.int32)
+        wgt = np.empty((s, topk), np.float32)
+        self.L.orc_moe_forward(_p(gw, f32p), ptr(gb, f32p), int(cfg["hash"]), ptr(t2e, i64),
+                               ptr(ids, i64), C.c_float(cfg["route_scale"]),
+                               C.c_float(cfg["limit"]), *tabs,
+                               *[_p(a, u8p) for a in sh], E, topk, dim, cfg["inter"],
+                               _p(x, f32p), s, *[_p(r, f32p) for r in res], _p(sp, f32p),
+                               _p(idx, i32p), _p(wgt, f32p))
+        return (*res, sp, idx, wgt)
+
     def fill_bytes(self, seed, stream, n, kind, first=0):
         out = np.empty(n, np.uint8)
         self.L.orc_fill_bytes(seed, stream, first, _p(out, u8p), n, kind)
@@ -174,6 +195,30 @@ class Oracle:
 class _WeightView(C.Structure):
     """c/st.h:88-89: {codes|packed, scales, O, K} — same layout for fp8 and fp4."""
     _fields_ = [("w", C.c_void_p), ("s", C.c_void_p), ("O", C.c_int64), ("K", C.c_int64)]
+
+
+def _moe_args(cfg, experts, shared, x):
+    """Argument tuple shared by orc_moe_forward and ref_moe_forward.
+    cfg: dict E, topk, dim, inter, route_scale, limit, hash, gate_w [E, dim],
+    gate_bias [E] or None, tid2eid [n, topk] int64 or None, ids [s] int64 or
+    None; experts: E tuples (w1, w1s, w2, w2s, w3, w3s); shared: FP8 (sw1,
+    sw1s, sw2, sw2s, sw3, sw3s)."""
+    keep = []
+
+    def arr(a, dt):
+        a = np.ascontiguousarray(a, dt)
+        keep.append(a)
+        return a
+    gw = arr(cfg["gate_w"], np.float32)
+    gb = arr(cfg["gate_bias"], np.float32) if cfg.get("gate_bias") is not None else None
+    t2e = arr(cfg["tid2eid"], np.int64) if cfg.get("tid2eid") is not None else None
+    ids = arr(cfg["ids"], np.int64) if cfg.get("ids") is not None else None
+    tabs = [(u8p * len(experts))(*[_p(e[i], u8p) for e in experts]) for i in range(6)]
+    sh = [arr(a, np.uint8) for a in shared]
+    x = arr(x, np.float32)
+    i64 = C.POINTER(C.c_int64)
+    ptr = lambda a, t: _p(a, t) if a is not None else None  # noqa: E731
+    return keep, tabs, gw, gb, t2e, ids, sh, x, ptr, i64
 
 
 class Reference:
@@ -205,6 +250,9 @@ class Reference:
             "ref_moe_routed": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float,
                                          f32p, u8pp, u8pp, u8pp, u8pp, u8pp, u8pp, f32p, i32p,
                                          C.c_int, f32p, f32p, f32p]),
+            "ref_moe_forward": (None, [C.c_int] * 4 + [C.c_float, C.c_float, C.c_int, f32p, f32p,
+                                                        i64p, i64p] + [u8pp] * 6 + [u8p] * 6
+                                + [f32p, C.c_int, f32p, f32p, f32p, f32p, i32p, f32p]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -253,6 +301,23 @@ class Reference:
         h = np.empty_like(g)
         self.L.ref_swiglu(_p(g, f32p), _p(u, f32p), _p(h, f32p), g.size, limit)
         return h
+
+    def moe_forward(self, cfg, experts, shared, x):
+        """The real apus_moe_forward: (out, routed, shared, sp, idx, wgt)."""
+        keep, tabs, gw, gb, t2e, ids, sh, x, ptr, i64 = _moe_args(cfg, experts, shared, x)
+        s, dim = x.shape
+        E, topk = cfg["E"], cfg["topk"]
+        res = [np.empty((s, dim), np.float32) for _ in range(3)]
+        sp = np.empty((s, E), np.float32)
+        idx = np.empty((s, topk), np.int32)
+        wgt = np.empty((s, topk), np.float32)
+        self.L.ref_moe_forward(E, topk, dim, cfg["inter"], C.c_float(cfg["route_scale"]),
+                               C.c_float(cfg["limit"]), int(cfg["hash"]), _p(gw, f32p),
+                               ptr(gb, f32p), ptr(t2e, i64), ptr(ids, i64), *tabs,
+                               *[_p(a, u8p) for a in sh], _p(x, f32p), s,
+                               *[_p(r, f32p) for r in res], _p(sp, f32p), _p(idx, i32p),
+                               _p(wgt, f32p))
+        return (*res, sp, idx, wgt)
 
     def moe_routed(self, experts, gate_w, x, idx, route_scale, limit):
         """Real apus_moe_forward with idx forced through hash routing; returns

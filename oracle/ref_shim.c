@@ -92,6 +92,47 @@ int ref_moe_routed(int E, int topk, int dim, int inter, float route_scale,
     return ok ? 0 : -1;
 }
 
+/* The real apus_moe_forward with every part live: gate (+bias) or hash
+ * routing, MXFP4 routed experts, FP8 shared expert. Returns the layer output
+ * and the intermediates the reference exposes (ApusMoeInterm, c/moe.h:64-71). */
+void ref_moe_forward(int E, int topk, int dim, int inter, float route_scale,
+                     float limit, int hash, const float *gate_w, const float *gate_bias,
+                     const int64_t *tid2eid, const int64_t *ids,
+                     const uint8_t *const *w1, const uint8_t *const *w1s,
+                     const uint8_t *const *w2, const uint8_t *const *w2s,
+                     const uint8_t *const *w3, const uint8_t *const *w3s,
+                     const uint8_t *sw1, const uint8_t *sw1s, const uint8_t *sw2,
+                     const uint8_t *sw2s, const uint8_t *sw3, const uint8_t *sw3s,
+                     const float *x, int s, float *out, float *routed, float *shared,
+                     float *sp, int32_t *idx, float *wgt) {
+    ApusMoeW w;
+    memset(&w, 0, sizeof w);
+    w.E = E; w.topk = topk; w.inter = inter; w.dim = dim; w.hash = hash;
+    w.route_scale = route_scale; w.limit = limit;
+    w.gate_w = gate_w; w.gate_bias = gate_bias; w.tid2eid = tid2eid;
+    ApusFp4W *a1 = calloc((size_t)E, sizeof(ApusFp4W));
+    ApusFp4W *a2 = calloc((size_t)E, sizeof(ApusFp4W));
+    ApusFp4W *a3 = calloc((size_t)E, sizeof(ApusFp4W));
+    for (int e = 0; e < E; e++) {
+        a1[e] = (ApusFp4W){ w1[e], w1s[e], inter, dim };
+        a2[e] = (ApusFp4W){ w2[e], w2s[e], dim, inter };
+        a3[e] = (ApusFp4W){ w3[e], w3s[e], inter, dim };
+    }
+    w.w1 = a1; w.w2 = a2; w.w3 = a3;
+    w.sw1 = (ApusFp8W){ sw1, sw1s, inter, dim };
+    w.sw2 = (ApusFp8W){ sw2, sw2s, dim, inter };
+    w.sw3 = (ApusFp8W){ sw3, sw3s, inter, dim };
+    ApusMoeInterm im;
+    memset(&im, 0, sizeof im);
+    im.router_scores = sp;
+    im.router_idx = idx;
+    im.router_w = wgt;
+    im.moe_routed = routed;
+    im.moe_shared = shared;
+    apus_moe_forward(&w, x, ids, s, out, &im);
+    free(a1); free(a2); free(a3);
+}
+
 /* c/attn.h:393-403 apus_act_quant_rows is static; run it over M rows
  * exactly as apus_fp4_linear / apus_fp8_linear do (BF16 round + act quant). */
 void ref_act_quant_rows(const float *x, int M, int K, float *xb, uint8_t *codes,

@@ -1,0 +1,186 @@
+"""The whole MoE sublayer on the device (apus_hip_moe_forward_dev) against
+the oracle's restatement of apus_moe_forward (c/moe.h:369-595).
+
+The device router sums the gate dot products in another order than the CPU's
+sequential loop and uses ROCm's expf/log1pf/sqrtf, so its scores agree within
+fp32 rounding, not bit for bit. The bars:
+
+* scores sp: |d| <= 1e-5 * max(1, |sp|) elementwise;
+* expert ids: equal for every token whose k-th and (k+1)-th selection scores
+  are more than 1e-4 apart (a closer pair may swap under rounding; such
+  tokens are left out of every comparison below); hash routing: equal always;
+* weights: relative 1e-5;
+* routed, shared and final outputs: max |d| / max |ref| <= 2^-7 (BF16
+  rounding of the expert linears, as in the routed-dispatch tests).
+
+Exact ties (identical gate rows, equal bias) must pick the lowest index, as
+the CPU's strict-greater-than scan does (c/attn.h:668-686).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from helpers import acts, fp8_weights, max_rel, moe_experts
+
+pytestmark = pytest.mark.gpu
+
+
+def _pack_fp8_np(w, O, K):
+    """FP8 MFMA-tiled layout: [O/16][K/128][2 halves][64 lanes][16 B]."""
+    return w.reshape(O // 16, 16, K // 128, 2, 4, 16).transpose(0, 2, 3, 4, 1, 5).reshape(w.shape)
+
+
+def _case(rng, E, dim, inter, s, topk, hash_, gate_scale=1.0):
+    sw = [fp8_weights(rng, inter, dim), fp8_weights(rng, dim, inter), fp8_weights(rng, inter, dim)]
+    cfg = {"E": E, "topk": topk, "dim": dim, "inter": inter, "route_scale": 2.5, "limit": 10.0,
+           "hash": hash_,
+           "gate_w": (rng.standard_normal((E, dim)) * gate_scale / np.sqrt(dim)).astype(np.float32),
+           "gate_bias": (rng.standard_normal(E) * 0.05).astype(np.float32)}
+    if hash_:
+        cfg["tid2eid"] = np.stack([rng.choice(E, topk, replace=False)
+                                   for _ in range(13)]).astype(np.int64)
+        cfg["ids"] = rng.integers(0, 13, s).astype(np.int64)
+    shared = (sw[0][0], sw[0][1], sw[1][0], sw[1][1], sw[2][0], sw[2][1])
+    return cfg, shared, acts(rng, s, dim)
+
+
+def _run_device(hip, st, cfg, shared, x, shared_tiled=False):
+    L = hip.lib()
+    s, dim = x.shape
+    E, topk, inter = cfg["E"], cfg["topk"], cfg["inter"]
+    keep = []
+
+    def dev(a):
+        b = hip.DevBuf.from_array(a)
+        keep.append(b)
+        return b.ptr
+    sw = list(shared)
+    if shared_tiled:
+        sw[0] = _pack_fp8_np(sw[0], inter, dim)
+        sw[2] = _pack_fp8_np(sw[2], dim, inter)
+        sw[4] = _pack_fp8_np(sw[4], inter, dim)
+    ml = hip.ApusHipMoeLayer()
+    ml.gate_w = dev(cfg["gate_w"])
+    ml.gate_bias = dev(cfg["gate_bias"]) if cfg.get("gate_bias") is not None else None
+    ml.tid2eid = dev(cfg["tid2eid"]) if cfg["hash"] else None
+    ml.hash = int(cfg["hash"])
+    ml.route_scale, ml.limit = cfg["route_scale"], cfg["limit"]
+    ml.sw1, ml.sw1s, ml.sw2, ml.sw2s, ml.sw3, ml.sw3s = (dev(a) for a in sw)
+    ml.shared_tiled = int(shared_tiled)
+    dx = dev(x)
+    dids = dev(cfg["ids"]) if cfg["hash"] else None
+    outs = {n: hip.DevBuf(max(1, int(np.prod(sh))) * 4) for n, sh in (
+        ("out", (s, dim)), ("sp", (s, E)), ("idx", (s, topk)), ("wgt", (s, topk)),
+        ("routed", (s, dim)), ("shared", (s, dim)))}
+    im = hip.ApusHipMoeInterm(outs["sp"].ptr, outs["idx"].ptr, outs["wgt"].ptr,
+                              outs["routed"].ptr, outs["shared"].ptr)
+    wsp = hip.DevBuf(L.apus_hip_moe_forward_workspace(st, s, topk))
+    hip._check(L.apus_hip_moe_forward_dev(st, 0, C.byref(ml), dx, dids, s, topk, outs["out"].ptr,
+                                          C.byref(im), wsp.ptr), "moe_forward_dev")
+    hip._check(L.apus_hip_synchronize(), "sync")
+    f = lambda n, sh, dt=np.float32: outs[n].to_array(dt, sh)  # noqa: E731
+    return (f("out", (s, dim)), f("routed", (s, dim)), f("shared", (s, dim)), f("sp", (s, E)),
+            f("idx", (s, topk), np.int32), f("wgt", (s, topk)))
+
+
+def _put_experts(hip, st, experts, dim, inter):
+    for e, ex in enumerate(experts):
+        W = [hip.ApusFp4W(t.ctypes.data_as(hip.u8p), sc.ctypes.data_as(hip.u8p), o, k)
+             for t, sc, o, k in ((ex[0], ex[1], inter, dim), (ex[2], ex[3], dim, inter),
+                                 (ex[4], ex[5], inter, dim))]
+        hip._check(hip.lib().apus_hip_store_put(st, 0, e, C.byref(W[0]), C.byref(W[1]),
+                                                C.byref(W[2])), "put")
+
+
+@pytest.fixture
+def store1(hip):
+    made = []
+
+    def make(E, dim, inter):
+        err = C.create_string_buffer(256)
+        st = hip.lib().apus_hip_store_create(1, E, dim, inter, err, 256)
+        assert st, err.value
+        made.append(st)
+        return st
+    yield make
+    for st in made:
+        hip.lib().apus_hip_store_free(st)
+
+
+def _clear_tokens(cfg, sp_ref):
+    """Tokens whose k-th and (k+1)-th selection scores differ by more than 1e-4."""
+    if cfg["hash"]:
+        return np.ones(sp_ref.shape[0], bool)
+    sel = np.sort(sp_ref.astype(np.float64) + cfg["gate_bias"], axis=1)[:, ::-1]
+    k = cfg["topk"]
+    if k >= sel.shape[1]:
+        return np.ones(sp_ref.shape[0], bool)
+    return (sel[:, k - 1] - sel[:, k]) > 1e-4
+
+
+def _compare(got, want, cfg):
+    out, routed, shared, sp, idx, wgt = got
+    w_out, w_routed, w_shared, w_sp, w_idx, w_wgt = want
+    assert np.all(np.abs(sp.astype(np.float64) - w_sp) <= 1e-5 * np.maximum(1.0, np.abs(w_sp)))
+    ok = _clear_tokens(cfg, w_sp)
+    assert ok.sum() >= max(1, len(ok) // 2), "too few tokens without near-ties"
+    assert np.array_equal(idx[ok], w_idx[ok])
+    assert max_rel(wgt[ok], w_wgt[ok]) <= 1e-5
+    assert max_rel(shared, w_shared) <= 2.0 ** -7
+    assert max_rel(routed[ok], w_routed[ok]) <= 2.0 ** -7
+    assert max_rel(out[ok], w_out[ok]) <= 2.0 ** -7
+
+
+@pytest.mark.parametrize("s,topk,hash_,gate_scale", [(1, 4, 0, 1.0), (7, 4, 0, 1.0), (5, 4, 1, 1.0),
+                                                      (4, 6, 0, 40.0)])
+def test_moe_forward_dev_small(hip, oracle, store1, rng, s, topk, hash_, gate_scale):
+    """Small shape; gate_scale 40 puts gate dot products past 20, where the
+    reference's softplus returns its argument."""
+    E, dim, inter = 16, 256, 128
+    experts = moe_experts(rng, E, dim, inter)
+    cfg, shared, x = _case(rng, E, dim, inter, s, topk, hash_, gate_scale)
+    st = store1(E, dim, inter)
+    _put_experts(hip, st, experts, dim, inter)
+    want = oracle.moe_forward(cfg, experts, shared, x)
+    got = _run_device(hip, st, cfg, shared, x)
+    _compare(got, want, cfg)
+
+
+def test_moe_forward_dev_exact_ties_pick_lowest_index(hip, oracle, store1, rng):
+    """All gate rows equal and no bias: every score ties, so the choice is
+    experts 0..topk-1 in order, with equal weights route_scale / topk."""
+    E, dim, inter, s, topk = 16, 256, 128, 3, 4
+    experts = moe_experts(rng, E, dim, inter)
+    cfg, shared, x = _case(rng, E, dim, inter, s, topk, 0)
+    cfg["gate_w"] = np.repeat(cfg["gate_w"][:1], E, axis=0)
+    cfg["gate_bias"] = np.zeros(E, np.float32)
+    st = store1(E, dim, inter)
+    _put_experts(hip, st, experts, dim, inter)
+    want = oracle.moe_forward(cfg, experts, shared, x)
+    got = _run_device(hip, st, cfg, shared, x)
+    assert np.array_equal(want[4], np.tile(np.arange(topk, dtype=np.int32), (s, 1)))
+    assert np.array_equal(got[4], want[4])
+    assert max_rel(got[5], want[5]) <= 1e-6
+    assert max_rel(got[0], want[0]) <= 2.0 ** -7
+
+
+@pytest.mark.parametrize("hash_,shared_tiled", [(0, True), (1, False)])
+def test_moe_forward_dev_model_shape(hip, oracle, store1, rng, hash_, shared_tiled):
+    """One decode token at the model's shape (256 experts, dim 4096, inter
+    2048, top-6), the store filled on the device; host copies of only the
+    experts the routing picks (the rest share a placeholder, which the
+    dispatch never reads)."""
+    from test_gpu_store import host_expert
+    E, dim, inter, s, topk, seed = 256, 4096, 2048, 2, 6, 3
+    cfg, shared, x = _case(rng, E, dim, inter, s, topk, hash_)
+    st = store1(E, dim, inter)
+    hip._check(hip.lib().apus_hip_store_fill_random(st, seed), "fill")
+    first = host_expert(oracle, seed, 0, 0, E, dim, inter)
+    probe = oracle.moe_forward(cfg, [first] * E, shared, x)
+    used = sorted(set(int(e) for e in probe[4].ravel()))
+    host = {e: host_expert(oracle, seed, 0, e, E, dim, inter) for e in used}
+    experts = [host.get(e, first) for e in range(E)]
+    want = oracle.moe_forward(cfg, experts, shared, x)
+    got = _run_device(hip, st, cfg, shared, x, shared_tiled)
+    _compare(got, want, cfg)

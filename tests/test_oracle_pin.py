@@ -276,3 +276,54 @@ def test_fill_bytes_ranges_and_determinism(oracle):
     vals = np.vectorize(oracle.e4m3_dequant)(w8)
     assert abs(vals.mean()) < 0.05 and 0.9 < vals.std() < 1.1
     assert not np.any((w8 & 0x7F) == 0x7F)
+
+
+def _moe_case(rng, E, dim, inter, s, topk, hash_):
+    from helpers import acts, fp8_weights, moe_experts
+    experts = moe_experts(rng, E, dim, inter)
+    sw1, sw1s = fp8_weights(rng, inter, dim)
+    sw2, sw2s = fp8_weights(rng, dim, inter)
+    sw3, sw3s = fp8_weights(rng, inter, dim)
+    cfg = {"E": E, "topk": topk, "dim": dim, "inter": inter, "route_scale": 2.5, "limit": 10.0,
+           "hash": hash_, "gate_w": (rng.standard_normal((E, dim)) / np.sqrt(dim)).astype(np.float32),
+           "gate_bias": (rng.standard_normal(E) * 0.05).astype(np.float32)}
+    if hash_:
+        cfg["tid2eid"] = np.stack([rng.choice(E, topk, replace=False) for _ in range(11)]).astype(np.int64)
+        cfg["ids"] = rng.integers(0, 11, s).astype(np.int64)
+    return cfg, experts, (sw1, sw1s, sw2, sw2s, sw3, sw3s), acts(rng, s, dim)
+
+
+@pytest.mark.parametrize("s,hash_", [(1, 0), (5, 0), (3, 1)])
+def test_moe_forward_restatement_vs_reference(oracle, ref, rng, s, hash_):
+    """orc_moe_forward (router + routed + FP8 shared + final bf16 sum) equals
+    the real apus_moe_forward bit for bit, intermediates included."""
+    cfg, experts, shared, x = _moe_case(rng, 16, 256, 128, s, 4, hash_)
+    got = oracle.moe_forward(cfg, experts, shared, x)
+    want = ref.moe_forward(cfg, experts, shared, x)
+    for name, a, b in zip(("out", "routed", "shared", "sp", "idx", "wgt"), got, want):
+        assert np.array_equal(a.view(np.uint32) if a.dtype != np.int32 else a,
+                              b.view(np.uint32) if b.dtype != np.int32 else b), name
+
+
+@pytest.mark.parametrize("case", ["ties", "large"])
+def test_router_edges_restatement_vs_reference(oracle, ref, rng, case):
+    """Router edge cases, restatement vs the real apus_moe_forward: exact ties
+    (identical gate rows, zero bias: the lowest indices win, in order) and
+    gate dot products past 20 (softplus returns its argument)."""
+    E, topk, s = 16, 4, 3
+    cfg, experts, shared, x = _moe_case(rng, E, 256, 128, s, topk, 0)
+    if case == "ties":
+        cfg["gate_w"] = np.repeat(cfg["gate_w"][:1], E, axis=0)
+        cfg["gate_bias"] = np.zeros(E, np.float32)
+    else:
+        cfg["gate_w"] = cfg["gate_w"] * 40.0
+    got = oracle.moe_forward(cfg, experts, shared, x)
+    want = ref.moe_forward(cfg, experts, shared, x)
+    for name, a, b in zip(("out", "routed", "shared", "sp", "idx", "wgt"), got, want):
+        assert np.array_equal(a.view(np.uint32) if a.dtype != np.int32 else a,
+                              b.view(np.uint32) if b.dtype != np.int32 else b), name
+    if case == "ties":
+        assert np.array_equal(got[4], np.tile(np.arange(topk, dtype=np.int32), (s, 1)))
+    else:
+        dots = x.astype(np.float64) @ cfg["gate_w"].T.astype(np.float64)
+        assert (dots > 20).any()
