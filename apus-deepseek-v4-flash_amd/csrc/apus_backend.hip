@@ -72,6 +72,10 @@ struct State {
     hipStream_t lane[8] = {};
     hipEvent_t lane_ev[8] = {};
     int nlanes = 1, cur_lane = 0;
+    /* the MoE sublayer's shared expert runs beside the router and the routed
+     * experts on this stream (forked from and joined to the caller's) */
+    hipStream_t side = nullptr;
+    hipEvent_t side_fork = nullptr, side_done = nullptr;
     std::unordered_map<const void *, DenseW> dense;
     std::unordered_map<uint64_t, ExpertW> experts;
     DevBuf scratch[8];
@@ -108,6 +112,10 @@ bool ensure_init() {
     if (!ok(hipEventCreate(&g.ev1), "hipEventCreate")) return false;
     g.lane[0] = g.stream;
     if (!ok(hipEventCreateWithFlags(&g.lane_ev[0], hipEventDisableTiming), "hipEventCreate")) return false;
+    if (!ok(hipStreamCreateWithFlags(&g.side, hipStreamNonBlocking), "hipStreamCreate") ||
+        !ok(hipEventCreateWithFlags(&g.side_fork, hipEventDisableTiming), "hipEventCreate") ||
+        !ok(hipEventCreateWithFlags(&g.side_done, hipEventDisableTiming), "hipEventCreate"))
+        return false;
     const char *mb = getenv("APUS_HIP_DENSE_MB");
     g.dense_budget = (size_t)(mb ? strtoull(mb, nullptr, 10) : 131072ull) << 20;
     g.inited = true;
@@ -381,7 +389,13 @@ struct MoeSlab {
 int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
                  const float *x, const int32_t *idx, const float *wgt, int s,
                  int topk, float *y, const MoeWs &w, bool wtiled, const MoeSlab *slab,
-                 hipStream_t st) {
+                 hipStream_t st, const float *add_src = nullptr, float *add_out = nullptr,
+                 hipEvent_t add_ready = nullptr) {
+    /* with add_out: also add_out = bf16(y + add_src), fused into the last
+     * launch where it can be; add_src is complete once add_ready has fired */
+    auto wait_add = [&]() {
+        return !add_ready || ok(hipStreamWaitEvent(st, add_ready, 0), "hipStreamWaitEvent");
+    };
     const int nj = s * topk;
     ApusExpertTable t;
     t.w1 = tab; t.w1s = tab + E; t.w2 = tab + 2 * E; t.w2s = tab + 3 * E;
@@ -417,6 +431,8 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
             b.pwoff[0] = slab->off[2]; b.psoff[0] = slab->off[3];
         }
         b.acc_w = wgt; b.acc_y = y; b.acc_topk = topk; b.acc_s = s;
+        b.add_src = add_out ? add_src : nullptr; b.add_out = add_out;
+        if (add_out && !wait_add()) return 1;
         return launched(apus_launch_moe_pair2(&b, st), "pair w2") ? 0 : 1;
     }
     /* few pairs, other topk: one launch entry per routed pair and matrix.
@@ -441,7 +457,10 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         b.pidx = idx; b.nmat = 1; b.adiv = 1; b.pE = E;
         b.pw[0] = t.w2; b.pws[0] = t.w2s; b.pout[0] = w.eo;
         b.acc_w = wgt; b.acc_y = y; b.tickets = w.tickets; b.acc_topk = topk; b.acc_s = s;
-        return launched(apus_launch_gemm_few(APUS_W_FP4, &b, nj, 1, 0, st), "pair w2") ? 0 : 1;
+        if (!launched(apus_launch_gemm_few(APUS_W_FP4, &b, nj, 1, 0, st), "pair w2")) return 1;
+        if (!add_out) return 0;
+        return wait_add() && launched(apus_launch_add_bf16(y, add_src, add_out, (size_t)s * dim, st),
+                                      "add") ? 0 : 1;
     }
     /* experts with at most SMALL pairs take the few-row GEMM schedule; at
      * most min(E, nj) experts are small and at most nj / (SMALL + 1) are
@@ -489,7 +508,9 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         const int rows = pass && use_items ? w.n_items : n;
         if (!launched(apus_launch_gemm(APUS_W_FP4, &b, rows, st), "gemm w2")) return 1;
     }
-    if (!launched(apus_launch_moe_accum(w.eo, wgt, s, topk, dim, y, st), "moe_accum"))
+    if (add_out && !wait_add()) return 1;
+    if (!launched(apus_launch_moe_accum(w.eo, wgt, s, topk, dim, y, add_out ? add_src : nullptr,
+                                        add_out, st), "moe_accum"))
         return 1;
     return 0;
 }
@@ -1130,6 +1151,39 @@ MoeFwdWs moe_fwd_carve(void *base, const ApusHipStore *st, int s, int topk) {
     }
     return w;
 }
+/* The FP8 shared expert sh = w2(swiglu(w1 x, w3 x)) with BF16-rounded
+ * linears (c/moe.h:570-585). Up to 8 tokens: w1 and w3 in one few-row launch
+ * (x quantised while staging), w2 with h = swiglu(g, u) computed and
+ * quantised while staging. More tokens: act quant, GEMMs, swiglu_quant. */
+int shared_expert(const ApusHipMoeLayer *ml, const float *x, int s, int dim, int inter,
+                  bool tiled, const MoeFwdWs &w, hipStream_t st) {
+    const int f8 = APUS_W_FP8 | (tiled ? APUS_HIP_W_TILED : 0);
+    const bool fused = s <= 8 && (dim == 2048 || dim == 4096) && (inter == 2048 || inter == 4096);
+    if (fused) {
+        ApusGemmArgs a{};
+        a.wtiled = tiled;
+        a.ent0.w = ml->sw1; a.ent0.ws = ml->sw1s; a.ent0.out = w.g; a.ent0.M = s;
+        a.ent1.w = ml->sw3; a.ent1.ws = ml->sw3s; a.ent1.out = w.u; a.ent1.M = s;
+        a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
+        a.asrc = APUS_A_F32; a.ax = x;
+        if (!launched(apus_launch_gemm_few(APUS_W_FP8, &a, 2, 8, 0, st), "shared w1/w3")) return 1;
+        ApusGemmArgs b{};
+        b.wtiled = tiled;
+        b.ent0.w = ml->sw2; b.ent0.ws = ml->sw2s; b.ent0.out = w.sh; b.ent0.M = s;
+        b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
+        b.asrc = APUS_A_SWIGLU; b.ax = w.g; b.au = w.u; b.limit = ml->limit;
+        return launched(apus_launch_gemm_few(APUS_W_FP8, &b, 1, 8, 0, st), "shared w2") ? 0 : 1;
+    }
+    uint8_t *xc = (uint8_t *)w.lin;
+    float *xs = (float *)((uint8_t *)w.lin + align256((size_t)s * dim));
+    if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, xc, xs, st), "shared act_quant") ||
+        gemm_dev(f8, ml->sw1, ml->sw1s, xc, xs, w.g, s, inter, dim, 1, st) ||
+        gemm_dev(f8, ml->sw3, ml->sw3s, xc, xs, w.u, s, inter, dim, 1, st) ||
+        !launched(apus_launch_swiglu_quant(w.g, w.u, s, inter, ml->limit, w.hc, w.hs, st),
+                  "shared swiglu"))
+        return 1;
+    return gemm_dev(f8, ml->sw2, ml->sw2s, w.hc, w.hs, w.sh, s, dim, inter, 1, st);
+}
 }  // namespace
 
 size_t apus_hip_moe_forward_workspace(const ApusHipStore *st, int s, int topk) {
@@ -1150,6 +1204,15 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
     const int E = st->E, dim = st->dim, inter = st->inter;
     hipStream_t sm = dev_stream();
     MoeFwdWs w = moe_fwd_carve(workspace, st, s, topk);
+    /* shared expert (FP8; BF16-rounded linears, SwiGLU, c/moe.h:570-585) on
+     * the side stream, beside the router and the routed experts: it needs
+     * only x */
+    const bool sh_tiled = ml->shared_tiled != 0;
+    if (!ok(hipEventRecord(g.side_fork, sm), "hipEventRecord") ||
+        !ok(hipStreamWaitEvent(g.side, g.side_fork, 0), "hipStreamWaitEvent") ||
+        shared_expert(ml, x, s, dim, inter, sh_tiled, w, g.side) ||
+        !ok(hipEventRecord(g.side_done, g.side), "hipEventRecord"))
+        return 1;
     /* router: scores, selection, weights */
     if (!launched(apus_launch_router(ml->gate_w, ml->hash ? nullptr : ml->gate_bias, x, s, dim, E,
                                      w.sp, ml->hash ? nullptr : w.sel, sm), "router") ||
@@ -1157,19 +1220,17 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
                                    ml->hash ? ml->tid2eid : nullptr, ml->hash ? ids : nullptr,
                                    ml->route_scale, w.idx, w.wgt, sm), "topk"))
         return 1;
-    /* routed experts */
-    if (apus_hip_moe_routed_dev(st, layer, x, w.idx, w.wgt, s, topk, ml->limit, w.y, w.routed))
-        return 1;
-    /* shared expert (FP8; BF16-rounded linears, SwiGLU, c/moe.h:570-585) */
-    const int f8 = APUS_W_FP8 | (ml->shared_tiled ? APUS_HIP_W_TILED : 0);
-    if (apus_hip_linear_dev(f8, ml->sw1, ml->sw1s, x, w.g, s, dim, inter, w.lin) ||
-        apus_hip_linear_dev(f8, ml->sw3, ml->sw3s, x, w.u, s, dim, inter, w.lin))
-        return 1;
-    if (!launched(apus_launch_swiglu_quant(w.g, w.u, s, inter, ml->limit, w.hc, w.hs, sm),
-                  "shared swiglu"))
-        return 1;
-    if (gemm_dev(f8, ml->sw2, ml->sw2s, w.hc, w.hs, w.sh, s, dim, inter, 1, sm)) return 1;
-    if (!launched(apus_launch_add_bf16(w.y, w.sh, out, (size_t)s * dim, sm), "add")) return 1;
+    /* routed experts; the last launch waits for the shared expert and also
+     * writes out = bf16(routed + shared) (c/moe.h:588-589) */
+    {
+        const MoeWs mw = moe_carve(w.routed, s, topk, st->E, st->dim, st->inter);
+        MoeSlab slab{st->layer_base[layer], st->expert_bytes, {}};
+        size_t off = 0;
+        for (int i = 0; i < 6; i++) { slab.off[i] = off; off += align256(st->sz[i]); }
+        if (moe_pipeline(E, dim, inter, ml->limit, st->layer_tab[layer], x, w.idx, w.wgt, s, topk,
+                         w.y, mw, st->tiled, &slab, sm, w.sh, out, g.side_done))
+            return 1;
+    }
     if (interm) {
         const struct { void *dst; const void *src; size_t n; } cp[5] = {
             {interm->router_scores, w.sp, (size_t)s * E * 4},

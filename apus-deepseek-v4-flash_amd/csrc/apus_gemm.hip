@@ -350,7 +350,7 @@ __device__ __forceinline__ void apus_expert_ptrs(const ApusGemmArgs &a, int mat,
 /* the entry of launch row y: table, routed pair, or the single entry */
 __device__ __forceinline__ ApusGemmEnt apus_entry_of(const ApusGemmArgs &a, int y) {
     if (a.ents) return apus_gld<ApusGemmEnt>(a.ents + y);
-    if (!a.pidx) return a.ent0;
+    if (!a.pidx) return y == 0 ? a.ent0 : a.ent1;
     ApusGemmEnt ent;
     const int p = y / a.nmat, mat = y - p * a.nmat;
     const int e = apus_gld<int>(a.pidx + p);
@@ -1087,7 +1087,9 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
                 eo = okj[j] ? apus_bf16_rne(eo) : 0.0f;
                 y = __fadd_rn(y, __fmul_rn(apus_gld<float>(args.acc_w + p0 + j), eo));
             }
-            apus_gst<float>(args.acc_y + (size_t)t * args.ldo + blockIdx.x * 16 + threadIdx.x, y);
+            const size_t o = (size_t)t * args.ldo + blockIdx.x * 16 + threadIdx.x;
+            apus_gst<float>(args.acc_y + o, y);
+            if (args.add_out) apus_gst<float>(args.add_out + o, apus_bf16_rne(y + apus_gld<float>(args.add_src + o)));
         }
     }
 }
@@ -1174,8 +1176,14 @@ hipError_t apus_launch_gemm_few(int wfmt, const ApusGemmArgs *a, int n_ent, int 
                                 int ks, hipStream_t st) {
     if (n_ent <= 0) return hipSuccess;
     if ((a->K != 2048 && a->K != 4096) || a->O % 128 || (rows != 1 && rows != 8) ||
-        (a->asrc == APUS_A_CODES && rows != 8) || (a->asrc == APUS_A_SWIGLU && wfmt != APUS_W_FP4) ||
+        (a->asrc == APUS_A_CODES && rows != 8) ||
         (a->acc_y && (!a->pidx || a->nmat != 1 || !a->tickets)) || ks < 0 || ks > 4 || ks == 3)
+        return hipErrorInvalidValue;
+    /* two by-value entries share their activation rows (staged once, before
+     * the entry lookup) */
+    if (!a->ents && !a->pidx &&
+        (n_ent > 2 || (n_ent == 2 && (a->ent1.a0 != a->ent0.a0 || a->ent1.arows != a->ent0.arows ||
+                                      a->ent1.M != a->ent0.M))))
         return hipErrorInvalidValue;
     if (!ks) ks = apus_dec_ks((size_t)n_ent * (a->O / 16));
     const bool fp4 = wfmt == APUS_W_FP4;
@@ -1194,8 +1202,13 @@ hipError_t apus_launch_gemm_few(int wfmt, const ApusGemmArgs *a, int n_ent, int 
         }
         break;
     case APUS_A_SWIGLU:
-        if (rows == 1) apus_launch_dec_k<APUS_W_FP4, 1, APUS_A_SWIGLU>(*a, n_ent, ks, st);
-        else           apus_launch_dec_k<APUS_W_FP4, 8, APUS_A_SWIGLU>(*a, n_ent, ks, st);
+        if (rows == 1) {
+            if (fp4) apus_launch_dec_k<APUS_W_FP4, 1, APUS_A_SWIGLU>(*a, n_ent, ks, st);
+            else     apus_launch_dec_k<APUS_W_FP8, 1, APUS_A_SWIGLU>(*a, n_ent, ks, st);
+        } else {
+            if (fp4) apus_launch_dec_k<APUS_W_FP4, 8, APUS_A_SWIGLU>(*a, n_ent, ks, st);
+            else     apus_launch_dec_k<APUS_W_FP8, 8, APUS_A_SWIGLU>(*a, n_ent, ks, st);
+        }
         break;
     default:
         return hipErrorInvalidValue;

@@ -31,6 +31,8 @@ typedef struct {
     const float *ascale;     /* [rows, K/128] */
     const ApusGemmEnt *ents; /* grouped: device array; else NULL */
     ApusGemmEnt ent0;        /* the entry when ents == NULL */
+    ApusGemmEnt ent1;        /* few-row schedule, ents and pidx NULL, two launch
+                              * entries: entry 1 (same activation rows as ent0) */
     int O, K, ldo, round_out;
     int wtiled;              /* every W (and FP4 scale) in the MFMA-tiled layout of
                               * apus_launch_pack: K 2048 or 4096, O % 128 == 0 */
@@ -67,6 +69,10 @@ typedef struct {
     float *acc_y;
     unsigned *tickets;
     int acc_topk, acc_s;
+    /* optional fused sum (apus_moe_pair2_kernel): add_out[t, o] =
+     * bf16(y[t, o] + add_src[t, o]), row stride ldo */
+    const float *add_src;
+    float *add_out;
     unsigned *zero;          /* zeroed by workgroups of launch row 0 (the */
     int nzero;               /* tickets of a later launch) */
     /* many-row schedule work list (optional): launch row y computes rows
@@ -164,9 +170,11 @@ hipError_t apus_launch_add_bf16(const float *a, const float *b, float *out, size
                                 hipStream_t st);
 
 /* y[t, i] = sum_j wgt[t, j] * eo[t*topk + j, i] in j order (mul, then add,
- * each rounded), starting from +0. */
+ * each rounded), starting from +0; with add_out, also add_out[t, i] =
+ * bf16(y[t, i] + add_src[t, i]). */
 hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,
-                                 int topk, int dim, float *y, hipStream_t st);
+                                 int topk, int dim, float *y, const float *add_src,
+                                 float *add_out, hipStream_t st);
 
 /* Counter-based fill (kind as orc_fill_bytes: 0 uniform byte, 1 E8M0
  * 118..130, 2 E4M3 of ~N(0,1), 3 E8M0 117..123). */

@@ -201,45 +201,70 @@ hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
 /* ---------------------------------------------------------------- router */
 
 /* Router scores (c/moe.h:352-367): sp[t, e] = sqrt(softplus(gate_w[e] . x[t]))
- * and, with a bias, biased = sp + bias[e] for the selection. One wave per
- * (token, expert): each lane takes a strided quarter-row of float4s, then a
- * fixed xor-shuffle tree; the fp32 sum order differs from the reference's
+ * and, with a bias, biased = sp + bias[e] for the selection. One workgroup
+ * per (expert, group of up to 8 tokens): the expert's gate row is read once
+ * into registers (thread i holds float4s i, i + 256, ...), each token's dot is
+ * a per-thread partial, a fixed xor-shuffle tree per wave and the four wave
+ * sums in wave order. The fp32 sum order differs from the reference's
  * sequential dot (and expf/log1pf come from ROCm's libm), so scores match
- * within fp32 rounding, not bitwise. dim % 256 == 0. */
+ * within fp32 rounding, not bitwise. dim % 256 == 0, dim <= 8192. */
+#define APUS_ROUTER_TT 8
 __global__ __launch_bounds__(256) void apus_router_kernel(
     const float *__restrict__ gate_w, const float *__restrict__ bias,
-    const float *__restrict__ x, int dim, int E, float *__restrict__ sp,
+    const float *__restrict__ x, int s, int dim, int E, float *__restrict__ sp,
     float *__restrict__ biased) {
-    const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int t = blockIdx.y;
-    if (e >= E) return;
-    const float *xr = x + (size_t)t * dim, *wr = gate_w + (size_t)e * dim;
-    float acc = 0.0f;
-    for (int k = lane * 4; k < dim; k += 256) {
-        const float4 a = *reinterpret_cast<const float4 *>(xr + k);
-        const float4 b = *reinterpret_cast<const float4 *>(wr + k);
-        acc = acc + a.x * b.x;
-        acc = acc + a.y * b.y;
-        acc = acc + a.z * b.z;
-        acc = acc + a.w * b.w;
-    }
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int e = blockIdx.x, t0 = blockIdx.y * APUS_ROUTER_TT;
+    const int nt = min(APUS_ROUTER_TT, s - t0);
+    const int n4 = dim >> 2;
+    const float4 *wr = reinterpret_cast<const float4 *>(gate_w + (size_t)e * dim);
+    float4 g[8];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
-    if (lane == 0) {
-        const float v = acc > 20.0f ? acc : log1pf(expf(acc));
+    for (int i = 0; i < 8; ++i)
+        g[i] = (tid + 256 * i < n4) ? apus_gld<float4>(wr + tid + 256 * i)
+                                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    float acc[APUS_ROUTER_TT];
+#pragma unroll
+    for (int t = 0; t < APUS_ROUTER_TT; ++t) {
+        acc[t] = 0.0f;
+        if (t < nt) {
+            const float4 *xr = reinterpret_cast<const float4 *>(x + (size_t)(t0 + t) * dim);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (tid + 256 * i < n4) {
+                    const float4 a = apus_gld<float4>(xr + tid + 256 * i);
+                    acc[t] = acc[t] + a.x * g[i].x;
+                    acc[t] = acc[t] + a.y * g[i].y;
+                    acc[t] = acc[t] + a.z * g[i].z;
+                    acc[t] = acc[t] + a.w * g[i].w;
+                }
+            }
+        }
+    }
+    __shared__ float part[4][APUS_ROUTER_TT];
+#pragma unroll
+    for (int t = 0; t < APUS_ROUTER_TT; ++t) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc[t] = acc[t] + __shfl_xor(acc[t], off, 64);
+        if (lane == 0) part[wv][t] = acc[t];
+    }
+    __syncthreads();
+    if (tid < nt) {
+        const float d = ((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid];
+        const float v = d > 20.0f ? d : log1pf(expf(d));
         const float r = sqrtf(v);
-        sp[(size_t)t * E + e] = r;
-        if (biased) biased[(size_t)t * E + e] = r + bias[e];
+        const size_t o = (size_t)(t0 + tid) * E + e;
+        sp[o] = r;
+        if (biased) biased[o] = r + bias[e];
     }
 }
 
 hipError_t apus_launch_router(const float *gate_w, const float *bias, const float *x, int s,
                               int dim, int E, float *sp, float *biased, hipStream_t st) {
     if (s <= 0) return hipSuccess;
-    if (dim % 256 || E <= 0) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(apus_router_kernel, dim3((E + 3) / 4, s), dim3(256), 0, st, gate_w, bias, x,
-                       dim, E, sp, biased);
+    if (dim % 256 || dim > 8192 || E <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(apus_router_kernel, dim3(E, (s + APUS_ROUTER_TT - 1) / APUS_ROUTER_TT),
+                       dim3(256), 0, st, gate_w, bias, x, s, dim, E, sp, biased);
     return hipGetLastError();
 }
 
@@ -248,51 +273,64 @@ hipError_t apus_launch_router(const float *gate_w, const float *bias, const floa
  * lowest index wins among equal scores, each index at most once,
  * c/attn.h:668-686), or the hash table's row for the token's id; then
  * wgt[j] = sp[idx[j]] / sum_j sp[idx[j]] * route_scale with the sum in j
- * order. E <= 1024, topk <= 16. */
+ * order. Each lane holds the selection and router scores of experts lane,
+ * lane + 64, ...; the winner's router score travels with it through the
+ * shuffle tree, so no dependent loads follow the selection. E <= 1024,
+ * topk <= 16. */
 __global__ __launch_bounds__(64) void apus_topk_kernel(
     const float *__restrict__ sel, const float *__restrict__ sp, int E, int topk,
     const int64_t *__restrict__ tid2eid, const int64_t *__restrict__ ids, float route_scale,
     int32_t *__restrict__ idx, float *__restrict__ wgt) {
     const int t = blockIdx.x, lane = threadIdx.x;
     __shared__ int32_t chosen[16];
+    __shared__ float chp[16];
     if (tid2eid) {
-        if (lane < topk) chosen[lane] = (int32_t)tid2eid[ids[t] * topk + lane];
+        if (lane < topk) {
+            const int e = (int)tid2eid[ids[t] * topk + lane];
+            chosen[lane] = e;
+            chp[lane] = sp[(size_t)t * E + e];
+        }
     } else {
-        float v[16];
+        float v[16], p[16];
         unsigned used = 0;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int e = lane + 64 * i;
             v[i] = e < E ? sel[(size_t)t * E + e] : 0.0f;
+            p[i] = e < E ? sp[(size_t)t * E + e] : 0.0f;
         }
         for (int j = 0; j < topk; ++j) {
             /* lane-local best among unused (lowest index first), then the
              * wave's: larger value wins, equal values keep the lower index */
-            float bv = 0.0f;
+            float bv = 0.0f, bp = 0.0f;
             int bi = -1;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int e = lane + 64 * i;
-                if (e < E && !(used & (1u << i)) && (bi < 0 || v[i] > bv)) { bv = v[i]; bi = e; }
+                if (e < E && !(used & (1u << i)) && (bi < 0 || v[i] > bv)) {
+                    bv = v[i]; bp = p[i]; bi = e;
+                }
             }
 #pragma unroll
             for (int off = 32; off >= 1; off >>= 1) {
                 const float ov = __shfl_xor(bv, off, 64);
+                const float op = __shfl_xor(bp, off, 64);
                 const int oi = __shfl_xor(bi, off, 64);
-                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) { bv = ov; bi = oi; }
+                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
+                    bv = ov; bp = op; bi = oi;
+                }
             }
-            if (lane == 0) chosen[j] = bi;
+            if (lane == 0) { chosen[j] = bi; chp[j] = bp; }
             if ((bi & 63) == lane) used |= 1u << (bi >> 6);
         }
     }
     __syncthreads();
     if (lane == 0) {
         float sum = 0.0f;
-        float w[16];
-        for (int j = 0; j < topk; ++j) { w[j] = sp[(size_t)t * E + chosen[j]]; sum += w[j]; }
+        for (int j = 0; j < topk; ++j) sum += chp[j];
         for (int j = 0; j < topk; ++j) {
             idx[t * topk + j] = chosen[j];
-            wgt[t * topk + j] = w[j] / sum * route_scale;
+            wgt[t * topk + j] = chp[j] / sum * route_scale;
         }
     }
 }
@@ -327,7 +365,8 @@ hipError_t apus_launch_add_bf16(const float *a, const float *b, float *out, size
 
 __global__ __launch_bounds__(256) void apus_moe_accum_kernel(
     const float *__restrict__ eo, const float *__restrict__ wgt, int s,
-    int topk, int dim, float *__restrict__ y) {
+    int topk, int dim, float *__restrict__ y, const float *__restrict__ add_src,
+    float *__restrict__ add_out) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     const int t = blockIdx.y;
     if (i >= dim) return;
@@ -337,14 +376,17 @@ __global__ __launch_bounds__(256) void apus_moe_accum_kernel(
         acc = __fadd_rn(acc, p);
     }
     y[(size_t)t * dim + i] = acc;
+    /* optional: the sublayer output bf16(y + shared) (c/moe.h:588-589) */
+    if (add_out) add_out[(size_t)t * dim + i] = apus_bf16_rne(acc + add_src[(size_t)t * dim + i]);
     (void)s;
 }
 
 hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,
-                                 int topk, int dim, float *y, hipStream_t st) {
+                                 int topk, int dim, float *y, const float *add_src,
+                                 float *add_out, hipStream_t st) {
     if (s <= 0) return hipSuccess;
     hipLaunchKernelGGL(apus_moe_accum_kernel, dim3((dim + 255) / 256, s), dim3(256), 0, st,
-                       eo, wgt, s, topk, dim, y);
+                       eo, wgt, s, topk, dim, y, add_src, add_out);
     return hipGetLastError();
 }
 

@@ -297,6 +297,45 @@ def bench_moe(H, dev, store, layers, s, idx, wgt, steps, dim=4096, inter=2048, E
             "frac_hbm": uniq * expert_bytes / t / 1e9 / HBM_PEAK_GBS}
 
 
+def bench_moe_sublayer(H, dev, store, layers, s, steps, dim=4096, inter=2048, E=256, topk=6):
+    """The whole MoE sublayer on the device (apus_hip_moe_forward_dev): router
+    over a random fp32 gate [E, dim] with a selection bias, routed experts from
+    the store, FP8 shared expert (random bytes, read as the tiled layout), bf16
+    sum. A step is one layer's sublayer for s tokens."""
+    import ctypes as C
+    L = H.lib()
+    rng = np.random.default_rng(5)
+    gate = dev.upload((rng.standard_normal((E, dim)) / np.sqrt(dim)).astype(np.float32))
+    bias = dev.upload((rng.standard_normal(E) * 0.05).astype(np.float32))
+    sh = []
+    for O, K in ((inter, dim), (dim, inter), (inter, dim)):
+        w = dev.alloc(O * K)
+        H._check(L.apus_hip_fill_random(w.ptr, O * K, 21, len(sh), 2), "fill")
+        scl = dev.alloc((O // 128) * (K // 128))
+        H._check(L.apus_hip_fill_random(scl.ptr, (O // 128) * (K // 128), 21, 10 + len(sh), 3),
+                 "fill")
+        sh += [w, scl]
+    ml = H.ApusHipMoeLayer()
+    ml.gate_w, ml.gate_bias, ml.hash = gate.ptr, bias.ptr, 0
+    ml.route_scale, ml.limit = 2.5, 10.0
+    ml.sw1, ml.sw1s, ml.sw2, ml.sw2s, ml.sw3, ml.sw3s = (b.ptr for b in sh)
+    ml.shared_tiled = 1
+    x = rng.standard_normal((s, dim)).astype(np.float32)
+    dx = dev.upload((x.view(np.uint32) & 0xFFFF0000).view(np.float32))
+    out = dev.alloc(s * dim * 4)
+    wsp = dev.alloc(L.apus_hip_moe_forward_workspace(store, s, topk))
+
+    def step(i):
+        H._check(L.apus_hip_moe_forward_dev(store, i % layers, C.byref(ml), dx.ptr, None, s, topk,
+                                            out.ptr, None, wsp.ptr), "moe_forward")
+
+    for i in range(2):
+        step(i)
+    H.synchronize()
+    ms = timed_graph(H, step, steps)
+    return {"us": ms * 1e3 / steps}
+
+
 # ------------------------------------------------------------------ CPU baseline
 
 def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=2048, topk=6):
@@ -483,6 +522,9 @@ def main():
                            "config2_decode_us": round(d["us"], 1),
                            "config2_decode_GBs": round(d["gbs"], 1),
                            "config2_unique_experts": d["unique_experts"]})
+            for sl in (1, 64):
+                r = bench_moe_sublayer(H, dev, store, layers, sl, 64)
+                extras[f"moe_sublayer_s{sl}_us"] = round(r["us"], 1)
         if want("prefill"):
             log("[bench] config 3 prefill MoE, 512 tokens top-6 of 256, Zipf(1.1)")
             idx, wgt = zipf_routing(rng, 512, 256, 6, 1.1)

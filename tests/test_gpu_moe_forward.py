@@ -10,8 +10,14 @@ fp32 rounding, not bit for bit. The bars:
   are more than 1e-4 apart (a closer pair may swap under rounding; such
   tokens are left out of every comparison below); hash routing: equal always;
 * weights: relative 1e-5;
-* routed, shared and final outputs: max |d| / max |ref| <= 2^-7 (BF16
-  rounding of the expert linears, as in the routed-dispatch tests).
+* routed, shared and final outputs: max |d| / max |ref| <= 2^-6 and
+  mean |d| / mean |ref| <= 2^-9. Each expert is a chain of BF16-rounded
+  linears with an E4M3 re-quantisation of h between them: a one-ulp BF16
+  difference in g or u (fp32 sums in another order rounding the other way)
+  can move an h element to the neighbouring E4M3 code, a 2^-3 relative step
+  of that element, which reaches the output scaled by its weight column. A
+  single expert (the shared one) shows that as a few outputs about two BF16
+  ulps of the largest output off; the routed sum of six experts averages it.
 
 Exact ties (identical gate rows, equal bias) must pick the lowest index, as
 the CPU's strict-greater-than scan does (c/attn.h:668-686).
@@ -21,7 +27,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
-from helpers import acts, fp8_weights, max_rel, moe_experts
+from helpers import acts, bf16, fp8_weights, max_rel, moe_experts
 
 pytestmark = pytest.mark.gpu
 
@@ -119,6 +125,11 @@ def _clear_tokens(cfg, sp_ref):
     return (sel[:, k - 1] - sel[:, k]) > 1e-4
 
 
+def mean_rel(got, want):
+    want = np.asarray(want, np.float64)
+    return float(np.abs(np.asarray(got, np.float64) - want).mean() / np.abs(want).mean())
+
+
 def _compare(got, want, cfg):
     out, routed, shared, sp, idx, wgt = got
     w_out, w_routed, w_shared, w_sp, w_idx, w_wgt = want
@@ -127,9 +138,12 @@ def _compare(got, want, cfg):
     assert ok.sum() >= max(1, len(ok) // 2), "too few tokens without near-ties"
     assert np.array_equal(idx[ok], w_idx[ok])
     assert max_rel(wgt[ok], w_wgt[ok]) <= 1e-5
-    assert max_rel(shared, w_shared) <= 2.0 ** -7
-    assert max_rel(routed[ok], w_routed[ok]) <= 2.0 ** -7
-    assert max_rel(out[ok], w_out[ok]) <= 2.0 ** -7
+    for a, b in ((shared, w_shared), (routed[ok], w_routed[ok]), (out[ok], w_out[ok])):
+        assert max_rel(a, b) <= 2.0 ** -6
+        assert mean_rel(a, b) <= 2.0 ** -9
+    # the final sum, fused into the routed path's last launch, is exactly
+    # bf16(routed + shared) (c/moe.h:588-589)
+    assert np.array_equal(out.view(np.uint32), bf16(routed + shared).view(np.uint32))
 
 
 @pytest.mark.parametrize("s,topk,hash_,gate_scale", [(1, 4, 0, 1.0), (7, 4, 0, 1.0), (5, 4, 1, 1.0),
@@ -165,14 +179,18 @@ def test_moe_forward_dev_exact_ties_pick_lowest_index(hip, oracle, store1, rng):
     assert max_rel(got[0], want[0]) <= 2.0 ** -7
 
 
-@pytest.mark.parametrize("hash_,shared_tiled", [(0, True), (1, False)])
-def test_moe_forward_dev_model_shape(hip, oracle, store1, rng, hash_, shared_tiled):
-    """One decode token at the model's shape (256 experts, dim 4096, inter
-    2048, top-6), the store filled on the device; host copies of only the
-    experts the routing picks (the rest share a placeholder, which the
-    dispatch never reads)."""
+@pytest.mark.parametrize("hash_,shared_tiled,s,topk", [(0, True, 2, 6), (1, False, 1, 6),
+                                                      (0, True, 12, 6), (0, False, 3, 4)])
+def test_moe_forward_dev_model_shape(hip, oracle, store1, rng, hash_, shared_tiled, s, topk):
+    """Decode tokens at the model's shape (256 experts, dim 4096, inter 2048),
+    the store filled on the device; host copies of only the experts the
+    routing picks (the rest share a placeholder, which the dispatch never
+    reads). The cases cover each routed mode's fused final sum (per-pair
+    kernels for top-6, the sorted pipeline for 72 pairs, the ticket path for
+    top-4) and both shared-expert paths (up to 8 tokens: two fused launches;
+    more: quantise, GEMMs, SwiGLU)."""
     from test_gpu_store import host_expert
-    E, dim, inter, s, topk, seed = 256, 4096, 2048, 2, 6, 3
+    E, dim, inter, seed = 256, 4096, 2048, 3
     cfg, shared, x = _case(rng, E, dim, inter, s, topk, hash_)
     st = store1(E, dim, inter)
     hip._check(hip.lib().apus_hip_store_fill_random(st, seed), "fill")
@@ -184,3 +202,45 @@ def test_moe_forward_dev_model_shape(hip, oracle, store1, rng, hash_, shared_til
     want = oracle.moe_forward(cfg, experts, shared, x)
     got = _run_device(hip, st, cfg, shared, x, shared_tiled)
     _compare(got, want, cfg)
+
+
+def test_moe_forward_dev_graph_replays(hip, oracle, store1, rng):
+    """The sublayer captured into a HIP graph (the shared expert forks onto
+    its own stream and joins back inside the capture): each of three
+    replays, with eager launches between them, equals the eager result."""
+    E, dim, inter, s, topk, seed = 256, 4096, 2048, 1, 6, 4
+    cfg, shared, x = _case(rng, E, dim, inter, s, topk, 0)
+    st = store1(E, dim, inter)
+    L = hip.lib()
+    hip._check(L.apus_hip_store_fill_random(st, seed), "fill")
+    keep = []
+
+    def dev(a):
+        b = hip.DevBuf.from_array(a)
+        keep.append(b)
+        return b.ptr
+    ml = hip.ApusHipMoeLayer()
+    ml.gate_w, ml.gate_bias, ml.hash = dev(cfg["gate_w"]), dev(cfg["gate_bias"]), 0
+    ml.route_scale, ml.limit = cfg["route_scale"], cfg["limit"]
+    ml.sw1, ml.sw1s, ml.sw2, ml.sw2s, ml.sw3, ml.sw3s = (dev(a) for a in shared)
+    dx = dev(x)
+    out = hip.DevBuf(s * dim * 4)
+    wsp = hip.DevBuf(L.apus_hip_moe_forward_workspace(st, s, topk))
+
+    def run():
+        hip._check(L.apus_hip_moe_forward_dev(st, 0, C.byref(ml), dx, None, s, topk, out.ptr,
+                                              None, wsp.ptr), "moe_forward_dev")
+    run()
+    hip._check(L.apus_hip_synchronize(), "sync")
+    eager = out.to_array(np.float32, (s, dim)).copy()
+    hip._check(L.apus_hip_graph_begin(), "graph_begin")
+    run()
+    hip._check(L.apus_hip_graph_end(), "graph_end")
+    for _ in range(3):
+        hip._check(L.apus_hip_memset(out.ptr, 0, s * dim * 4), "memset")
+        hip._check(L.apus_hip_graph_replay(1), "replay")
+        hip._check(L.apus_hip_synchronize(), "sync")
+        got = out.to_array(np.float32, (s, dim))
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32))
+        run()                                   # eager work between replays
+        hip._check(L.apus_hip_synchronize(), "sync")
