@@ -342,7 +342,7 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
     size_t o_pair = take(nj * 4), o_tok = take(nj * 4);
     const size_t te = (size_t)E * sizeof(ApusGemmEnt);
     size_t o_e13s = take(2 * te), o_e2s = take(te), o_e13l = take(2 * te), o_e2l = take(te);
-    size_t o_g = take(nj * inter * 4), o_u = take(nj * inter * 4);
+    size_t o_g = take((nj + s) * inter * 4), o_u = take(nj * inter * 4);
     size_t o_hc = take(nj * inter), o_hs = take(nj * (inter / 128) * 4);
     size_t o_eo = take(nj * dim * 4);
     size_t o_tab = take(6 * (size_t)E * sizeof(void *));
@@ -386,11 +386,25 @@ struct MoeSlab {
     size_t stride, off[6];
 };
 
+/* whether moe_pipeline runs the one-token kernels with the FP8 shared expert
+ * fused in (its w2 needs K = inter = 2048) */
+bool moe_pair_fused(int dim, int inter, int s, int topk) {
+    return s * topk <= moe_pair_max() && (dim == 2048 || dim == 4096) && inter == 2048 &&
+           (topk == 6 || topk == 8);
+}
+
+/* the FP8 shared expert fused into the one-token MoE kernels */
+struct SharedFuse {
+    const uint8_t *w[3], *ws[3];   /* w1, w2, w3 and their tile scales */
+    int tiled;
+    float *sh_out, *out;           /* sh = bf16(w2 h); out = bf16(y + sh) */
+};
+
 int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
                  const float *x, const int32_t *idx, const float *wgt, int s,
                  int topk, float *y, const MoeWs &w, bool wtiled, const MoeSlab *slab,
                  hipStream_t st, const float *add_src = nullptr, float *add_out = nullptr,
-                 hipEvent_t add_ready = nullptr) {
+                 hipEvent_t add_ready = nullptr, const SharedFuse *shf = nullptr) {
     /* with add_out: also add_out = bf16(y + add_src), fused into the last
      * launch where it can be; add_src is complete once add_ready has fired */
     auto wait_add = [&]() {
@@ -407,7 +421,13 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
      * output columns over each token's pairs, accumulating y in (t, j) order
      * inside the workgroup */
     if (pair_shape && (topk == 6 || topk == 8)) {
+        if (shf && inter != 2048) return 1;         /* callers check moe_pair_fused() */
         ApusGemmArgs a{};
+        a.npairs = nj; a.acc_s = s;
+        if (shf) {
+            for (int i = 0; i < 3; i++) { a.shw[i] = shf->w[i]; a.shws[i] = shf->ws[i]; }
+            a.sh_tiled = shf->tiled;
+        }
         a.wtiled = wtiled;
         a.O = inter; a.K = dim; a.ldo = inter;
         a.ax = x; a.limit = limit;
@@ -432,6 +452,11 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         }
         b.acc_w = wgt; b.acc_y = y; b.acc_topk = topk; b.acc_s = s;
         b.add_src = add_out ? add_src : nullptr; b.add_out = add_out;
+        b.npairs = nj;
+        if (shf) {
+            for (int i = 0; i < 3; i++) { b.shw[i] = shf->w[i]; b.shws[i] = shf->ws[i]; }
+            b.sh_tiled = shf->tiled; b.sh_out = shf->sh_out; b.add_out = shf->out;
+        }
         if (add_out && !wait_add()) return 1;
         return launched(apus_launch_moe_pair2(&b, st), "pair w2") ? 0 : 1;
     }
@@ -1208,11 +1233,23 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
      * the side stream, beside the router and the routed experts: it needs
      * only x */
     const bool sh_tiled = ml->shared_tiled != 0;
-    if (!ok(hipEventRecord(g.side_fork, sm), "hipEventRecord") ||
-        !ok(hipStreamWaitEvent(g.side, g.side_fork, 0), "hipStreamWaitEvent") ||
-        shared_expert(ml, x, s, dim, inter, sh_tiled, w, g.side) ||
-        !ok(hipEventRecord(g.side_done, g.side), "hipEventRecord"))
+    static const bool use_side = [] {
+        const char *v = getenv("APUS_HIP_MOE_SIDE");
+        return v ? atoi(v) != 0 : true;
+    }();
+    const bool fused = moe_pair_fused(dim, inter, s, topk) && dim % 128 == 0;
+    SharedFuse shf{{ml->sw1, ml->sw2, ml->sw3}, {ml->sw1s, ml->sw2s, ml->sw3s}, sh_tiled, w.sh, out};
+    if (fused) {
+        /* the shared expert runs inside the routed pair kernels */
+    } else if (use_side) {
+        if (!ok(hipEventRecord(g.side_fork, sm), "hipEventRecord") ||
+            !ok(hipStreamWaitEvent(g.side, g.side_fork, 0), "hipStreamWaitEvent") ||
+            shared_expert(ml, x, s, dim, inter, sh_tiled, w, g.side) ||
+            !ok(hipEventRecord(g.side_done, g.side), "hipEventRecord"))
+            return 1;
+    } else if (shared_expert(ml, x, s, dim, inter, sh_tiled, w, sm)) {
         return 1;
+    }
     /* router: scores, selection, weights */
     if (!launched(apus_launch_router(ml->gate_w, ml->hash ? nullptr : ml->gate_bias, x, s, dim, E,
                                      w.sp, ml->hash ? nullptr : w.sel, sm), "router") ||
@@ -1228,7 +1265,8 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
         size_t off = 0;
         for (int i = 0; i < 6; i++) { slab.off[i] = off; off += align256(st->sz[i]); }
         if (moe_pipeline(E, dim, inter, ml->limit, st->layer_tab[layer], x, w.idx, w.wgt, s, topk,
-                         w.y, mw, st->tiled, &slab, sm, w.sh, out, g.side_done))
+                         w.y, mw, st->tiled, &slab, sm, fused ? nullptr : w.sh, fused ? nullptr : out,
+                         use_side && !fused ? g.side_done : nullptr, fused ? &shf : nullptr))
             return 1;
     }
     if (interm) {

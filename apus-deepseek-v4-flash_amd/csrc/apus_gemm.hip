@@ -922,49 +922,42 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
 }
 
 /*
- * One-token MoE dispatch kernels (few routed pairs, MXFP4 experts).
+ * One-token MoE dispatch kernels (few routed pairs, MXFP4 experts; with SH,
+ * also the FP8 shared expert of each token in the same two launches).
  *
  * w1/w3 (apus_moe_pair13_kernel): a workgroup owns 32 rows of inter for one
  * pair; each wave streams one 16-row tile of w1 or w3 over the whole K (one
  * accumulation chain, as the few-row schedule without a K split); the pair's
  * x row is quantised once while staging. The epilogue meets g and u in LDS
- * and writes h = swiglu(bf16 g, bf16 u) (c/moe.h:113-126, :198-209).
+ * and writes h = swiglu(bf16 g, bf16 u) (c/moe.h:113-126, :198-209). With SH,
+ * launch rows npairs + t do the same for token t's shared expert (FP8 w1/w3,
+ * c/moe.h:570-585) and write its h to h row npairs + t.
  *
  * w2 (apus_moe_pair2_kernel): a workgroup owns 16 columns of dim and, token by
  * token, multiplies the token's NP = topk staged h rows against their experts'
  * weights; the 4 waves split K in quarters and their partial sums meet in LDS
  * (added in part order), then y[t, o] = sum_j wgt * bf16(eo_j) in j order
  * (c/moe.h:148-158, :447-449). The weight ring runs across the pairs, so the
- * whole tile's weights are in flight at once; nothing leaves the workgroup but y.
+ * whole tile's weights are in flight at once; nothing leaves the workgroup but
+ * y. With SH, the token's shared h is staged as row NP and multiplied by the
+ * FP8 shared w2 in the same workgroup: sh = bf16(w2 h) and the sublayer
+ * output bf16(y + sh) (c/moe.h:588-589) are written too.
  */
-template <int NS>
-__global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args) {
-    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16;
+template <int WF, int NS>
+__device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const ApusStageRaw<APUS_A_F32> &raw,
+                                                 const ApusGemmEnt &ent, bool tiled, bool ok,
+                                                 int hrow, uint8_t *lcodes, uint8_t *lsc,
+                                                 float (*lgu)[2][64]) {
+    constexpr int K = NS * 512;
     constexpr int PD = 3;
-    __shared__ __align__(16) uint8_t lcodes[LDK];
-    __shared__ uint8_t lsc[NQ];
-    __shared__ float lgu[2][2][64];            /* [mat][tile][lane] */
-    if (args.zero && blockIdx.y == 0) {
-        for (int i = blockIdx.x * 256 + threadIdx.x; i < args.nzero; i += gridDim.x * 256)
-            args.zero[i] = 0u;
-    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    /* wave = 2 * tile + mat: two 16-row tiles of inter, w1 and w3 each, whole K */
     const int mat = wave & 1, tile = wave >> 1;
-    const int p = blockIdx.y;
     const int o = blockIdx.x * 32 + tile * 16 + r;
-    /* the pair's x row: its loads go out first */
-    ApusStageRaw<APUS_A_F32> raw;
-    apus_stage_load<K, APUS_A_F32>(args, nullptr, p / args.adiv, 0, 1, 0, raw);
-    const int e = apus_gld<int>(args.pidx + p);
-    const bool ok = (unsigned)e < (unsigned)args.pE;
-    ApusGemmEnt ent;
-    apus_expert_ptrs(args, mat, ok ? e : 0, ent.w, ent.ws);
-    const ApusWLane wl = apus_wlane<APUS_W_FP4>(ent, args.wtiled, o, lane, K);
-    ApusBFrag<APUS_W_FP4> ring[PD];
+    const ApusWLane wl = apus_wlane<WF>(ent, tiled, o, lane, K);
+    ApusBFrag<WF> ring[PD];
 #pragma unroll
-    for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl, u);
+    for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, u);
     apus_stage_quant<K, APUS_A_F32>(args, raw, lcodes, lsc);
     apus_lds_barrier();
     /* A row 0 is the pair's x; the other 15 rows are zero */
@@ -973,7 +966,7 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
     apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-        ApusBFrag<APUS_W_FP4> &cur = ring[s % PD];
+        ApusBFrag<WF> &cur = ring[s % PD];
 #pragma unroll
         for (int st = 0; st < 4; ++st) {
             const int q = s * 4 + st;
@@ -981,12 +974,20 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
             const uint4 a1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
             const apus_v8i a = apus_v8i{(int)a0.x & z, (int)a0.y & z, (int)a0.z & z, (int)a0.w & z,
                                         (int)a1.x & z, (int)a1.y & z, (int)a1.z & z, (int)a1.w & z};
-            const apus_v4u w = cur.w[st][0];
-            const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
-            const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
-            acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, (int)lsc[q], sb);
+            if constexpr (WF == APUS_W_FP4) {
+                const apus_v4u w = cur.w[st][0];
+                const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, (int)lsc[q], sb);
+            } else {
+                const apus_v4u w0 = cur.w[st][0], w1 = cur.w[st][1];
+                const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                            (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, (int)lsc[q],
+                                                                           (int)cur.s[st]);
+            }
         }
-        if (s + PD < NS) apus_load_b_full<APUS_W_FP4>(cur, wl, s + PD);
+        if (s + PD < NS) apus_load_b_full<WF>(cur, wl, s + PD);
     }
     /* lane (g 0, r) holds D[0][r]: this pair, inter column o. Every lane
      * stores its element (a lane-dependent store as the only consumer of the
@@ -997,23 +998,64 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
     if (threadIdx.x < 32) {
         const int t = threadIdx.x >> 4, rr = threadIdx.x & 15;
         const float h = ok ? apus_swiglu_h(lgu[0][t][rr], lgu[1][t][rr], args.limit) : 0.0f;
-        apus_gst<float>(args.pout[0] + (size_t)p * args.O + blockIdx.x * 32 + t * 16 + rr, h);
+        apus_gst<float>(args.pout[0] + (size_t)hrow * args.O + blockIdx.x * 32 + t * 16 + rr, h);
     }
 }
 
-template <int NS, int NP>
+template <int NS, bool SH>
+__global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args) {
+    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16;
+    __shared__ __align__(16) uint8_t lcodes[LDK];
+    __shared__ uint8_t lsc[NQ];
+    __shared__ float lgu[2][2][64];            /* [mat][tile][lane] */
+    if (args.zero && blockIdx.y == 0) {
+        for (int i = blockIdx.x * 256 + threadIdx.x; i < args.nzero; i += gridDim.x * 256)
+            args.zero[i] = 0u;
+    }
+    const int mat = (threadIdx.x >> 6) & 1;
+    const int p = blockIdx.y;
+    ApusStageRaw<APUS_A_F32> raw;
+    if (SH && p >= args.npairs) {
+        /* token t's shared expert: FP8 w1 / w3 */
+        const int t = p - args.npairs;
+        apus_stage_load<K, APUS_A_F32>(args, nullptr, t, 0, 1, 0, raw);
+        ApusGemmEnt ent;
+        ent.w = mat ? args.shw[2] : args.shw[0];
+        ent.ws = mat ? args.shws[2] : args.shws[0];
+        apus_pair13_body<APUS_W_FP8, NS>(args, raw, ent, args.sh_tiled, true, p, lcodes, lsc, lgu);
+        return;
+    }
+    /* the pair's x row: its loads go out first */
+    apus_stage_load<K, APUS_A_F32>(args, nullptr, p / args.adiv, 0, 1, 0, raw);
+    const int e = apus_gld<int>(args.pidx + p);
+    const bool ok = (unsigned)e < (unsigned)args.pE;
+    ApusGemmEnt ent;
+    apus_expert_ptrs(args, mat, ok ? e : 0, ent.w, ent.ws);
+    apus_pair13_body<APUS_W_FP4, NS>(args, raw, ent, args.wtiled, ok, p, lcodes, lsc, lgu);
+}
+
+template <int NS, int NP, bool SH>
 __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) {
     constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16, KS = 4, NSW = NS / KS;
     constexpr int STEPS = NP * NSW, PD = STEPS < 6 ? STEPS : (NSW == 1 ? 6 : 4);
+    constexpr int NR = NP + (SH ? 1 : 0);            /* staged h rows per token */
     static_assert(NS % KS == 0 && NP <= 8, "pair2 shape");
-    __shared__ __align__(16) uint8_t lcodes[NP * LDK];
-    __shared__ uint8_t lsc[NP * NQ];
-    __shared__ float lred[KS][NP][64];
+    static_assert(!SH || NSW == 1, "the shared w2 takes one 512-slice per wave");
+    __shared__ __align__(16) uint8_t lcodes[NR * LDK];
+    __shared__ uint8_t lsc[NR * NQ];
+    __shared__ float lred[KS][NR][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int kpart = wave;
     const int o = blockIdx.x * 16 + r;
     const int sbase = kpart * NSW;
+    /* the shared w2 stream of this lane (FP8, one 512-slice per wave) */
+    ApusWLane wsh{};
+    if constexpr (SH) {
+        ApusGemmEnt ent;
+        ent.w = args.shw[1]; ent.ws = args.shws[1];
+        wsh = apus_wlane<APUS_W_FP8>(ent, args.sh_tiled, o, lane, K);
+    }
     for (int t = 0; t < args.acc_s; ++t) {
         const int p0 = t * NP;
         apus_lds_barrier();                 /* the previous token's LDS readers are done */
@@ -1033,6 +1075,8 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
         ApusBFrag<APUS_W_FP4> ring[PD];
 #pragma unroll
         for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl[u / NSW], sbase + u % NSW);
+        ApusBFrag<APUS_W_FP8> fsh;
+        if constexpr (SH) apus_load_b_full<APUS_W_FP8>(fsh, wsh, sbase);
         apus_stage_quant<K, APUS_A_F32>(args, raw0, lcodes, lsc);
         constexpr int PASSES = (NP * NQ + 31) / 32;
 #pragma unroll
@@ -1040,6 +1084,13 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
             ApusStageRaw<APUS_A_F32> rp;
             apus_stage_load<K, APUS_A_F32>(args, nullptr, p0, 0, NP, pass, rp);
             apus_stage_quant<K, APUS_A_F32>(args, rp, lcodes, lsc);
+        }
+        if constexpr (SH) {
+            /* the shared h row (h row npairs + t) goes to LDS row NP */
+            static_assert(NQ <= 32, "one pass per shared row");
+            ApusStageRaw<APUS_A_F32> rs;
+            apus_stage_load<K, APUS_A_F32>(args, nullptr, args.npairs + t, 0, 1, 0, rs);
+            apus_stage_quant<K, APUS_A_F32>(args, rs, lcodes + NP * LDK, lsc + NP * NQ);
         }
         apus_lds_barrier();
         apus_v4f acc[NP];
@@ -1068,6 +1119,26 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
             if (stp + PD < STEPS)
                 apus_load_b_full<APUS_W_FP4>(cur, wl[(stp + PD) / NSW], sbase + (stp + PD) % NSW);
         }
+        apus_v4f accs = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (SH) {
+            /* A row NP is the shared h */
+            const int z = r == NP ? -1 : 0;
+            const uint8_t *arow = lcodes + NP * LDK + g * 16;
+            const uint8_t *asr = lsc + NP * NQ;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int q = sbase * 4 + st;
+                const uint4 a0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
+                const uint4 a1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+                const apus_v8i a = apus_v8i{(int)a0.x & z, (int)a0.y & z, (int)a0.z & z, (int)a0.w & z,
+                                            (int)a1.x & z, (int)a1.y & z, (int)a1.z & z, (int)a1.w & z};
+                const apus_v4u w0 = fsh.w[st][0], w1 = fsh.w[st][1];
+                const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                            (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                accs = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, accs, (int)asr[q],
+                                                                            (int)fsh.s[st]);
+            }
+        }
         /* pair j's result sits in D[j][r]: lane (g = j / 4, r), element j % 4.
          * Every lane stores (the reader picks the right lane): a store under a
          * lane-dependent condition would be the only consumer of the MFMA
@@ -1075,6 +1146,7 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
          * region, where a matrix instruction does not see the inactive lanes */
 #pragma unroll
         for (int j = 0; j < NP; ++j) lred[kpart][j][lane] = acc[j][j & 3];
+        if constexpr (SH) lred[kpart][NP][lane] = accs[NP & 3];
         __syncthreads();
         if (threadIdx.x < 16) {
             float y = 0.0f;
@@ -1087,19 +1159,36 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
                 eo = okj[j] ? apus_bf16_rne(eo) : 0.0f;
                 y = __fadd_rn(y, __fmul_rn(apus_gld<float>(args.acc_w + p0 + j), eo));
             }
-            const size_t o = (size_t)t * args.ldo + blockIdx.x * 16 + threadIdx.x;
-            apus_gst<float>(args.acc_y + o, y);
-            if (args.add_out) apus_gst<float>(args.add_out + o, apus_bf16_rne(y + apus_gld<float>(args.add_src + o)));
+            const size_t oo = (size_t)t * args.ldo + blockIdx.x * 16 + threadIdx.x;
+            apus_gst<float>(args.acc_y + oo, y);
+            if constexpr (SH) {
+                const int src = (NP >> 2) * 16 + threadIdx.x;
+                float sh = lred[0][NP][src];
+#pragma unroll
+                for (int kp = 1; kp < KS; ++kp) sh += lred[kp][NP][src];
+                sh = apus_bf16_rne(sh);
+                apus_gst<float>(args.sh_out + oo, sh);
+                apus_gst<float>(args.add_out + oo, apus_bf16_rne(y + sh));
+            } else if (args.add_out) {
+                apus_gst<float>(args.add_out + oo, apus_bf16_rne(y + apus_gld<float>(args.add_src + oo)));
+            }
         }
     }
 }
 
 hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t st) {
     if (npairs <= 0) return hipSuccess;
-    if ((a->K != 2048 && a->K != 4096) || a->O % 32) return hipErrorInvalidValue;
-    dim3 grid(a->O / 32, npairs), block(256);
-    if (a->K == 4096) hipLaunchKernelGGL(apus_moe_pair13_kernel<8>, grid, block, 0, st, *a);
-    else              hipLaunchKernelGGL(apus_moe_pair13_kernel<4>, grid, block, 0, st, *a);
+    if ((a->K != 2048 && a->K != 4096) || a->O % 32 || a->npairs != npairs) return hipErrorInvalidValue;
+    const bool sh = a->shw[0] != nullptr;
+    if (sh && (a->acc_s <= 0 || a->O % 128)) return hipErrorInvalidValue;
+    dim3 grid(a->O / 32, npairs + (sh ? a->acc_s : 0)), block(256);
+    if (a->K == 4096) {
+        if (sh) hipLaunchKernelGGL((apus_moe_pair13_kernel<8, true>), grid, block, 0, st, *a);
+        else    hipLaunchKernelGGL((apus_moe_pair13_kernel<8, false>), grid, block, 0, st, *a);
+    } else {
+        if (sh) hipLaunchKernelGGL((apus_moe_pair13_kernel<4, true>), grid, block, 0, st, *a);
+        else    hipLaunchKernelGGL((apus_moe_pair13_kernel<4, false>), grid, block, 0, st, *a);
+    }
     return hipGetLastError();
 }
 
@@ -1107,14 +1196,25 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
     if (a->acc_s <= 0) return hipSuccess;
     if ((a->K != 2048 && a->K != 4096) || a->O % 16 || (a->acc_topk != 6 && a->acc_topk != 8))
         return hipErrorInvalidValue;
+    const bool sh = a->shw[1] != nullptr;
+    /* the fused shared w2 needs K = 2048 (one 512-slice per wave), its
+     * outputs and the sum's destination */
+    if (sh && (a->K != 2048 || a->O % 128 || !a->sh_out || !a->add_out ||
+               a->npairs != a->acc_s * a->acc_topk))
+        return hipErrorInvalidValue;
     dim3 grid(a->O / 16), block(256);
+#define APUS_P2(NS, NP, SH) hipLaunchKernelGGL((apus_moe_pair2_kernel<NS, NP, SH>), grid, block, 0, st, *a)
     if (a->K == 4096) {
-        if (a->acc_topk == 6) hipLaunchKernelGGL((apus_moe_pair2_kernel<8, 6>), grid, block, 0, st, *a);
-        else                  hipLaunchKernelGGL((apus_moe_pair2_kernel<8, 8>), grid, block, 0, st, *a);
+        if (a->acc_topk == 6) APUS_P2(8, 6, false);
+        else                  APUS_P2(8, 8, false);
+    } else if (sh) {
+        if (a->acc_topk == 6) APUS_P2(4, 6, true);
+        else                  APUS_P2(4, 8, true);
     } else {
-        if (a->acc_topk == 6) hipLaunchKernelGGL((apus_moe_pair2_kernel<4, 6>), grid, block, 0, st, *a);
-        else                  hipLaunchKernelGGL((apus_moe_pair2_kernel<4, 8>), grid, block, 0, st, *a);
+        if (a->acc_topk == 6) APUS_P2(4, 6, false);
+        else                  APUS_P2(4, 8, false);
     }
+#undef APUS_P2
     return hipGetLastError();
 }
 

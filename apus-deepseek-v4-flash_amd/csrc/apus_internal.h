@@ -73,6 +73,14 @@ typedef struct {
      * bf16(y[t, o] + add_src[t, o]), row stride ldo */
     const float *add_src;
     float *add_out;
+    /* one-token MoE kernels: routed pairs in the launch (apus_moe_pair13 /
+     * pair2), and optionally each token's FP8 shared expert fused in: w1,
+     * w2, w3 = shw[0..2] with tile scales shws (MFMA-tiled when sh_tiled);
+     * its h goes to h row npairs + t, sh = bf16(w2 h) to sh_out, and
+     * add_out = bf16(y + sh) */
+    int npairs, sh_tiled;
+    const uint8_t *shw[3], *shws[3];
+    float *sh_out;
     unsigned *zero;          /* zeroed by workgroups of launch row 0 (the */
     int nzero;               /* tickets of a later launch) */
     /* many-row schedule work list (optional): launch row y computes rows

@@ -268,70 +268,65 @@ hipError_t apus_launch_router(const float *gate_w, const float *bias, const floa
     return hipGetLastError();
 }
 
-/* Expert choice and weights of one token per wave (c/moe.h:384-410): the
- * stable descending top-k of the selection scores (strict greater-than: the
- * lowest index wins among equal scores, each index at most once,
+/* Expert choice and weights of one token per workgroup (c/moe.h:384-410):
+ * the stable descending top-k of the selection scores (strict greater-than:
+ * the lowest index wins among equal scores, each index at most once,
  * c/attn.h:668-686), or the hash table's row for the token's id; then
  * wgt[j] = sp[idx[j]] / sum_j sp[idx[j]] * route_scale with the sum in j
- * order. Each lane holds the selection and router scores of experts lane,
- * lane + 64, ...; the winner's router score travels with it through the
- * shuffle tree, so no dependent loads follow the selection. E <= 1024,
- * topk <= 16. */
-__global__ __launch_bounds__(64) void apus_topk_kernel(
+ * order. The repeated arg-max scan of the reference picks experts in the
+ * order of the key (score descending, index ascending), so expert e lands in
+ * slot rank(e) = #{f : v_f > v_e or (v_f == v_e and f < e)} when that rank is
+ * below topk: each thread ranks its experts against 64-bit keys in LDS
+ * (branch-free compares), with no dependent chain between the slots.
+ * E <= 1024, topk <= 16. */
+__global__ __launch_bounds__(256) void apus_topk_kernel(
     const float *__restrict__ sel, const float *__restrict__ sp, int E, int topk,
     const int64_t *__restrict__ tid2eid, const int64_t *__restrict__ ids, float route_scale,
     int32_t *__restrict__ idx, float *__restrict__ wgt) {
-    const int t = blockIdx.x, lane = threadIdx.x;
+    const int t = blockIdx.x, tid = threadIdx.x;
+    __shared__ __align__(16) uint64_t lk[1024];
+    const int E4 = (E + 3) >> 2;
     __shared__ int32_t chosen[16];
     __shared__ float chp[16];
     if (tid2eid) {
-        if (lane < topk) {
-            const int e = (int)tid2eid[ids[t] * topk + lane];
-            chosen[lane] = e;
-            chp[lane] = sp[(size_t)t * E + e];
+        if (tid < topk) {
+            const int e = (int)tid2eid[ids[t] * topk + tid];
+            chosen[tid] = e;
+            chp[tid] = sp[(size_t)t * E + e];
         }
     } else {
-        float v[16], p[16];
-        unsigned used = 0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int e = lane + 64 * i;
-            v[i] = e < E ? sel[(size_t)t * E + e] : 0.0f;
-            p[i] = e < E ? sp[(size_t)t * E + e] : 0.0f;
+        /* key(e) = (order-preserving bits of the score, ~e): larger keys
+         * come first, so equal scores keep the lower index; -0 is folded
+         * into +0 (the reference's comparison treats them as equal) */
+        for (int e = tid; e < E4 * 4; e += 256) {
+            uint64_t k = 0;
+            if (e < E) {
+                const uint32_t b = __float_as_uint(sel[(size_t)t * E + e] + 0.0f);
+                const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+                k = ((uint64_t)o << 32) | (uint32_t)~(uint32_t)e;
+            }
+            lk[e] = k;
         }
-        for (int j = 0; j < topk; ++j) {
-            /* lane-local best among unused (lowest index first), then the
-             * wave's: larger value wins, equal values keep the lower index */
-            float bv = 0.0f, bp = 0.0f;
-            int bi = -1;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int e = lane + 64 * i;
-                if (e < E && !(used & (1u << i)) && (bi < 0 || v[i] > bv)) {
-                    bv = v[i]; bp = p[i]; bi = e;
-                }
+        __syncthreads();
+        for (int e = tid; e < E; e += 256) {
+            const uint64_t ke = lk[e];
+            int rank = 0;
+            for (int f2 = 0; f2 < E4 * 2; ++f2) {
+                const ulonglong2 u = *reinterpret_cast<const ulonglong2 *>(lk + 2 * f2);
+                rank += (int)(u.x > ke) + (int)(u.y > ke);
             }
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) {
-                const float ov = __shfl_xor(bv, off, 64);
-                const float op = __shfl_xor(bp, off, 64);
-                const int oi = __shfl_xor(bi, off, 64);
-                if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi < bi))) {
-                    bv = ov; bp = op; bi = oi;
-                }
+            if (rank < topk) {
+                chosen[rank] = e;
+                chp[rank] = sp[(size_t)t * E + e];
             }
-            if (lane == 0) { chosen[j] = bi; chp[j] = bp; }
-            if ((bi & 63) == lane) used |= 1u << (bi >> 6);
         }
     }
     __syncthreads();
-    if (lane == 0) {
+    if (tid < topk) {
         float sum = 0.0f;
         for (int j = 0; j < topk; ++j) sum += chp[j];
-        for (int j = 0; j < topk; ++j) {
-            idx[t * topk + j] = chosen[j];
-            wgt[t * topk + j] = chp[j] / sum * route_scale;
-        }
+        idx[t * topk + tid] = chosen[tid];
+        wgt[t * topk + tid] = chp[tid] / sum * route_scale;
     }
 }
 
@@ -340,7 +335,7 @@ hipError_t apus_launch_topk(const float *sel, const float *sp, int s, int E, int
                             int32_t *idx, float *wgt, hipStream_t st) {
     if (s <= 0) return hipSuccess;
     if (E <= 0 || E > 1024 || topk <= 0 || topk > 16 || topk > E) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(apus_topk_kernel, dim3(s), dim3(64), 0, st, sel, sp, E, topk, tid2eid, ids,
+    hipLaunchKernelGGL(apus_topk_kernel, dim3(s), dim3(256), 0, st, sel, sp, E, topk, tid2eid, ids,
                        route_scale, idx, wgt);
     return hipGetLastError();
 }
