@@ -76,6 +76,9 @@ struct State {
      * experts on this stream (forked from and joined to the caller's) */
     hipStream_t side = nullptr;
     hipEvent_t side_fork = nullptr, side_done = nullptr;
+    /* per-lane counters of the one-token MoE h hand-off (apus_moe_pair13):
+     * zeroed once here, every launch leaves them zero */
+    unsigned *pair_tk[8] = {};
     std::unordered_map<const void *, DenseW> dense;
     std::unordered_map<uint64_t, ExpertW> experts;
     DevBuf scratch[8];
@@ -91,6 +94,19 @@ bool ok(hipError_t e, const char *what) {
     if (e == hipSuccess) return true;
     set_err("%s: %s", what, hipGetErrorString(e));
     return false;
+}
+
+/* counters per lane: (pairs + tokens) x (inter / 128) groups */
+constexpr size_t PAIR_TK_CAP = 8192;
+
+bool alloc_pair_tickets(int lane) {
+    if (g.pair_tk[lane]) return true;
+    void *p = nullptr;
+    if (!ok(hipMalloc(&p, PAIR_TK_CAP * sizeof(unsigned)), "hipMalloc tickets") ||
+        !ok(hipMemset(p, 0, PAIR_TK_CAP * sizeof(unsigned)), "hipMemset tickets"))
+        return false;
+    g.pair_tk[lane] = (unsigned *)p;
+    return true;
 }
 
 bool ensure_init() {
@@ -112,6 +128,7 @@ bool ensure_init() {
     if (!ok(hipEventCreate(&g.ev1), "hipEventCreate")) return false;
     g.lane[0] = g.stream;
     if (!ok(hipEventCreateWithFlags(&g.lane_ev[0], hipEventDisableTiming), "hipEventCreate")) return false;
+    if (!alloc_pair_tickets(0)) return false;
     if (!ok(hipStreamCreateWithFlags(&g.side, hipStreamNonBlocking), "hipStreamCreate") ||
         !ok(hipEventCreateWithFlags(&g.side_fork, hipEventDisableTiming), "hipEventCreate") ||
         !ok(hipEventCreateWithFlags(&g.side_done, hipEventDisableTiming), "hipEventCreate"))
@@ -135,6 +152,13 @@ void *scratch(int i, size_t n) {
 
 /* stream of the currently selected lane (for *_dev launches) */
 hipStream_t dev_stream() { return g.lane[g.cur_lane]; }
+
+/* the h hand-off counters of the lane that owns stream st */
+unsigned *pair_tickets(hipStream_t st) {
+    for (int i = 0; i < g.nlanes; i++)
+        if (g.lane[i] == st) return g.pair_tk[i];
+    return g.pair_tk[0];
+}
 
 bool upload(void *dst, const void *src, size_t n) {
     return ok(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g.stream), "H2D");
@@ -343,7 +367,7 @@ MoeWs moe_carve(void *base, int s, int topk, int E, int dim, int inter) {
     const size_t te = (size_t)E * sizeof(ApusGemmEnt);
     size_t o_e13s = take(2 * te), o_e2s = take(te), o_e13l = take(2 * te), o_e2l = take(te);
     size_t o_g = take((nj + s) * inter * 4), o_u = take(nj * inter * 4);
-    size_t o_hc = take(nj * inter), o_hs = take(nj * (inter / 128) * 4);
+    size_t o_hc = take((nj + s) * inter), o_hs = take((nj + s) * (inter / 128) * 4);
     size_t o_eo = take(nj * dim * 4);
     size_t o_tab = take(6 * (size_t)E * sizeof(void *));
     size_t o_tk = take((size_t)(dim / 16) * sizeof(unsigned));
@@ -388,10 +412,21 @@ struct MoeSlab {
 
 /* whether moe_pipeline runs the one-token kernels with the FP8 shared expert
  * fused in (its w2 needs K = inter = 2048) */
-bool moe_pair_fused(int dim, int inter, int s, int topk) {
-    return s * topk <= moe_pair_max() && (dim == 2048 || dim == 4096) && inter == 2048 &&
-           (topk == 6 || topk == 8);
+bool moe_pair_mode(int dim, int inter, int s, int topk) {
+    return s * topk <= moe_pair_max() && (dim == 2048 || dim == 4096) &&
+           (inter == 2048 || inter == 4096) && (topk == 6 || topk == 8);
 }
+bool moe_pair_fused(int dim, int inter, int s, int topk) {
+    return moe_pair_mode(dim, inter, s, topk) && inter == 2048;
+}
+
+/* expert choice fused into the one-token w1/w3 kernel (pair mode only) */
+struct RouteFuse {
+    const float *sel, *sp;         /* [s, E] selection and router scores */
+    const int64_t *t2e, *ids;      /* hash routing (t2e set) */
+    float scale;
+    int E;
+};
 
 /* the FP8 shared expert fused into the one-token MoE kernels */
 struct SharedFuse {
@@ -404,7 +439,8 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
                  const float *x, const int32_t *idx, const float *wgt, int s,
                  int topk, float *y, const MoeWs &w, bool wtiled, const MoeSlab *slab,
                  hipStream_t st, const float *add_src = nullptr, float *add_out = nullptr,
-                 hipEvent_t add_ready = nullptr, const SharedFuse *shf = nullptr) {
+                 hipEvent_t add_ready = nullptr, const SharedFuse *shf = nullptr,
+                 const RouteFuse *rf = nullptr) {
     /* with add_out: also add_out = bf16(y + add_src), fused into the last
      * launch where it can be; add_src is complete once add_ready has fired */
     auto wait_add = [&]() {
@@ -420,10 +456,20 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
      * per (16 rows, pair) with SwiGLU in the epilogue -> h rows; w2 per 16
      * output columns over each token's pairs, accumulating y in (t, j) order
      * inside the workgroup */
+    if ((shf || rf) && !(pair_shape && (topk == 6 || topk == 8))) {
+        set_err("moe pipeline: fused shared expert / routing need the one-token kernels");
+        return 1;
+    }
     if (pair_shape && (topk == 6 || topk == 8)) {
         if (shf && inter != 2048) return 1;         /* callers check moe_pair_fused() */
         ApusGemmArgs a{};
         a.npairs = nj; a.acc_s = s;
+        if (rf) {
+            /* idx / wgt are written by the w1/w3 launch */
+            a.rsel = rf->sel; a.rsp = rf->sp; a.rt2e = rf->t2e; a.rids = rf->ids;
+            a.rscale = rf->scale; a.rE = rf->E;
+            a.ridx = const_cast<int32_t *>(idx); a.rwgt = const_cast<float *>(wgt);
+        }
         if (shf) {
             for (int i = 0; i < 3; i++) { a.shw[i] = shf->w[i]; a.shws[i] = shf->ws[i]; }
             a.sh_tiled = shf->tiled;
@@ -438,12 +484,17 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
             a.pwoff[0] = slab->off[0]; a.psoff[0] = slab->off[1];
             a.pwoff[1] = slab->off[4]; a.psoff[1] = slab->off[5];
         }
-        a.pout[0] = w.gm;                           /* h rows [nj, inter] */
+        a.pout[0] = w.gm;                           /* h rows [nj (+ s), inter] */
+        if ((size_t)(nj + s) * (inter / 128) > PAIR_TK_CAP) {
+            set_err("moe pipeline: %d pairs exceed the one-token kernels' counters", nj);
+            return 1;
+        }
+        a.hq = w.hc; a.hqs = (uint8_t *)w.hs; a.hq_tk = pair_tickets(st);
         if (!launched(apus_launch_moe_pair13(&a, nj, st), "pair w1/w3")) return 1;
         ApusGemmArgs b{};
         b.wtiled = wtiled;
         b.O = dim; b.K = inter; b.ldo = dim;
-        b.ax = w.gm;
+        b.hq = w.hc; b.hqs = (uint8_t *)w.hs;
         b.pidx = idx; b.pE = E;
         b.pw[0] = t.w2; b.pws[0] = t.w2s;
         if (slab) {
@@ -1075,7 +1126,8 @@ int apus_hip_lanes(int n) {
     if (n < 1 || n > 8) { set_err("lanes: 1..8"); return 1; }
     for (int i = g.nlanes; i < n; i++) {
         if (!ok(hipStreamCreateWithFlags(&g.lane[i], hipStreamNonBlocking), "hipStreamCreate") ||
-            !ok(hipEventCreateWithFlags(&g.lane_ev[i], hipEventDisableTiming), "hipEventCreate"))
+            !ok(hipEventCreateWithFlags(&g.lane_ev[i], hipEventDisableTiming), "hipEventCreate") ||
+            !alloc_pair_tickets(i))
             return 1;
         g.nlanes = i + 1;
     }
@@ -1238,6 +1290,9 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
         return v ? atoi(v) != 0 : true;
     }();
     const bool fused = moe_pair_fused(dim, inter, s, topk) && dim % 128 == 0;
+    const bool route_fused = moe_pair_mode(dim, inter, s, topk) && E <= 1024;
+    const RouteFuse rf{ml->hash ? nullptr : w.sel, w.sp, ml->hash ? ml->tid2eid : nullptr,
+                       ml->hash ? ids : nullptr, ml->route_scale, E};
     SharedFuse shf{{ml->sw1, ml->sw2, ml->sw3}, {ml->sw1s, ml->sw2s, ml->sw3s}, sh_tiled, w.sh, out};
     if (fused) {
         /* the shared expert runs inside the routed pair kernels */
@@ -1253,9 +1308,10 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
     /* router: scores, selection, weights */
     if (!launched(apus_launch_router(ml->gate_w, ml->hash ? nullptr : ml->gate_bias, x, s, dim, E,
                                      w.sp, ml->hash ? nullptr : w.sel, sm), "router") ||
-        !launched(apus_launch_topk(ml->hash ? nullptr : w.sel, w.sp, s, E, topk,
-                                   ml->hash ? ml->tid2eid : nullptr, ml->hash ? ids : nullptr,
-                                   ml->route_scale, w.idx, w.wgt, sm), "topk"))
+        (!route_fused &&
+         !launched(apus_launch_topk(ml->hash ? nullptr : w.sel, w.sp, s, E, topk,
+                                    ml->hash ? ml->tid2eid : nullptr, ml->hash ? ids : nullptr,
+                                    ml->route_scale, w.idx, w.wgt, sm), "topk")))
         return 1;
     /* routed experts; the last launch waits for the shared expert and also
      * writes out = bf16(routed + shared) (c/moe.h:588-589) */
@@ -1266,7 +1322,8 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
         for (int i = 0; i < 6; i++) { slab.off[i] = off; off += align256(st->sz[i]); }
         if (moe_pipeline(E, dim, inter, ml->limit, st->layer_tab[layer], x, w.idx, w.wgt, s, topk,
                          w.y, mw, st->tiled, &slab, sm, fused ? nullptr : w.sh, fused ? nullptr : out,
-                         use_side && !fused ? g.side_done : nullptr, fused ? &shf : nullptr))
+                         use_side && !fused ? g.side_done : nullptr, fused ? &shf : nullptr,
+                         route_fused ? &rf : nullptr))
             return 1;
     }
     if (interm) {

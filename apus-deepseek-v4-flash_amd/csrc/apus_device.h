@@ -110,4 +110,62 @@ __device__ __forceinline__ void apus_lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+/* Expert choice of one token by a 256-thread workgroup (c/moe.h:384-410):
+ * the stable descending top-k of the selection scores sel[0..E) (the
+ * reference's repeated arg-max with strict greater-than: the lowest index
+ * wins among equal scores, c/attn.h:668-686), or, with t2e, the hash table's
+ * row t2e[0..topk). The arg-max scan picks experts in the order of the key
+ * (score descending, index ascending), so expert e lands in slot rank(e) =
+ * #{f : key(f) > key(e)} when that rank is below topk; key(e) = (order-
+ * preserving bits of the score with -0 folded into +0, ~e) makes the
+ * comparison one 64-bit compare. Leaves chosen[j] and its router score
+ * chp[j] = sp[chosen[j]] in LDS for j < topk (visible after the final
+ * barrier). Every thread of the workgroup must call it. E <= 1024. */
+__device__ __forceinline__ void apus_route_token(const float *sel, const float *sp, int E, int topk,
+                                                 const int64_t *t2e, uint64_t *lk, int32_t *chosen,
+                                                 float *chp) {
+    const int tid = threadIdx.x;
+    if (t2e) {
+        if (tid < topk) {
+            const int e = (int)t2e[tid];
+            chosen[tid] = e;
+            chp[tid] = sp[e];
+        }
+    } else {
+        const int E4 = (E + 3) >> 2;
+        for (int e = tid; e < E4 * 4; e += 256) {
+            uint64_t k = 0;
+            if (e < E) {
+                const uint32_t b = __float_as_uint(sel[e] + 0.0f);
+                const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+                k = ((uint64_t)o << 32) | (uint32_t)~(uint32_t)e;
+            }
+            lk[e] = k;
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += 256) {
+            const uint64_t ke = lk[e];
+            int rank = 0;
+            for (int f2 = 0; f2 < E4 * 2; ++f2) {
+                const ulonglong2 u = *reinterpret_cast<const ulonglong2 *>(lk + 2 * f2);
+                rank += (int)(u.x > ke) + (int)(u.y > ke);
+            }
+            if (rank < topk) {
+                chosen[rank] = e;
+                chp[rank] = sp[e];
+            }
+        }
+    }
+    __syncthreads();
+}
+
+/* wgt[j] = chp[j] / sum_j' chp[j'] * route_scale, the sum in j order
+ * (c/moe.h:400-410) */
+__device__ __forceinline__ float apus_route_weight(const float *chp, int topk, int j,
+                                                   float route_scale) {
+    float sum = 0.0f;
+    for (int i = 0; i < topk; ++i) sum += chp[i];
+    return chp[j] / sum * route_scale;
+}
+
 #endif /* APUS_DEVICE_H */

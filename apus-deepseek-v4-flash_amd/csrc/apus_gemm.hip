@@ -995,10 +995,55 @@ __device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const
      * pick the g == 0 lanes of the w1 and w3 waves */
     lgu[mat][tile][lane] = apus_bf16_rne(acc[0]);
     __syncthreads();
+    float *hdst = args.pout[0] + (size_t)hrow * args.O;
     if (threadIdx.x < 32) {
         const int t = threadIdx.x >> 4, rr = threadIdx.x & 15;
         const float h = ok ? apus_swiglu_h(lgu[0][t][rr], lgu[1][t][rr], args.limit) : 0.0f;
-        apus_gst<float>(args.pout[0] + (size_t)hrow * args.O + blockIdx.x * 32 + t * 16 + rr, h);
+        float *dst = hdst + blockIdx.x * 32 + t * 16 + rr;
+        if (args.hq) /* device-coherent: the group's last workgroup reads it */
+            __hip_atomic_store(dst, h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+            apus_gst<float>(dst, h);
+    }
+    if (!args.hq) return;
+    /* The four workgroups of a 128-column group take tickets once their h
+     * stores have completed; the last one quantises the group as the
+     * activation quantiser does (c/fp4.h:293-321: BF16, amax, E8M0 scale,
+     * E4M3 codes), reading the h values with device-coherent loads, and
+     * returns the counter to zero for the next launch. */
+    __shared__ int last;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int G = args.O >> 7, gq = blockIdx.x >> 2;
+    unsigned *tk = args.hq_tk + (size_t)hrow * G + gq;
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 3u;
+    __syncthreads();
+    if (!last || threadIdx.x >= 8) return;
+    const float *src = hdst + gq * 128 + threadIdx.x * 16;
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        v[i] = apus_bf16_rne(__hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    const uint32_t e = apus_act_scale_exp(m);
+    const float inv = apus_inv_pow2_from_exp(e);
+    uint32_t w4[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        w4[i] = apus_e4m3_code(v[4 * i] * inv) | (apus_e4m3_code(v[4 * i + 1] * inv) << 8) |
+                (apus_e4m3_code(v[4 * i + 2] * inv) << 16) |
+                (apus_e4m3_code(v[4 * i + 3] * inv) << 24);
+    apus_gst<apus_v4u>(args.hq + (size_t)hrow * args.O + gq * 128 + threadIdx.x * 16,
+                       apus_v4u{w4[0], w4[1], w4[2], w4[3]});
+    if (threadIdx.x == 0) {
+        apus_gst<uint8_t>(args.hqs + (size_t)hrow * G + gq, (uint8_t)e);
+        __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -1027,7 +1072,24 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
     }
     /* the pair's x row: its loads go out first */
     apus_stage_load<K, APUS_A_F32>(args, nullptr, p / args.adiv, 0, 1, 0, raw);
-    const int e = apus_gld<int>(args.pidx + p);
+    int e;
+    if (args.rsp) {
+        __shared__ __align__(16) uint64_t lk[1024];
+        __shared__ int32_t chosen[16];
+        __shared__ float chp[16];
+        const int t = p / args.adiv, j = p - t * args.adiv;
+        apus_route_token(args.rt2e ? nullptr : args.rsel + (size_t)t * args.rE,
+                         args.rsp + (size_t)t * args.rE, args.rE, args.adiv,
+                         args.rt2e ? args.rt2e + apus_gld<int64_t>(args.rids + t) * args.adiv : nullptr,
+                         lk, chosen, chp);
+        e = chosen[j];
+        if (blockIdx.x == 0 && threadIdx.x == 0) {
+            apus_gst<int>(args.ridx + p, e);
+            apus_gst<float>(args.rwgt + p, apus_route_weight(chp, args.adiv, j, args.rscale));
+        }
+    } else {
+        e = apus_gld<int>(args.pidx + p);
+    }
     const bool ok = (unsigned)e < (unsigned)args.pE;
     ApusGemmEnt ent;
     apus_expert_ptrs(args, mat, ok ? e : 0, ent.w, ent.ws);
@@ -1036,13 +1098,11 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
 
 template <int NS, int NP, bool SH>
 __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) {
-    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16, KS = 4, NSW = NS / KS;
+    constexpr int K = NS * 512, NQ = NS * 4, KS = 4, NSW = NS / KS;
     constexpr int STEPS = NP * NSW, PD = STEPS < 6 ? STEPS : (NSW == 1 ? 6 : 4);
-    constexpr int NR = NP + (SH ? 1 : 0);            /* staged h rows per token */
+    constexpr int NR = NP + (SH ? 1 : 0);            /* A rows per token */
     static_assert(NS % KS == 0 && NP <= 8, "pair2 shape");
     static_assert(!SH || NSW == 1, "the shared w2 takes one 512-slice per wave");
-    __shared__ __align__(16) uint8_t lcodes[NR * LDK];
-    __shared__ uint8_t lsc[NR * NQ];
     __shared__ float lred[KS][NR][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -1058,10 +1118,26 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
     }
     for (int t = 0; t < args.acc_s; ++t) {
         const int p0 = t * NP;
-        apus_lds_barrier();                 /* the previous token's LDS readers are done */
-        /* the token's NP h rows: first pass's loads before the expert lookups */
-        ApusStageRaw<APUS_A_F32> raw0;
-        apus_stage_load<K, APUS_A_F32>(args, nullptr, p0, 0, NP, 0, raw0);
+        /* A operands straight from the quantised h rows: lane (r, g) holds
+         * row r's codes for its K sub-blocks (pair r, or the shared h as row
+         * NP); an MFMA for pair j masks every row but j */
+        const bool arow = r < NR;
+        const int hr = r < NP ? p0 + r : args.npairs + t;
+        const uint8_t *ab = args.hq + (size_t)(arow ? hr : p0) * K + g * 16;
+        uint4 av[NSW][4][2];
+        unsigned asv[NSW];
+#pragma unroll
+        for (int si = 0; si < NSW; ++si) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int q = (sbase + si) * 4 + st;
+                av[si][st][0] = apus_gld<uint4>(ab + q * 128);
+                av[si][st][1] = apus_gld<uint4>(ab + q * 128 + 64);
+            }
+            /* rows that feed no MFMA get a finite scale (their codes are masked) */
+            asv[si] = arow ? apus_gld<unsigned>(args.hqs + (size_t)hr * NQ + (sbase + si) * 4)
+                           : 0x7f7f7f7fu;
+        }
         ApusWLane wl[NP];
         bool okj[NP];
 #pragma unroll
@@ -1077,68 +1153,45 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
         for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl[u / NSW], sbase + u % NSW);
         ApusBFrag<APUS_W_FP8> fsh;
         if constexpr (SH) apus_load_b_full<APUS_W_FP8>(fsh, wsh, sbase);
-        apus_stage_quant<K, APUS_A_F32>(args, raw0, lcodes, lsc);
-        constexpr int PASSES = (NP * NQ + 31) / 32;
-#pragma unroll
-        for (int pass = 1; pass < PASSES; ++pass) {
-            ApusStageRaw<APUS_A_F32> rp;
-            apus_stage_load<K, APUS_A_F32>(args, nullptr, p0, 0, NP, pass, rp);
-            apus_stage_quant<K, APUS_A_F32>(args, rp, lcodes, lsc);
-        }
-        if constexpr (SH) {
-            /* the shared h row (h row npairs + t) goes to LDS row NP */
-            static_assert(NQ <= 32, "one pass per shared row");
-            ApusStageRaw<APUS_A_F32> rs;
-            apus_stage_load<K, APUS_A_F32>(args, nullptr, args.npairs + t, 0, 1, 0, rs);
-            apus_stage_quant<K, APUS_A_F32>(args, rs, lcodes + NP * LDK, lsc + NP * NQ);
-        }
-        apus_lds_barrier();
         apus_v4f acc[NP];
 #pragma unroll
         for (int j = 0; j < NP; ++j) acc[j] = apus_v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int stp = 0; stp < STEPS; ++stp) {
-            const int j = stp / NSW, s = sbase + stp % NSW;
+            const int j = stp / NSW, si = stp % NSW;
             ApusBFrag<APUS_W_FP4> &cur = ring[stp % PD];
-            /* A row j is pair j's h; the other rows are zero */
             const int z = r == j ? -1 : 0;
-            const uint8_t *arow = lcodes + j * LDK + g * 16;
-            const uint8_t *asr = lsc + j * NQ;
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                const int q = s * 4 + st;
-                const uint4 a0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
-                const uint4 a1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+                const uint4 a0 = av[si][st][0], a1 = av[si][st][1];
                 const apus_v8i a = apus_v8i{(int)a0.x & z, (int)a0.y & z, (int)a0.z & z, (int)a0.w & z,
                                             (int)a1.x & z, (int)a1.y & z, (int)a1.z & z, (int)a1.w & z};
                 const apus_v4u w = cur.w[st][0];
                 const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                const int sa = (int)((asv[si] >> (8 * st)) & 0xffu);
                 const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
-                acc[j] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[j], (int)asr[q], sb);
+                acc[j] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[j], sa, sb);
             }
             if (stp + PD < STEPS)
                 apus_load_b_full<APUS_W_FP4>(cur, wl[(stp + PD) / NSW], sbase + (stp + PD) % NSW);
         }
         apus_v4f accs = {0.f, 0.f, 0.f, 0.f};
         if constexpr (SH) {
-            /* A row NP is the shared h */
             const int z = r == NP ? -1 : 0;
-            const uint8_t *arow = lcodes + NP * LDK + g * 16;
-            const uint8_t *asr = lsc + NP * NQ;
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                const int q = sbase * 4 + st;
-                const uint4 a0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
-                const uint4 a1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+                const uint4 a0 = av[0][st][0], a1 = av[0][st][1];
                 const apus_v8i a = apus_v8i{(int)a0.x & z, (int)a0.y & z, (int)a0.z & z, (int)a0.w & z,
                                             (int)a1.x & z, (int)a1.y & z, (int)a1.z & z, (int)a1.w & z};
                 const apus_v4u w0 = fsh.w[st][0], w1 = fsh.w[st][1];
                 const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
                                             (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
-                accs = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, accs, (int)asr[q],
+                const int sa = (int)((asv[0] >> (8 * st)) & 0xffu);
+                accs = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, accs, sa,
                                                                             (int)fsh.s[st]);
             }
         }
+        apus_lds_barrier();                 /* the previous token's lred readers are done */
         /* pair j's result sits in D[j][r]: lane (g = j / 4, r), element j % 4.
          * Every lane stores (the reader picks the right lane): a store under a
          * lane-dependent condition would be the only consumer of the MFMA
@@ -1178,9 +1231,14 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
 
 hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t st) {
     if (npairs <= 0) return hipSuccess;
-    if ((a->K != 2048 && a->K != 4096) || a->O % 32 || a->npairs != npairs) return hipErrorInvalidValue;
+    if ((a->K != 2048 && a->K != 4096) || a->O % 128 || a->npairs != npairs ||
+        (a->hq && (!a->hqs || !a->hq_tk)))
+        return hipErrorInvalidValue;
     const bool sh = a->shw[0] != nullptr;
     if (sh && (a->acc_s <= 0 || a->O % 128)) return hipErrorInvalidValue;
+    if (a->rsp && (a->rE <= 0 || a->rE > 1024 || a->adiv > 16 || a->adiv > a->rE || !a->ridx ||
+                   !a->rwgt || (!a->rt2e && !a->rsel) || (a->rt2e && !a->rids)))
+        return hipErrorInvalidValue;
     dim3 grid(a->O / 32, npairs + (sh ? a->acc_s : 0)), block(256);
     if (a->K == 4096) {
         if (sh) hipLaunchKernelGGL((apus_moe_pair13_kernel<8, true>), grid, block, 0, st, *a);
@@ -1194,7 +1252,8 @@ hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t
 
 hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
     if (a->acc_s <= 0) return hipSuccess;
-    if ((a->K != 2048 && a->K != 4096) || a->O % 16 || (a->acc_topk != 6 && a->acc_topk != 8))
+    if ((a->K != 2048 && a->K != 4096) || a->O % 16 || (a->acc_topk != 6 && a->acc_topk != 8) ||
+        !a->hq || !a->hqs || a->npairs < a->acc_s * a->acc_topk)
         return hipErrorInvalidValue;
     const bool sh = a->shw[1] != nullptr;
     /* the fused shared w2 needs K = 2048 (one 512-slice per wave), its

@@ -81,6 +81,23 @@ typedef struct {
     int npairs, sh_tiled;
     const uint8_t *shw[3], *shws[3];
     float *sh_out;
+    /* apus_moe_pair13 with rsp set: each workgroup chooses its pair's expert
+     * itself (apus_route_token over token t's selection scores rsel[t] or
+     * the hash row rt2e[rids[t]]), and the workgroups of column block 0
+     * write the choice and its weight to ridx / rwgt (the w2 launch's pidx
+     * and acc_w) */
+    /* one-token MoE h hand-off: apus_moe_pair13 quantises h per 128-group
+     * (E4M3 codes hq [rows, O], E8M0 bytes hqs [rows, O/128]) through
+     * hq_tk, one counter per (row, group), zero at launch and left zero;
+     * apus_moe_pair2 reads its A operands straight from hq / hqs */
+    uint8_t *hq, *hqs;
+    unsigned *hq_tk;
+    const float *rsel, *rsp;
+    const int64_t *rt2e, *rids;
+    float rscale;
+    int rE;
+    int32_t *ridx;
+    float *rwgt;
     unsigned *zero;          /* zeroed by workgroups of launch row 0 (the */
     int nzero;               /* tickets of a later launch) */
     /* many-row schedule work list (optional): launch row y computes rows

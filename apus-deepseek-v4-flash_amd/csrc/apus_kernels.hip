@@ -268,65 +268,21 @@ hipError_t apus_launch_router(const float *gate_w, const float *bias, const floa
     return hipGetLastError();
 }
 
-/* Expert choice and weights of one token per workgroup (c/moe.h:384-410):
- * the stable descending top-k of the selection scores (strict greater-than:
- * the lowest index wins among equal scores, each index at most once,
- * c/attn.h:668-686), or the hash table's row for the token's id; then
- * wgt[j] = sp[idx[j]] / sum_j sp[idx[j]] * route_scale with the sum in j
- * order. The repeated arg-max scan of the reference picks experts in the
- * order of the key (score descending, index ascending), so expert e lands in
- * slot rank(e) = #{f : v_f > v_e or (v_f == v_e and f < e)} when that rank is
- * below topk: each thread ranks its experts against 64-bit keys in LDS
- * (branch-free compares), with no dependent chain between the slots.
- * E <= 1024, topk <= 16. */
+/* Expert choice and weights of one token per workgroup (apus_route_token;
+ * c/moe.h:384-410): idx[t, j] and wgt[t, j] = sp[idx[t, j]] / sum * route_scale. */
 __global__ __launch_bounds__(256) void apus_topk_kernel(
     const float *__restrict__ sel, const float *__restrict__ sp, int E, int topk,
     const int64_t *__restrict__ tid2eid, const int64_t *__restrict__ ids, float route_scale,
     int32_t *__restrict__ idx, float *__restrict__ wgt) {
     const int t = blockIdx.x, tid = threadIdx.x;
     __shared__ __align__(16) uint64_t lk[1024];
-    const int E4 = (E + 3) >> 2;
     __shared__ int32_t chosen[16];
     __shared__ float chp[16];
-    if (tid2eid) {
-        if (tid < topk) {
-            const int e = (int)tid2eid[ids[t] * topk + tid];
-            chosen[tid] = e;
-            chp[tid] = sp[(size_t)t * E + e];
-        }
-    } else {
-        /* key(e) = (order-preserving bits of the score, ~e): larger keys
-         * come first, so equal scores keep the lower index; -0 is folded
-         * into +0 (the reference's comparison treats them as equal) */
-        for (int e = tid; e < E4 * 4; e += 256) {
-            uint64_t k = 0;
-            if (e < E) {
-                const uint32_t b = __float_as_uint(sel[(size_t)t * E + e] + 0.0f);
-                const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-                k = ((uint64_t)o << 32) | (uint32_t)~(uint32_t)e;
-            }
-            lk[e] = k;
-        }
-        __syncthreads();
-        for (int e = tid; e < E; e += 256) {
-            const uint64_t ke = lk[e];
-            int rank = 0;
-            for (int f2 = 0; f2 < E4 * 2; ++f2) {
-                const ulonglong2 u = *reinterpret_cast<const ulonglong2 *>(lk + 2 * f2);
-                rank += (int)(u.x > ke) + (int)(u.y > ke);
-            }
-            if (rank < topk) {
-                chosen[rank] = e;
-                chp[rank] = sp[(size_t)t * E + e];
-            }
-        }
-    }
-    __syncthreads();
+    apus_route_token(tid2eid ? nullptr : sel + (size_t)t * E, sp + (size_t)t * E, E, topk,
+                     tid2eid ? tid2eid + ids[t] * topk : nullptr, lk, chosen, chp);
     if (tid < topk) {
-        float sum = 0.0f;
-        for (int j = 0; j < topk; ++j) sum += chp[j];
         idx[t * topk + tid] = chosen[tid];
-        wgt[t * topk + tid] = chp[tid] / sum * route_scale;
+        wgt[t * topk + tid] = apus_route_weight(chp, topk, tid, route_scale);
     }
 }
 
