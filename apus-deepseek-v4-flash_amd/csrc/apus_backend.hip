@@ -1340,6 +1340,19 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
     return 0;
 }
 
+int apus_hip_check_e4m3_hw(unsigned *mismatches, unsigned *last_bad_bits) {
+    if (!ensure_init()) return 1;
+    unsigned *d = (unsigned *)scratch(7, 2 * sizeof(unsigned));
+    if (!d || !ok(hipMemsetAsync(d, 0, 2 * sizeof(unsigned), g.stream), "memset") ||
+        !launched(apus_launch_e4m3_hw_check(d, d + 1, g.stream), "e4m3 check"))
+        return 1;
+    unsigned h[2];
+    if (!download(h, d, sizeof h) || !finish()) return 1;
+    if (mismatches) *mismatches = h[0];
+    if (last_bad_bits) *last_bad_bits = h[1];
+    return 0;
+}
+
 float apus_hip_host_bf16_round(float x) { return apus_bf16_rne(x); }
 uint8_t apus_hip_host_e4m3_quant(float x) { return (uint8_t)apus_e4m3_code(x); }
 float apus_hip_host_act_scale(float amax) { return apus_pow2_from_exp(apus_act_scale_exp(amax)); }

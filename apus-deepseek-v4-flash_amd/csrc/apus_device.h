@@ -110,6 +110,19 @@ __device__ __forceinline__ void apus_lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+/* Two or four E4M3 codes (bytes a, b[, c, d] in order) by the hardware conversion,
+ * round-to-nearest-even. Equal to apus_e4m3_code for every fp32 input with
+ * |x| <= 448 (checked exhaustively on the device by
+ * apus_hip_check_e4m3_hw); callers pass values already scaled into that range
+ * (activation groups: |v| / s <= 448 by the choice of s). */
+__device__ __forceinline__ uint32_t apus_e4m3_pack2_hw(float a, float b) {
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false) & 0xffffu;
+}
+__device__ __forceinline__ uint32_t apus_e4m3_pack4_hw(float a, float b, float c, float d) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
 /* Expert choice of one token by a 256-thread workgroup (c/moe.h:384-410):
  * the stable descending top-k of the selection scores sel[0..E) (the
  * reference's repeated arg-max with strict greater-than: the lowest index

@@ -429,9 +429,8 @@ __device__ __forceinline__ void apus_stage_quant(const ApusGemmArgs &a, const Ap
     uint32_t w4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        w4[i] = apus_e4m3_code(v[4 * i] * inv) | (apus_e4m3_code(v[4 * i + 1] * inv) << 8) |
-                (apus_e4m3_code(v[4 * i + 2] * inv) << 16) |
-                (apus_e4m3_code(v[4 * i + 3] * inv) << 24);
+        w4[i] = apus_e4m3_pack4_hw(v[4 * i] * inv, v[4 * i + 1] * inv, v[4 * i + 2] * inv,
+                                   v[4 * i + 3] * inv);
     *reinterpret_cast<uint4 *>(lcodes + r.row * LDK + r.q * 128 + sub * 16) =
         uint4{w4[0], w4[1], w4[2], w4[3]};
     if (sub == 0) lsc[r.row * NQ + r.q] = (uint8_t)e;
@@ -1036,9 +1035,8 @@ __device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const
     uint32_t w4[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        w4[i] = apus_e4m3_code(v[4 * i] * inv) | (apus_e4m3_code(v[4 * i + 1] * inv) << 8) |
-                (apus_e4m3_code(v[4 * i + 2] * inv) << 16) |
-                (apus_e4m3_code(v[4 * i + 3] * inv) << 24);
+        w4[i] = apus_e4m3_pack4_hw(v[4 * i] * inv, v[4 * i + 1] * inv, v[4 * i + 2] * inv,
+                                   v[4 * i + 3] * inv);
     apus_gst<apus_v4u>(args.hq + (size_t)hrow * args.O + gq * 128 + threadIdx.x * 16,
                        apus_v4u{w4[0], w4[1], w4[2], w4[3]});
     if (threadIdx.x == 0) {

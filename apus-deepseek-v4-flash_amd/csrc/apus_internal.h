@@ -190,6 +190,8 @@ hipError_t apus_launch_router(const float *gate_w, const float *bias, const floa
 hipError_t apus_launch_topk(const float *sel, const float *sp, int s, int E, int topk,
                             const int64_t *tid2eid, const int64_t *ids, float route_scale,
                             int32_t *idx, float *wgt, hipStream_t st);
+/* hardware E4M3 conversion vs the integer encoder over |x| <= 448 */
+hipError_t apus_launch_e4m3_hw_check(unsigned *bad, unsigned *last_bad, hipStream_t st);
 /* out = bf16(a + b) */
 hipError_t apus_launch_add_bf16(const float *a, const float *b, float *out, size_t n,
                                 hipStream_t st);

@@ -30,9 +30,8 @@ __global__ __launch_bounds__(256) void apus_act_quant_kernel(
     const float amax = apus_wave_max(fmaxf(fabsf(v0), fabsf(v1)));
     const uint32_t e = apus_act_scale_exp(amax);
     const float inv = apus_inv_pow2_from_exp(e);
-    const uint32_t c0 = apus_e4m3_code(v0 * inv), c1 = apus_e4m3_code(v1 * inv);
     *reinterpret_cast<uint16_t *>(codes + (size_t)m * K + b * 128 + lane * 2) =
-        (uint16_t)(c0 | (c1 << 8));
+        (uint16_t)apus_e4m3_pack2_hw(v0 * inv, v1 * inv);
     if (lane == 0) scales[(size_t)m * nab + b] = apus_pow2_from_exp(e);
 }
 
@@ -64,8 +63,7 @@ __global__ __launch_bounds__(256) void apus_swiglu_quant_kernel(
     const float amax = apus_wave_max(fmaxf(fabsf(h[0]), fabsf(h[1])));
     const uint32_t e = apus_act_scale_exp(amax);
     const float inv = apus_inv_pow2_from_exp(e);
-    const uint32_t c0 = apus_e4m3_code(h[0] * inv), c1 = apus_e4m3_code(h[1] * inv);
-    *reinterpret_cast<uint16_t *>(codes + off) = (uint16_t)(c0 | (c1 << 8));
+    *reinterpret_cast<uint16_t *>(codes + off) = (uint16_t)apus_e4m3_pack2_hw(h[0] * inv, h[1] * inv);
     if (lane == 0) scales[(size_t)m * nab + b] = apus_pow2_from_exp(e);
 }
 
@@ -338,6 +336,36 @@ hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,
     if (s <= 0) return hipSuccess;
     hipLaunchKernelGGL(apus_moe_accum_kernel, dim3((dim + 255) / 256, s), dim3(256), 0, st,
                        eo, wgt, s, topk, dim, y, add_src, add_out);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------- E4M3 conversion check */
+
+/* Every fp32 input x with |x| <= 448 (both signs): the hardware conversion
+ * (apus_e4m3_pack4_hw) against apus_e4m3_code; counts mismatches and keeps
+ * the largest mismatching input bits. */
+__global__ __launch_bounds__(256) void apus_e4m3_hw_check_kernel(uint32_t n, unsigned *bad,
+                                                                 unsigned *last_bad) {
+    const uint32_t i0 = (blockIdx.x * 256u + threadIdx.x) * 2u;
+    unsigned nbad = 0, lb = 0;
+    if (i0 < n) {
+        const float x0 = __uint_as_float(i0), x1 = __uint_as_float(i0 + 1 < n ? i0 + 1 : i0);
+        const uint32_t hw = apus_e4m3_pack4_hw(x0, x1, -x0, -x1);
+        const uint32_t sw = apus_e4m3_code(x0) | (apus_e4m3_code(x1) << 8) |
+                            (apus_e4m3_code(-x0) << 16) | (apus_e4m3_code(-x1) << 24);
+        if (hw != sw) { nbad = 1; lb = i0; }
+    }
+    if (nbad) {
+        __hip_atomic_fetch_add(bad, nbad, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_max(last_bad, lb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+hipError_t apus_launch_e4m3_hw_check(unsigned *bad, unsigned *last_bad, hipStream_t st) {
+    const uint32_t n = 0x43e00001u;                  /* bits of 448.0f, inclusive */
+    const uint32_t pairs = (n + 1) / 2;
+    hipLaunchKernelGGL(apus_e4m3_hw_check_kernel, dim3((pairs + 255) / 256), dim3(256), 0, st, n,
+                       bad, last_bad);
     return hipGetLastError();
 }
 

@@ -326,6 +326,13 @@ const char *apus_hip_last_error(void);
 /* Device name and compute-unit count of the current device. */
 int   apus_hip_device_info(char *name, size_t cap, int *cus);
 
+/* Device self-check: the hardware E4M3 conversion the kernels use for
+ * activation codes equals the integer round-to-nearest-even encoder
+ * (apus_hip_host_e4m3_quant, c/fp4.h:219-253) for every fp32 input with
+ * |x| <= 448, both signs. No counterpart in the reference: it proves the
+ * precondition of using the hardware instruction. Synchronous. */
+int   apus_hip_check_e4m3_hw(unsigned *mismatches, unsigned *last_bad_bits);
+
 /* ---- host twins of the device numerics (no GPU needed) ---- */
 float    apus_hip_host_bf16_round(float x);
 uint8_t  apus_hip_host_e4m3_quant(float x);

@@ -60,3 +60,14 @@ def test_fp8_decode_every_code(hip, oracle):
         for i, k in enumerate((0, 1)):
             want = np.float32(oracle.e4m3_dequant(int(w[o, k])) * oracle.ue8m0(int(ws[o // 128, 0])))
             assert abs(got[i, o]) == abs(want) and (want == 0 or np.sign(got[i, o]) == np.sign(want)), (o, k)
+
+
+def test_hw_e4m3_conversion_exhaustive(hip):
+    """The hardware E4M3 conversion that quantises activations inside the
+    one-token MoE kernels equals the integer round-to-nearest-even encoder
+    (itself equal to the reference's apus_e4m3_quant_f32 for all 2^32
+    inputs, on the host) for every fp32 input with |x| <= 448."""
+    import ctypes as C
+    bad, last = C.c_uint(), C.c_uint()
+    hip._check(hip.lib().apus_hip_check_e4m3_hw(C.byref(bad), C.byref(last)), "check")
+    assert bad.value == 0, f"{bad.value} mismatches, e.g. bits {last.value:#010x}"
