@@ -90,6 +90,11 @@ class ApusHipMoeInterm(C.Structure):
     _fields_ = [("router_scores", vp), ("router_idx", vp), ("router_w", vp),
                 ("moe_routed", vp), ("moe_shared", vp)]
 
+class ApusHipSlabRec(C.Structure):
+    """One routed expert's slab in an apus container (include/apus_hip.h)."""
+    _fields_ = [("shard", C.c_int32), ("pad", C.c_int32), ("off", C.c_uint64), ("len", C.c_uint64),
+                ("rel", C.c_uint32 * 6), ("O", C.c_int64 * 3), ("K", C.c_int64 * 3)]
+
 # entry point -> (restype, argtypes); exactly the declarations of include/apus_hip.h
 SIGNATURES = {
     "apus_hip_enable": (C.c_int, [C.c_char_p, C.c_size_t]),
@@ -133,6 +138,12 @@ SIGNATURES = {
     "apus_hip_moe_forward_dev": (C.c_int, [vp, C.c_int, C.POINTER(ApusHipMoeLayer), vp, vp,
                                            C.c_int, C.c_int, vp, C.POINTER(ApusHipMoeInterm),
                                            vp]),
+    "apus_hip_container_open": (vp, [C.c_char_p, C.c_int, C.c_int, C.c_int, C.c_char_p,
+                                     C.c_size_t]),
+    "apus_hip_container_close": (None, [vp]),
+    "apus_hip_container_slab": (C.c_int, [vp, C.c_int, C.c_int, C.POINTER(ApusHipSlabRec)]),
+    "apus_hip_container_shard": (C.c_char_p, [vp, C.c_int]),
+    "apus_hip_store_load": (C.c_int, [vp, vp, C.c_int, C.c_char_p, C.c_size_t]),
     "apus_hip_malloc": (vp, [C.c_size_t]),
     "apus_hip_free": (C.c_int, [vp]),
     "apus_hip_h2d": (C.c_int, [vp, vp, C.c_size_t]),

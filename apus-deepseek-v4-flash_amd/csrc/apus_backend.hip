@@ -18,12 +18,20 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <fcntl.h>
+#include <unistd.h>
+
 #include <algorithm>
+#include <atomic>
+#include <condition_variable>
+#include <deque>
 #include <mutex>
+#include <thread>
 #include <unordered_map>
 #include <vector>
 
 #include "../../include/apus_hip.h"
+#include "apus_container.h"
 #include "apus_internal.h"
 #include "apus_numerics.h"
 
@@ -1031,6 +1039,182 @@ int apus_hip_store_put(ApusHipStore *st, int layer, int eid, const ApusFp4W *w1,
         g.bytes_uploaded += st->sz[2 * m] + st->sz[2 * m + 1];
     }
     return finish() ? 0 : 1;
+}
+
+/* Container slabs -> the store. io_threads readers pread whole slabs into a
+ * ring of pinned host buffers; this thread uploads each filled buffer with
+ * asynchronous copies (through a device staging slab and the pack kernel when
+ * the store is MFMA-tiled) and hands the buffer back once its copies are done.
+ * Shapes are checked against the store before anything is read. */
+int apus_hip_store_load(ApusHipStore *st, const ApusHipContainer *c, int io_threads, char *err,
+                        size_t errcap) {
+    auto fail = [&](const char *fmt, ...) {
+        char m[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(m, sizeof m, fmt, ap);
+        va_end(ap);
+        set_err("%s", m);
+        if (err && errcap) snprintf(err, errcap, "%s", m);
+        return 1;
+    };
+    if (!st || !c) return fail("store_load: bad arguments");
+    if (c->n_layers != st->L || c->E != st->E)
+        return fail("store_load: container has %d layers x %d experts, store %d x %d", c->n_layers,
+                    c->E, st->L, st->E);
+    const int64_t wantO[3] = {st->inter, st->dim, st->inter}, wantK[3] = {st->dim, st->inter, st->dim};
+    const size_t n = c->recs.size();
+    for (size_t i = 0; i < n; i++) {
+        const ApusHipSlabRec &r = c->recs[i];
+        for (int t = 0; t < 3; t++)
+            if (r.O[t] != wantO[t] || r.K[t] != wantK[t])
+                return fail("store_load: expert %zu.%zu w%d is [%lld, %lld], the store holds [%lld, %lld]",
+                            i / c->E, i % c->E, t + 1, (long long)r.O[t], (long long)r.K[t],
+                            (long long)wantO[t], (long long)wantK[t]);
+    }
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init()) return fail("%s", g_err);
+    const size_t slab = c->slab_bytes;
+    const int nthr = io_threads > 0 ? std::min(io_threads, 32) : 4;
+    const int nbuf = std::max(4, 2 * nthr);
+    std::vector<int> fds;
+    for (const std::string &sh : c->shards) {
+        const std::string path = c->dir + "/" + sh;
+        const int fd = open(path.c_str(), O_RDONLY);
+        if (fd < 0) {
+            for (int f : fds) close(f);
+            return fail("store_load: cannot open %s", path.c_str());
+        }
+        fds.push_back(fd);
+    }
+    std::vector<uint8_t *> hbuf(nbuf, nullptr), dbuf(nbuf, nullptr);
+    std::vector<hipEvent_t> ev(nbuf, nullptr);
+    bool setup = true;
+    for (int b = 0; b < nbuf && setup; b++) {
+        setup = ok(hipHostMalloc((void **)&hbuf[b], slab, hipHostMallocDefault), "hipHostMalloc") &&
+                ok(hipEventCreateWithFlags(&ev[b], hipEventDisableTiming), "hipEventCreate") &&
+                (!st->tiled || ok(hipMalloc((void **)&dbuf[b], slab), "hipMalloc staging"));
+    }
+    struct Done { size_t idx; int buf; bool ok; };
+    std::mutex mu;
+    std::condition_variable cv;
+    std::deque<int> free_bufs;
+    std::deque<Done> ready;
+    std::atomic<size_t> next{0};
+    std::atomic<bool> stop{false};
+    for (int b = 0; b < nbuf; b++) free_bufs.push_back(b);
+    auto reader = [&]() {
+        for (;;) {
+            const size_t i = next.fetch_add(1);
+            if (i >= n || stop) return;
+            int b;
+            {
+                std::unique_lock<std::mutex> l(mu);
+                cv.wait(l, [&] { return !free_bufs.empty() || stop; });
+                if (stop) return;
+                b = free_bufs.front();
+                free_bufs.pop_front();
+            }
+            const ApusHipSlabRec &r = c->recs[i];
+            size_t got = 0;
+            bool good = true;
+            while (got < slab) {
+                const ssize_t k = pread(fds[r.shard], hbuf[b] + got, slab - got, (off_t)(r.off + got));
+                if (k <= 0) { good = false; break; }
+                got += (size_t)k;
+            }
+            {
+                std::lock_guard<std::mutex> l(mu);
+                ready.push_back({i, b, good});
+            }
+            cv.notify_all();
+        }
+    };
+    std::vector<std::thread> threads;
+    if (setup)
+        for (int t = 0; t < nthr; t++) threads.emplace_back(reader);
+    std::deque<int> pending;                      /* buffers whose copies are in flight */
+    int rc = setup ? 0 : 1;
+    size_t failed_idx = 0;
+    for (size_t done = 0; rc == 0 && done < n; done++) {
+        Done d;
+        {
+            std::unique_lock<std::mutex> l(mu);
+            while (ready.empty()) {
+                /* every buffer may be waiting on its copies: free the oldest */
+                if (free_bufs.empty() && !pending.empty()) {
+                    const int b = pending.front();
+                    pending.pop_front();
+                    l.unlock();
+                    if (!ok(hipEventSynchronize(ev[b]), "hipEventSynchronize")) rc = 1;
+                    l.lock();
+                    free_bufs.push_back(b);
+                    cv.notify_all();
+                    if (rc) break;
+                    continue;
+                }
+                cv.wait(l);
+            }
+            if (rc) break;
+            d = ready.front();
+            ready.pop_front();
+        }
+        if (!d.ok) { rc = 2; failed_idx = d.idx; break; }
+        const int layer = (int)(d.idx / c->E), eid = (int)(d.idx % c->E);
+        const ApusHipSlabRec &r = c->recs[d.idx];
+        uint8_t *dst[6];
+        size_t off = 0;
+        for (int i = 0; i < 6; i++) {
+            dst[i] = st->layer_base[layer] + st->expert_bytes * eid + off;
+            off += align256(st->sz[i]);
+        }
+        for (int m = 0; m < 3 && rc == 0; m++) {
+            const uint8_t *hw = hbuf[d.buf] + r.rel[2 * m], *hs = hbuf[d.buf] + r.rel[2 * m + 1];
+            const size_t wb = st->sz[2 * m], sb = st->sz[2 * m + 1];
+            if (!st->tiled) {
+                if (!ok(hipMemcpyAsync(dst[2 * m], hw, wb, hipMemcpyHostToDevice, g.stream), "H2D") ||
+                    !ok(hipMemcpyAsync(dst[2 * m + 1], hs, sb, hipMemcpyHostToDevice, g.stream), "H2D"))
+                    rc = 1;
+            } else {
+                uint8_t *sw = dbuf[d.buf] + r.rel[2 * m], *ss = dbuf[d.buf] + r.rel[2 * m + 1];
+                if (!ok(hipMemcpyAsync(sw, hw, wb, hipMemcpyHostToDevice, g.stream), "H2D") ||
+                    !ok(hipMemcpyAsync(ss, hs, sb, hipMemcpyHostToDevice, g.stream), "H2D") ||
+                    !launched(apus_launch_pack(APUS_W_FP4, sw, ss, dst[2 * m], dst[2 * m + 1],
+                                               (int)r.O[m], (int)r.K[m], 0, g.stream), "pack"))
+                    rc = 1;
+            }
+            g.bytes_uploaded += wb + sb;
+        }
+        if (rc == 0 && !ok(hipEventRecord(ev[d.buf], g.stream), "hipEventRecord")) rc = 1;
+        {
+            std::lock_guard<std::mutex> l(mu);
+            pending.push_back(d.buf);
+            /* hand back every buffer whose copies have finished */
+            while (!pending.empty() && hipEventQuery(ev[pending.front()]) == hipSuccess) {
+                free_bufs.push_back(pending.front());
+                pending.pop_front();
+            }
+        }
+        cv.notify_all();
+    }
+    {
+        std::lock_guard<std::mutex> l(mu);
+        stop = true;
+    }
+    cv.notify_all();
+    for (auto &t : threads) t.join();
+    if (!finish() && rc == 0) rc = 1;
+    for (int b = 0; b < nbuf; b++) {
+        if (hbuf[b]) (void)hipHostFree(hbuf[b]);
+        if (dbuf[b]) (void)hipFree(dbuf[b]);
+        if (ev[b]) (void)hipEventDestroy(ev[b]);
+    }
+    for (int f : fds) close(f);
+    if (rc == 2)
+        return fail("store_load: read of expert %zu.%zu failed (%s)", failed_idx / c->E,
+                    failed_idx % c->E, c->shards[c->recs[failed_idx].shard].c_str());
+    if (rc) return fail("store_load: %s", g_err);
+    return 0;
 }
 
 int apus_hip_store_get(const ApusHipStore *st, int layer, int eid, const uint8_t *ptrs[6]) {

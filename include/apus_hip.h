@@ -255,6 +255,39 @@ int      apus_hip_moe_routed_dev(const ApusHipStore *st, int layer,
                                  const float *wgt, int s, int topk,
                                  float limit, float *y, void *workspace);
 
+/* ---- apus model containers: routed-expert slabs on disk -> the store ----
+ *
+ * An apus container is a directory with model.safetensors.index.json (or
+ * <dir>/weights/...) whose "weight_map" names the shard of every tensor; the
+ * six tensors of a routed expert (layers.L.ffn.experts.E.w{1,2,3}.{weight,
+ * scale}; MTP blocks: mtp.K.ffn.experts..., store layer n_main + K) lie back
+ * to back in one shard (tools/convert.py:91-93), forming one slab per expert.
+ * The index follows apus_store_open (c/cache.h:1030-1110, slab derivation
+ * :431-509): 6 of 6 tensors per expert, one shard, contiguous, I8 weights
+ * [O, K/2] with F8_E8M0 scales [O, K/32], one slab size for all experts. */
+typedef struct {
+    int32_t  shard;           /* index of the shard file (apus_hip_container_shard) */
+    int32_t  pad;
+    uint64_t off, len;        /* absolute file offset and bytes of the slab */
+    uint32_t rel[6];          /* offsets of w1, w1s, w2, w2s, w3, w3s in the slab */
+    int64_t  O[3], K[3];      /* logical shapes of w1, w2, w3 */
+} ApusHipSlabRec;
+typedef struct ApusHipContainer ApusHipContainer;
+/* Host only (no device use). n_layers counts main + MTP expert layers. */
+ApusHipContainer *apus_hip_container_open(const char *model_dir, int n_layers, int n_mtp,
+                                          int n_experts, char *err, size_t errcap);
+void     apus_hip_container_close(ApusHipContainer *c);
+int      apus_hip_container_slab(const ApusHipContainer *c, int layer, int eid,
+                                 ApusHipSlabRec *out);
+/* path of shard i (NULL when out of range) */
+const char *apus_hip_container_shard(const ApusHipContainer *c, int i);
+/* Read every expert slab of the container into the store (its layers and
+ * experts must match; w1/w3 [inter, dim], w2 [dim, inter]), re-laid out as
+ * the store keeps them. io_threads readers (<= 0: 4) pread slabs into pinned
+ * host buffers while earlier ones upload. Synchronous; 0 on success. */
+int      apus_hip_store_load(ApusHipStore *st, const ApusHipContainer *c, int io_threads,
+                             char *err, size_t errcap);
+
 /* The whole MoE sublayer of one layer on the device (c/moe.h:369-595,
  * apus_moe_forward): router scores sqrt(softplus(gate_w x)) (c/moe.h:352-367),
  * expert choice by stable top-k of the scores plus gate_bias or by the hash

@@ -23,6 +23,8 @@ f32p = C.POINTER(C.c_float)
 f64p = C.POINTER(C.c_double)
 i32p = C.POINTER(C.c_int32)
 i64p = C.POINTER(C.c_int64)
+u64p = C.POINTER(C.c_uint64)
+u32p = C.POINTER(C.c_uint32)
 u8pp = C.POINTER(u8p)
 
 
@@ -253,6 +255,9 @@ class Reference:
             "ref_moe_forward": (None, [C.c_int] * 4 + [C.c_float, C.c_float, C.c_int, f32p, f32p,
                                                         i64p, i64p] + [u8pp] * 6 + [u8p] * 6
                                 + [f32p, C.c_int, f32p, f32p, f32p, f32p, i32p, f32p]),
+            "ref_store_index": (C.c_int, [C.c_char_p, C.c_int, C.c_int, C.c_int, i32p, u64p, u64p,
+                                          u32p, i64p, i64p, C.c_char_p, C.c_int,
+                                          C.POINTER(C.c_int), u8p, C.c_char_p, C.c_size_t]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -301,6 +306,39 @@ class Reference:
         h = np.empty_like(g)
         self.L.ref_swiglu(_p(g, f32p), _p(u, f32p), _p(h, f32p), g.size, limit)
         return h
+
+    def store_index(self, path, n_layers, n_mtp, E, with_slabs=False):
+        """The reference expert store's slab records (apus_store_open):
+        ([(shard_name, off, len, rel[6], O[3], K[3])] layer-major, slabs or
+        None), or raises ValueError with the reference's message."""
+        n = n_layers * E
+        shard = np.zeros(n, np.int32)
+        off, ln = np.zeros(n, np.uint64), np.zeros(n, np.uint64)
+        rel = np.zeros((n, 6), np.uint32)
+        O, K = np.zeros((n, 3), np.int64), np.zeros((n, 3), np.int64)
+        cap = 256
+        names = C.create_string_buffer(cap * 64)
+        nn = C.c_int()
+        err = C.create_string_buffer(512)
+        # slabs are sized after a first pass that learns the slab length
+        rc = self.L.ref_store_index(path.encode(), n_layers, n_mtp, E, _p(shard, i32p),
+                                    _p(off, u64p), _p(ln, u64p), _p(rel, u32p), _p(O, i64p),
+                                    _p(K, i64p), names, cap, C.byref(nn), None, err, 512)
+        if rc:
+            raise ValueError(err.value.decode())
+        slabs = None
+        if with_slabs:
+            slabs = np.zeros((n, int(ln.max())), np.uint8)
+            rc = self.L.ref_store_index(path.encode(), n_layers, n_mtp, E, _p(shard, i32p),
+                                        _p(off, u64p), _p(ln, u64p), _p(rel, u32p), _p(O, i64p),
+                                        _p(K, i64p), names, cap, C.byref(nn), _p(slabs, u8p),
+                                        err, 512)
+            if rc:
+                raise ValueError(err.value.decode())
+        nm = [names.raw[k * cap:(k + 1) * cap].split(b"\0")[0].decode() for k in range(nn.value)]
+        recs = [(nm[shard[i]], int(off[i]), int(ln[i]), rel[i].tolist(), O[i].tolist(), K[i].tolist())
+                for i in range(n)]
+        return recs, slabs
 
     def moe_forward(self, cfg, experts, shared, x):
         """The real apus_moe_forward: (out, routed, shared, sp, idx, wgt)."""

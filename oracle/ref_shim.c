@@ -1,6 +1,7 @@
 /*
  * oracle/ref_shim.c — builds the reference's OWN CPU kernels (c/fp4.h,
- * c/fp8.h, c/attn.h linears, c/moe.h dispatch, c/pool.h, c/x86.h) from the
+ * c/fp8.h, c/attn.h linears, c/moe.h dispatch, c/cache.h expert store,
+ * c/pool.h, c/x86.h) from the
  * sources where they lie under the apus checkout (-I <apus>/c) into
  * oracle/_ref/libapus_ref.so. Nothing from the reference is copied here:
  * this file only instantiates the header-only implementations and adds a
@@ -17,6 +18,7 @@
 #define APUS_MHC_IMPLEMENTATION
 #define APUS_ATTN_IMPLEMENTATION
 #define APUS_MOE_IMPLEMENTATION
+#define APUS_CACHE_IMPLEMENTATION
 #include "compat.h"
 #include "fp4.h"
 #include "fp8.h"
@@ -25,6 +27,7 @@
 #include "mhc.h"
 #include "attn.h"
 #include "moe.h"
+#include "cache.h"
 
 #include <stdlib.h>
 #include <string.h>
@@ -139,4 +142,65 @@ void ref_act_quant_rows(const float *x, int M, int K, float *xb, uint8_t *codes,
                         float *scales) {
     ApusActQuantJob aq = { x, xb, codes, scales, K, apus_fp4_act_blocks((size_t)K) };
     apus_act_quant_rows(&aq, 0, (size_t)M);
+}
+
+
+/* The reference expert store's slab index (c/cache.h:1030-1110
+ * apus_store_open, :431-509 derivation), opened synchronously with no usage
+ * file. Writes, per (layer, expert) in layer-major order: the shard name's
+ * index in `names` (first-use order, each name NUL-terminated in a
+ * name_cap-byte field), the slab's file offset, length, member offsets and
+ * w1..w3 shapes, and the expert's slab bytes read through
+ * apus_store_resolve when `slabs` is non-NULL. Returns 0, or -1 with err. */
+int ref_store_index(const char *dir, int n_layers, int n_mtp, int E, int32_t *shard,
+                    uint64_t *off, uint64_t *len, uint32_t *rel, int64_t *O, int64_t *K,
+                    char *names, int name_cap, int *n_names, uint8_t *slabs,
+                    char *err, size_t errcap) {
+    ApusStoreCfg cfg = {0};
+    cfg.n_layers = n_layers;
+    cfg.n_experts = E;
+    cfg.n_mtp = n_mtp;
+    cfg.io_threads = -1;
+    cfg.nocache = -1;
+    cfg.usage_path = "";
+    ApusStore *st = apus_store_open(dir, &cfg, err, errcap);
+    if (!st) return -1;
+    *n_names = 0;
+    for (int i = 0; i < n_layers * E; i++) {
+        const ApusSlabRec *r = &st->recs[i];
+        int sid = -1;
+        for (int k = 0; k < st->shards_n; k++)
+            if (st->shards[k].lz == r->lz) sid = k;
+        shard[i] = sid;
+        off[i] = r->off;
+        len[i] = r->len;
+        for (int j = 0; j < 6; j++) rel[6 * i + j] = r->rel[j];
+        for (int t = 0; t < 3; t++) { O[3 * i + t] = r->O[t]; K[3 * i + t] = r->K[t]; }
+    }
+    for (int k = 0; k < st->shards_n; k++)
+        snprintf(names + (size_t)k * name_cap, (size_t)name_cap, "%s", st->shards[k].name);
+    *n_names = st->shards_n;
+    if (slabs) {
+        for (int i = 0; i < n_layers * E; i++) {
+            ApusFp4W w[3];
+            if (apus_store_resolve(st, i / E, i % E, &w[0], &w[1], &w[2])) {
+                snprintf(err, errcap, "resolve %d.%d failed", i / E, i % E);
+                apus_store_close(st);
+                return -1;
+            }
+            /* members in canonical order at their slab offsets */
+            const uint8_t *src[6] = {w[0].packed, w[0].scales, w[1].packed, w[1].scales,
+                                     w[2].packed, w[2].scales};
+            const ApusSlabRec *r = &st->recs[i];
+            const size_t sz[6] = {
+                (size_t)(r->O[0] * r->K[0] / 2), (size_t)(r->O[0] * r->K[0] / 32),
+                (size_t)(r->O[1] * r->K[1] / 2), (size_t)(r->O[1] * r->K[1] / 32),
+                (size_t)(r->O[2] * r->K[2] / 2), (size_t)(r->O[2] * r->K[2] / 32)};
+            for (int j = 0; j < 6; j++)
+                memcpy(slabs + (size_t)i * r->len + r->rel[j], src[j], sz[j]);
+            apus_store_layer_end(st, i / E);
+        }
+    }
+    apus_store_close(st);
+    return 0;
 }
