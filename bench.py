@@ -417,6 +417,47 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
         L_.apus_hip_store_free(store)
 
 
+def bench_store_load(H, experts=64, dim=4096, inter=2048, threads=8):
+    """Expert slab loader: write a one-layer container of `experts` config-2
+    experts to a temporary directory, then time apus_hip_store_load into an
+    MFMA-tiled store (the freshly written shards are in the page cache, so
+    this measures the pread + pinned-buffer + PCIe + pack pipeline, not a
+    cold disk)."""
+    import ctypes as C
+    import shutil
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import container_util as cu
+    L_ = H.lib()
+    rng = np.random.default_rng(9)
+    d = tempfile.mkdtemp(prefix="apus_container_")
+    try:
+        arr = cu.expert_arrays(rng, dim, inter)   # one expert's bytes, reused
+        entries = []
+        for e in range(experts):
+            entries += cu.expert_entries(0, e, arr)
+        cu.write_container(d, {"model-00001.safetensors": entries})
+        err = C.create_string_buffer(512)
+        c = L_.apus_hip_container_open(d.encode(), 1, 0, experts, err, 512)
+        if not c:
+            raise RuntimeError(err.value.decode())
+        st = L_.apus_hip_store_create(1, experts, dim, inter, err, 256)
+        try:
+            t0 = time.perf_counter()
+            if L_.apus_hip_store_load(st, c, threads, err, 512):
+                raise RuntimeError(err.value.decode())
+            dt = time.perf_counter() - t0
+            rec = H.ApusHipSlabRec()
+            L_.apus_hip_container_slab(c, 0, 0, C.byref(rec))
+            nbytes = rec.len * experts
+        finally:
+            L_.apus_hip_store_free(st)
+            L_.apus_hip_container_close(c)
+        return {"GBs": nbytes / dt / 1e9, "bytes": nbytes, "s": dt}
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def cpu_baseline(O=2048, K=4096, budget_s=12.0):
     """apus's own apus_fp4_gemm_mt (AVX2 rows + pthread pool) on config 0."""
     threads = min(os.cpu_count() or 1, 16)
@@ -467,7 +508,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: gemv,fp8,decode,prefill,full")
+    ap.add_argument("--only", default="", help="comma list: gemv,fp8,decode,prefill,full,load")
     ap.add_argument("--full-layers", type=int, default=43,
                     help="config 4: resident MoE layers (43 fill ~148 GB)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -548,6 +589,10 @@ def main():
                        "config4_bytes_per_token": f["bytes_per_token"],
                        "config4_launches_per_token": f["launches_per_token"]})
 
+    if not args.skip_extras and want("load"):
+        log("[bench] expert slab loader: 64 experts from a page-cached container")
+        ld = bench_store_load(H)
+        extras.update({"store_load_GBs": round(ld["GBs"], 2), "store_load_bytes": ld["bytes"]})
     if args.calibrate_copy:
         # a plain copy of known size: its FETCH_SIZE / WRITE_SIZE counters give
         # the scale between the counters and bytes moved
