@@ -203,11 +203,13 @@ uint64_t fingerprint(const uint8_t *p, size_t n) {
  * sampled contents changed is re-uploaded */
 /* shapes whose weights are kept in the MFMA-tiled layout (the decode,
  * prefill and tile schedules read it) */
-bool tiled_shape(int O, int K) { return (K == 2048 || K == 4096) && O > 0 && O % 128 == 0; }
+bool tiled_shape(int O, int K) { return apus_fast_k(K) && O > 0 && O % 128 == 0; }
 
 /* routed experts of this shape are held MFMA-tiled (w1/w3 [inter, dim] and
- * w2 [dim, inter] all qualify) */
-bool moe_tiled(int dim, int inter) { return tiled_shape(inter, dim) && tiled_shape(dim, inter); }
+ * w2 [dim, inter] with K 2048 or 4096: the grouped schedules) */
+bool moe_tiled(int dim, int inter) {
+    return apus_group_k(dim) && apus_group_k(inter) && inter % 128 == 0 && dim % 128 == 0;
+}
 
 /* host row-major weights -> device, MFMA-tiled when `tiled` (staged through
  * scratch slots 4 and 5) */
@@ -284,7 +286,7 @@ int gemm_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acode
  * when the shape does not qualify (the caller quantises, then multiplies) */
 int linear_fused(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x, float *out,
                  int M, int K, int O, hipStream_t st) {
-    if (M > 8 || (K != 2048 && K != 4096) || O % 128) return -1;
+    if (M > 8 || !apus_fast_k(K) || O % 128) return -1;
     ApusGemmArgs a{};
     a.wtiled = (wfmt & APUS_HIP_W_TILED) ? 1 : 0;
     wfmt &= ~APUS_HIP_W_TILED;
@@ -894,7 +896,7 @@ static int linear_dev(int wfmt, const uint8_t *w, const uint8_t *ws, const float
     const int fmt = wfmt & ~APUS_HIP_W_TILED;
     if ((fmt != APUS_W_FP4 && fmt != APUS_W_FP8) ||
         ((wfmt & APUS_HIP_W_TILED) && !tiled_shape(O, K))) {
-        set_err("linear_dev: bad format, or tiled weights with K not 2048/4096 or O %% 128 != 0");
+        set_err("linear_dev: bad format, or tiled weights with K not 1024/2048/4096/8192 or O %% 128 != 0");
         return 1;
     }
     if (!workspace) { set_err("linear_dev: workspace required"); return 1; }

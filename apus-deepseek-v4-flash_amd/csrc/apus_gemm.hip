@@ -484,9 +484,6 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
         if constexpr (ASRC == APUS_A_CODES) {
             /* stage: row indices, then every code/scale load, then the LDS
              * writes (no load waits on another load's result more than once) */
-            constexpr int STAGE = R * K16 / 256;       /* 16-byte loads per thread */
-            constexpr int RPJ = 256 / K16;             /* rows per 256 loads */
-            static_assert(RPJ >= 1 && R % RPJ == 0, "staging shape");
             int ridx[R];
             if (ent.arows) {
 #pragma unroll
@@ -495,36 +492,65 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
 #pragma unroll
                 for (int j = 0; j < R; ++j) ridx[j] = ent.a0 + c0 + min(j, rows - 1);
             }
+            /* a row is K16 16-byte pieces: RPJ rows per pass of the 256
+             * threads when K16 <= 256, else CPR passes per row */
+            constexpr int RPJ = K16 <= 256 ? 256 / K16 : 1;
+            constexpr int CPR = K16 <= 256 ? 1 : K16 / 256;
+            constexpr int STAGE = K16 <= 256 ? R * K16 / 256 : R * CPR;
+            static_assert(RPJ >= 1 && R % RPJ == 0 && (K16 <= 256 || K16 % 256 == 0), "staging shape");
             uint4 v[STAGE];
 #pragma unroll
             for (int j = 0; j < STAGE; ++j) {
-                const int rsub = threadIdx.x / K16;         /* 0..RPJ-1 */
-                const int cc = threadIdx.x - rsub * K16;
-                int ar = ridx[j * RPJ];
+                int row, cc;
+                if constexpr (K16 <= 256) {
+                    const int rsub = threadIdx.x / K16;         /* 0..RPJ-1 */
+                    row = j * RPJ + rsub;
+                    cc = threadIdx.x - rsub * K16;
+                } else {
+                    row = j / CPR;
+                    cc = (j % CPR) * 256 + threadIdx.x;
+                }
+                int ar = ridx[0];
 #pragma unroll
-                for (int t = 1; t < RPJ; ++t) ar = rsub == t ? ridx[j * RPJ + t] : ar;
+                for (int t = 1; t < R; ++t) ar = row == t ? ridx[t] : ar;
                 /* only the entry's rows are read; the test is uniform over
                  * each wave (a row is K16 >= 128 consecutive threads) */
-                if (j * RPJ + rsub < rows) v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);
+                if (row < rows) v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);
                 else v[j] = uint4{0u, 0u, 0u, 0u};
             }
-            const int si = threadIdx.x % (R * NQ), srr = si / NQ;
-            int sar = ridx[0];
+            constexpr int SPT = (R * NQ + 255) / 256;          /* scales per thread */
+            float scv[SPT];
 #pragma unroll
-            for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
-            const float scv = apus_gld<float>(args.ascale + ((size_t)sar * NQ + (si - srr * NQ)));
+            for (int k = 0; k < SPT; ++k) {
+                const int si = threadIdx.x + 256 * k, srr = si / NQ;
+                int sar = ridx[0];
+#pragma unroll
+                for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
+                scv[k] = si < R * NQ ? apus_gld<float>(args.ascale + ((size_t)sar * NQ + (si - srr * NQ)))
+                                     : 1.0f;
+            }
             /* weight prefetch ring: issued after the staging loads (so waiting
              * for those does not wait for these) and before the LDS hand-off */
 #pragma unroll
             for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, sbase + u);
 #pragma unroll
             for (int j = 0; j < STAGE; ++j) {
-                const int rsub = threadIdx.x / K16;
-                const int cc = threadIdx.x - rsub * K16;
-                if (j * RPJ + rsub < rows)
-                    *reinterpret_cast<uint4 *>(lcodes + (j * RPJ + rsub) * LDK + cc * 16) = v[j];
+                int row, cc;
+                if constexpr (K16 <= 256) {
+                    const int rsub = threadIdx.x / K16;
+                    row = j * RPJ + rsub;
+                    cc = threadIdx.x - rsub * K16;
+                } else {
+                    row = j / CPR;
+                    cc = (j % CPR) * 256 + threadIdx.x;
+                }
+                if (row < rows) *reinterpret_cast<uint4 *>(lcodes + row * LDK + cc * 16) = v[j];
             }
-            if (threadIdx.x < R * NQ && srr < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv);
+#pragma unroll
+            for (int k = 0; k < SPT; ++k) {
+                const int si = threadIdx.x + 256 * k;
+                if (si < R * NQ && si / NQ < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv[k]);
+            }
         } else {
             /* first pass: loads (unless issued before the entry lookup), the
              * weight ring, then the quantisation; later passes load and
@@ -1284,32 +1310,39 @@ void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
     constexpr int K = NS * 512, NQ = NS * 4;
     const size_t lds = (((size_t)R * (K + 16) + (size_t)R * NQ + 15) & ~(size_t)15) +
                        (KS > 1 ? 256 * sizeof(float) * 4 : 0);
+    if (lds > 65536) {
+        /* eight staged rows of K = 8192 need more than the default 64 KB */
+        static const hipError_t attr = hipFuncSetAttribute(
+            reinterpret_cast<const void *>(&apus_gemm_decode_kernel<WF, R, NS, PD, KS, ASRC>),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        (void)attr;
+    }
     dim3 gd(d.O / (16 * APUS_DEC_WAVES / KS), n_ent), bd(256);
     hipLaunchKernelGGL((apus_gemm_decode_kernel<WF, R, NS, PD, KS, ASRC>), gd, bd, lds, st, d);
 }
 
+/* the K split for K = 512 * NS: KS divides NS; single-row chunks always split
+ * K (with one chunk per workgroup and whole-K waves the compiler hoists every
+ * slice's weight loads and runs out of registers) */
+template <int WF, int R, int NS, int ASRC>
+void apus_launch_dec_ns(const ApusGemmArgs &d, int n_ent, int ks, hipStream_t st) {
+    if constexpr (NS >= 4) {
+        if (ks == 4) { apus_launch_dec<WF, R, NS, 4, ASRC>(d, n_ent, st); return; }
+    }
+    if constexpr (R != 1) {
+        if (ks == 1) { apus_launch_dec<WF, R, NS, 1, ASRC>(d, n_ent, st); return; }
+    }
+    apus_launch_dec<WF, R, NS, 2, ASRC>(d, n_ent, st);
+}
+
 template <int WF, int R, int ASRC>
 void apus_launch_dec_k(const ApusGemmArgs &d, int n_ent, int ks, hipStream_t st) {
-    if constexpr (R == 1) {
-        /* single-row chunks always split K: with one chunk per workgroup and
-         * whole-K waves the compiler hoists every slice's weight loads and
-         * runs out of registers */
-        if (d.K == 4096) {
-            if (ks == 4) apus_launch_dec<WF, R, 8, 4, ASRC>(d, n_ent, st);
-            else apus_launch_dec<WF, R, 8, 2, ASRC>(d, n_ent, st);
-        } else {
-            if (ks == 4) apus_launch_dec<WF, R, 4, 4, ASRC>(d, n_ent, st);
-            else apus_launch_dec<WF, R, 4, 2, ASRC>(d, n_ent, st);
-        }
-    } else if (d.K == 4096) {
-        if (ks == 1) apus_launch_dec<WF, R, 8, 1, ASRC>(d, n_ent, st);
-        else if (ks == 2) apus_launch_dec<WF, R, 8, 2, ASRC>(d, n_ent, st);
-        else apus_launch_dec<WF, R, 8, 4, ASRC>(d, n_ent, st);
-    } else {
-        if (ks == 1) apus_launch_dec<WF, R, 4, 1, ASRC>(d, n_ent, st);
-        else if (ks == 2) apus_launch_dec<WF, R, 4, 2, ASRC>(d, n_ent, st);
-        else apus_launch_dec<WF, R, 4, 4, ASRC>(d, n_ent, st);
+    if constexpr (ASRC != APUS_A_SWIGLU) {
+        if (d.K == 1024) { apus_launch_dec_ns<WF, R, 2, ASRC>(d, n_ent, ks, st); return; }
+        if (d.K == 8192) { apus_launch_dec_ns<WF, R, 16, ASRC>(d, n_ent, ks, st); return; }
     }
+    if (d.K == 4096) apus_launch_dec_ns<WF, R, 8, ASRC>(d, n_ent, ks, st);
+    else             apus_launch_dec_ns<WF, R, 4, ASRC>(d, n_ent, ks, st);
 }
 
 /* waves per 16-row tile: the smallest K split that still gives about one
@@ -1332,8 +1365,9 @@ int apus_dec_ks(size_t row_tiles) {
 hipError_t apus_launch_gemm_few(int wfmt, const ApusGemmArgs *a, int n_ent, int rows,
                                 int ks, hipStream_t st) {
     if (n_ent <= 0) return hipSuccess;
-    if ((a->K != 2048 && a->K != 4096) || a->O % 128 || (rows != 1 && rows != 8) ||
+    if (!apus_fast_k(a->K) || a->O % 128 || (rows != 1 && rows != 8) ||
         (a->asrc == APUS_A_CODES && rows != 8) ||
+        (a->asrc == APUS_A_SWIGLU && !apus_group_k(a->K)) ||
         (a->acc_y && (!a->pidx || a->nmat != 1 || !a->tickets)) || ks < 0 || ks > 4 || ks == 3)
         return hipErrorInvalidValue;
     /* two by-value entries share their activation rows (staged once, before
@@ -1382,7 +1416,8 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
     if (a->items && (wfmt != APUS_W_FP4 || !grouped)) return hipErrorInvalidValue;
     if (a->wtiled) {
         /* tiled weights: only the decode, prefill and tile schedules read them */
-        if ((a->K != 2048 && a->K != 4096) || a->O % 128) return hipErrorInvalidValue;
+        if (!(grouped ? apus_group_k(a->K) : apus_fast_k(a->K)) || a->O % 128)
+            return hipErrorInvalidValue;
         if (!grouped && a->ent0.M <= R) {
             ApusGemmArgs d = *a;
             d.asrc = APUS_A_CODES;
@@ -1393,7 +1428,7 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
      * take the decode schedule, larger ones the prefill schedule (two
      * launches over the same entry table, each skipping the other's entries) */
     if (grouped && (row_tiles >= 512 || (a->max_m > 0 && a->max_m <= R) || a->wtiled) &&
-        (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
+        apus_group_k(a->K) && a->O % 128 == 0) {
         const bool run_dec = !(a->min_m >= R);
         const bool run_pre = !(a->max_m > 0 && a->max_m <= R);
         if (run_dec) {
@@ -1420,15 +1455,27 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
         return hipGetLastError();
     }
     /* dense GEMMs with more than 8 rows: the tile schedule */
-    if (!grouped && a->ent0.M > R && (a->K == 2048 || a->K == 4096) && a->O % 128 == 0) {
+    if (!grouped && a->ent0.M > R && apus_fast_k(a->K) && a->O % 128 == 0) {
         dim3 gt(a->O / 128, (a->ent0.M + 63) / 64, 1), bt(256);
+#define APUS_TILE(NQ, PD) hipLaunchKernelGGL((apus_gemm_tile_kernel<WFC, NQ, PD, 6>), gt, bt, 0, st, *a)
         if (wfmt == APUS_W_FP4) {
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_tile_kernel<APUS_W_FP4, 32, 8, 6>), gt, bt, 0, st, *a);
-            else              hipLaunchKernelGGL((apus_gemm_tile_kernel<APUS_W_FP4, 16, 8, 6>), gt, bt, 0, st, *a);
+            constexpr int WFC = APUS_W_FP4;
+            switch (a->K) {
+            case 1024: APUS_TILE(8, 8); break;
+            case 2048: APUS_TILE(16, 8); break;
+            case 4096: APUS_TILE(32, 8); break;
+            default:   APUS_TILE(64, 8); break;
+            }
         } else {
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_tile_kernel<APUS_W_FP8, 32, 6, 6>), gt, bt, 0, st, *a);
-            else              hipLaunchKernelGGL((apus_gemm_tile_kernel<APUS_W_FP8, 16, 6, 6>), gt, bt, 0, st, *a);
+            constexpr int WFC = APUS_W_FP8;
+            switch (a->K) {
+            case 1024: APUS_TILE(8, 6); break;
+            case 2048: APUS_TILE(16, 6); break;
+            case 4096: APUS_TILE(32, 6); break;
+            default:   APUS_TILE(64, 6); break;
+            }
         }
+#undef APUS_TILE
         return hipGetLastError();
     }
     /* other grouped shapes with many row tiles */

@@ -107,6 +107,13 @@ typedef struct {
 
 enum { APUS_A_CODES = 0, APUS_A_F32 = 1, APUS_A_SWIGLU = 2 };
 
+/* reduction lengths with the MFMA schedules (decode, tile) and the MFMA-tiled
+ * weight layout for dense GEMMs: 512 * {2, 4, 8, 16} (the model's dense FP8
+ * shapes have K 1024, 4096 and 8192; experts 2048 and 4096) */
+static inline bool apus_fast_k(int K) { return K == 1024 || K == 2048 || K == 4096 || K == 8192; }
+/* grouped launches (experts) keep to K 2048 and 4096 */
+static inline bool apus_group_k(int K) { return K == 2048 || K == 4096; }
+
 /* rows (tokens) per chunk of the many-row (prefill) schedule for MXFP4
  * weights: one work-list item */
 #define APUS_PREFILL_ROWS 64

@@ -250,6 +250,40 @@ def bench_fp8(H, dev, steps, O=4096, K=4096, copies=40):
 
 # ------------------------------------------------------------------ MoE (configs 2, 3)
 
+# the model's dense FP8 projections (reference/config.json: dim 4096, q_lora
+# 1024, 64 heads x 512, o_lora 1024 x 8 groups); name -> (O, K)
+ATTN_FP8 = {"wq_a": (1024, 4096), "wq_b": (32768, 1024), "wkv": (512, 4096), "wo_b": (4096, 8192)}
+
+
+def bench_attn_fp8(H, dev, steps=64, M=1, copies=8, tiled=True):
+    """One-token FP8 linears at the attention shapes (fp32 x -> BF16 out, act
+    quant fused), MFMA-tiled weights, `copies` distinct weight copies in
+    rotation so each launch streams from HBM."""
+    L = H.lib()
+    out = {}
+    for name, (O, K) in ATTN_FP8.items():
+        wb, sb = O * K, (O // 128) * (K // 128)
+        w = dev.alloc(wb * copies)
+        ws = dev.alloc(sb * copies)
+        H._check(L.apus_hip_fill_random(w.ptr, wb * copies, 3, 1, 2), "fill")
+        H._check(L.apus_hip_fill_random(ws.ptr, sb * copies, 3, 2, 3), "fill")
+        x = dev.upload(np.random.default_rng(1).standard_normal((M, K)).astype(np.float32))
+        y = dev.alloc(M * O * 4)
+        wl = dev.alloc(L.apus_hip_linear_workspace(M, K))
+
+        def step(i, O=O, K=K, w=w, ws=ws, x=x, y=y, wl=wl, wb=wb, sb=sb):
+            c = i % copies
+            H._check(L.apus_hip_linear_dev(1 | (H.W_TILED if tiled else 0), w.ptr + c * wb,
+                                           ws.ptr + c * sb, x.ptr, y.ptr, M, K, O, wl.ptr), "linear")
+
+        for i in range(4):
+            step(i)
+        H.synchronize()
+        us = timed_graph(H, step, steps) * 1e3 / steps
+        out[name] = {"us": us, "GBs": (wb + sb) / us / 1e3}
+    return out
+
+
 def zipf_routing(rng, s, E, topk, a):
     """top-k distinct experts per token with popularity ~ rank^-a (random rank order)."""
     p = 1.0 / np.arange(1, E + 1) ** a
@@ -547,6 +581,9 @@ def main():
         extras["config1_fp8_M1_us"] = round(f8["M1"]["us"], 2)
         extras["config1_fp8_M512_TFLOPs"] = round(f8["M512"]["tflops"], 1)
         extras["config1_fp8_M512_us"] = round(f8["M512"]["us"], 2)
+        for name, r in bench_attn_fp8(H, dev).items():
+            extras[f"attn_{name}_M1_us"] = round(r["us"], 2)
+            extras[f"attn_{name}_M1_GBs"] = round(r["GBs"], 1)
     if not args.skip_extras and (want("decode") or want("prefill")):
         layers = 4
         err = __import__("ctypes").create_string_buffer(256)

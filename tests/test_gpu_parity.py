@@ -81,7 +81,8 @@ def _check_linear(got, want, unrounded, tag):
 
 # M <= 8 with K 2048/4096 runs the one-launch path (act quant inside the
 # GEMM staging); the other shapes quantise first
-@pytest.mark.parametrize("M,O,K", [(1, 2048, 4096), (4, 4096, 2048), (8, 256, 2048), (9, 2048, 4096)])
+@pytest.mark.parametrize("M,O,K", [(1, 2048, 4096), (4, 4096, 2048), (8, 256, 2048), (9, 2048, 4096),
+                                   (1, 512, 8192), (3, 256, 1024)])
 def test_fp4_linear(hip, oracle, rng, M, O, K):
     w, ws = fp4_weights(rng, O, K)
     x = acts(rng, M, K)
@@ -91,7 +92,8 @@ def test_fp4_linear(hip, oracle, rng, M, O, K):
     _check_linear(got, want, oracle.fp4_gemm(w, ws, c, s), f"fp4 linear M={M} O={O} K={K}")
 
 
-@pytest.mark.parametrize("M,O,K", [(1, 4096, 4096), (8, 4096, 2048), (3, 256, 512), (12, 1024, 4096)])
+@pytest.mark.parametrize("M,O,K", [(1, 4096, 4096), (8, 4096, 2048), (3, 256, 512), (12, 1024, 4096),
+                                   (1, 1024, 8192), (8, 512, 8192), (4, 512, 1024), (1, 2048, 1024)])
 def test_fp8_linear(hip, oracle, rng, M, O, K):
     w, ws = fp8_weights(rng, O, K)
     x = acts(rng, M, K)
@@ -121,9 +123,12 @@ def test_fp4_gemm_m_independent(hip, oracle, rng):
 
 
 @pytest.mark.parametrize("fmt,M,O,K", [("fp8", 100, 256, 4096), ("fp8", 64, 384, 2048),
-                                       ("fp4", 77, 256, 4096), ("fp4", 9, 128, 2048)])
+                                       ("fp4", 77, 256, 4096), ("fp4", 9, 128, 2048),
+                                       ("fp8", 70, 256, 8192), ("fp8", 33, 128, 1024),
+                                       ("fp4", 20, 256, 1024), ("fp4", 65, 128, 8192)])
 def test_gemm_tile_schedule(hip, oracle, rng, fmt, M, O, K):
-    """More than 8 rows, K 2048/4096: the 64 x 128 tile schedule, ragged M."""
+    """More than 8 rows, K 1024/2048/4096/8192: the 64 x 128 tile schedule,
+    ragged M."""
     c, s = oracle.act_quant(acts(rng, M, K, 2.0))
     if fmt == "fp8":
         w, ws = fp8_weights(rng, O, K)

@@ -106,7 +106,8 @@ def test_tiled_grouped_equals_rowmajor(hip, oracle, rng, fmt, O, K, Ms):
 
 
 @pytest.mark.parametrize("fmt,M,O,K", [(0, 100, 256, 2048), (1, 70, 384, 4096),
-                                       (0, 1, 2048, 4096), (1, 3, 4096, 4096)])
+                                       (0, 1, 2048, 4096), (1, 3, 4096, 4096),
+                                       (1, 40, 256, 8192), (0, 2, 256, 1024)])
 def test_tiled_dense(hip, oracle, rng, fmt, M, O, K):
     """Dense GEMM entry points on tiled weights: more than 8 rows (tile
     schedule, bitwise equal to row-major) and few rows (oracle bar)."""
@@ -129,7 +130,8 @@ def test_tiled_dense(hip, oracle, rng, fmt, M, O, K):
     assert max_rel(outs[1], want) <= 1e-3
 
 
-@pytest.mark.parametrize("fmt,M,O,K", [(1, 1, 4096, 4096), (0, 6, 2048, 4096), (1, 20, 1024, 2048)])
+@pytest.mark.parametrize("fmt,M,O,K", [(1, 1, 4096, 4096), (0, 6, 2048, 4096), (1, 20, 1024, 2048),
+                                       (1, 8, 1024, 8192), (0, 1, 512, 1024)])
 def test_tiled_linear_dev(hip, rng, fmt, M, O, K):
     """apus_hip_linear_dev on tiled weights equals the row-major linear bit
     for bit (the same schedule for the same M)."""
