@@ -109,6 +109,9 @@ SIGNATURES = {
     "apus_hip_fp4_gemm_grouped": (C.c_int, [C.POINTER(ApusFp4GemmEnt), C.c_size_t, u8p, f32p,
                                             C.c_size_t, C.c_size_t]),
     "apus_hip_moe_routed": (C.c_int, [C.POINTER(ApusMoeW), f32p, i32p, f32p, C.c_int, f32p]),
+    "apus_hip_f32_linear": (C.c_int, [vp, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "apus_hip_head_gemv": (C.c_int, [vp, f32p, f32p, C.c_int64, C.c_int64]),
+    "apus_hip_wlinear_dev": (C.c_int, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int]),
     "apus_hip_act_quant": (C.c_int, [f32p, C.c_int, C.c_int, u8p, f32p]),
     "apus_hip_fp4_gemm": (C.c_int, [u8p, u8p, u8p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
     "apus_hip_fp8_gemm": (C.c_int, [u8p, u8p, u8p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
@@ -267,6 +270,42 @@ def fp8_linear(w, ws, x):
     W = fp8_weight(w, ws)
     _check(lib().apus_hip_fp8_linear(C.byref(W), _p(x, f32p), _p(out, f32p), M, K, O),
            "fp8_linear")
+    return out
+
+
+def f32_linear(w, x, flags=0):
+    """Plain-weight linear hook: w [O, K] float32 (or uint16 BF16 bits with
+    flags & 4), x [M, K] float32; flags 1 = BF16 input, 2 = BF16 output."""
+    w = np.ascontiguousarray(w)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    O = w.shape[0]
+    out = np.empty((M, O), np.float32)
+    _check(lib().apus_hip_f32_linear(w.ctypes.data, _p(x, f32p), _p(out, f32p), M, K, O, flags),
+           "f32_linear")
+    return out
+
+
+class StTensor(C.Structure):
+    """c/st.h:46-53 ApusStTensor (head GEMV view)."""
+    _fields_ = [("name", C.c_char * 160), ("dtype", C.c_int), ("ndim", C.c_int),
+                ("shape", C.c_int64 * 8), ("data", vp), ("nbytes", C.c_size_t)]
+
+
+def head_gemv(w, x):
+    """LM-head GEMV over a BF16 (uint16 bits) or F32 view w [O, K]; x [K]."""
+    w = np.ascontiguousarray(w)
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    O, K = w.shape
+    t = StTensor()
+    t.name = b"head"
+    t.dtype = 4 if w.dtype == np.uint16 else 6
+    t.ndim = 2
+    t.shape[0], t.shape[1] = O, K
+    t.data = w.ctypes.data
+    t.nbytes = w.nbytes
+    out = np.empty(O, np.float32)
+    _check(lib().apus_hip_head_gemv(C.byref(t), _p(x, f32p), _p(out, f32p), O, K), "head_gemv")
     return out
 
 

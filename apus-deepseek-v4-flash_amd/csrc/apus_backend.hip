@@ -229,7 +229,7 @@ bool upload_weights(int wfmt, uint8_t *dw, uint8_t *dws, const void *w, const vo
 
 const DenseW *dense_weight(int wfmt, const uint8_t *w, const uint8_t *ws, size_t wbytes,
                            size_t sbytes, int O, int K) {
-    const uint64_t fp = fingerprint(w, wbytes) ^ (fingerprint(ws, sbytes) * 31);
+    const uint64_t fp = fingerprint(w, wbytes) ^ (ws && sbytes ? fingerprint(ws, sbytes) * 31 : 0);
     auto it = g.dense.find(w);
     if (it != g.dense.end()) {
         DenseW &d = it->second;
@@ -249,7 +249,7 @@ const DenseW *dense_weight(int wfmt, const uint8_t *w, const uint8_t *ws, size_t
     DenseW d{ws, nullptr, nullptr, wbytes, sbytes, fp, wfmt, O, K, false};
     if (!ok(hipMalloc(&d.w, wbytes), "hipMalloc weight")) return nullptr;
     if (!ok(hipMalloc(&d.ws, sbytes), "hipMalloc scales")) { hipFree(d.w); return nullptr; }
-    d.tiled = tiled_shape(O, K);
+    d.tiled = wfmt <= APUS_W_FP8 && tiled_shape(O, K);
     if (!upload_weights(wfmt, d.w, d.ws, w, ws, wbytes, sbytes, O, K, d.tiled)) {
         hipFree(d.w); hipFree(d.ws);
         return nullptr;
@@ -625,8 +625,8 @@ int apus_hip_enable(char *err, size_t errcap) {
         return -1;
     }
     g.hooks.fp8_linear = apus_hip_fp8_linear;
-    g.hooks.f32_linear = nullptr;
-    g.hooks.head_gemv = nullptr;
+    g.hooks.f32_linear = apus_hip_f32_linear;
+    g.hooks.head_gemv = apus_hip_head_gemv;
     g.hooks.fp4_linear = apus_hip_fp4_linear;
     g.hooks.fp4_gemm_grouped = apus_hip_fp4_gemm_grouped;
     g.hooks.moe_routed = apus_hip_moe_routed;
@@ -688,6 +688,57 @@ int apus_hip_fp4_gemm(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes
 int apus_hip_fp8_gemm(const uint8_t *w, const uint8_t *ws, const uint8_t *acodes,
                       const float *as, float *out, int M, int O, int K) {
     return gemm_host(APUS_W_FP8, w, ws, acodes, as, out, M, O, K);
+}
+
+/* ---- plain-weight linears (c/attn.h:600-666, c/model.h:638-647) ---- */
+
+static int wlinear_host(const void *w, bool bf16, const float *x, float *out, int M, int K, int O,
+                        int flags) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!ensure_init()) return 1;
+    if (M <= 0 || K <= 0 || O <= 0 || K % 8) {
+        set_err("plain-weight linear: unsupported shape M=%d K=%d O=%d (needs K %% 8 == 0)", M, K, O);
+        return 1;
+    }
+    const size_t wbytes = (size_t)O * K * (bf16 ? 2 : 4);
+    const DenseW *d = dense_weight(bf16 ? APUS_W_BF16 : APUS_W_F32, (const uint8_t *)w, nullptr,
+                                   wbytes, 0, O, K);
+    if (!d) return 1;
+    float *dx = (float *)scratch(0, (size_t)M * K * 4);
+    float *dout = (float *)scratch(3, (size_t)M * O * 4);
+    if (!dx || !dout || !upload(dx, x, (size_t)M * K * 4)) return 1;
+    if (!launched(apus_launch_wgemv(d->w, dx, dout, M, K, O, (flags & 3) | (bf16 ? 4 : 0), g.stream),
+                  "wgemv"))
+        return 1;
+    return download(out, dout, (size_t)M * O * 4) && finish() ? 0 : 1;
+}
+
+int apus_hip_f32_linear(const float *w, const float *x, float *out, int M, int K, int O,
+                        int flags) {
+    if (!w || !x || !out || (flags & ~7)) return 1;
+    return wlinear_host(w, (flags & APUS_HIP_W_BF16) != 0, x, out, M, K, O, flags);
+}
+
+int apus_hip_head_gemv(const ApusStTensor *head, const float *x, float *out, int64_t O,
+                       int64_t K) {
+    if (!head || !x || !out || O <= 0 || K <= 0 || O > 0x7fffffff || K > 0x7fffffff) return 1;
+    const bool bf16 = head->dtype == APUS_ST_BF16;
+    if ((!bf16 && head->dtype != APUS_ST_F32) || head->ndim != 2 || head->shape[0] != O ||
+        head->shape[1] != K || head->nbytes != (size_t)(O * K * (bf16 ? 2 : 4)) || !head->data) {
+        set_err("head_gemv: needs a BF16 or F32 [O, K] view");
+        return 1;
+    }
+    return wlinear_host(head->data, bf16, x, out, 1, (int)K, (int)O, 0);
+}
+
+int apus_hip_wlinear_dev(const void *w, const float *x, float *out, int M, int K, int O,
+                         int flags) {
+    if (!ensure_init()) return 1;
+    if (!w || !x || !out || (flags & ~7) || M <= 0 || K <= 0 || O <= 0 || K % 8) {
+        set_err("wlinear_dev: bad arguments (K %% 8 == 0 needed)");
+        return 1;
+    }
+    return launched(apus_launch_wgemv(w, x, out, M, K, O, flags, dev_stream()), "wgemv") ? 0 : 1;
 }
 
 int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent, const uint8_t *acodes,

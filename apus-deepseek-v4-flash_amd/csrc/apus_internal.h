@@ -12,7 +12,7 @@
 #include <stdint.h>
 
 /* weight formats of the block-scaled GEMM */
-enum { APUS_W_FP4 = 0, APUS_W_FP8 = 1 };
+enum { APUS_W_FP4 = 0, APUS_W_FP8 = 1, APUS_W_F32 = 2, APUS_W_BF16 = 3 };
 
 /* One GEMM of a (possibly grouped) launch. Output row m of this entry is
  *   out[orow(m) * ldo + o] = sum_k A[arow(m), k] * W[o, k]   (o < O)
@@ -197,6 +197,11 @@ hipError_t apus_launch_router(const float *gate_w, const float *bias, const floa
 hipError_t apus_launch_topk(const float *sel, const float *sp, int s, int E, int topk,
                             const int64_t *tid2eid, const int64_t *ids, float route_scale,
                             int32_t *idx, float *wgt, hipStream_t st);
+/* plain-weight linear (FP32 or BF16-bit weights [O, K], FP32 accumulate):
+ * out[m, o] = sum_k w[o, k] * x'[m, k]; flags as the f32_linear hook
+ * (1: x' = bf16(x), 2: bf16 output, 4: BF16 weights). K % 8 == 0. */
+hipError_t apus_launch_wgemv(const void *w, const float *x, float *out, int M, int K, int O,
+                             int flags, hipStream_t st);
 /* hardware E4M3 conversion vs the integer encoder over |x| <= 448 */
 hipError_t apus_launch_e4m3_hw_check(unsigned *bad, unsigned *last_bad, hipStream_t st);
 /* out = bf16(a + b) */

@@ -339,6 +339,94 @@ hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,
     return hipGetLastError();
 }
 
+/* ------------------------------------------------- plain-weight GEMV */
+
+/* Plain-weight linears (c/attn.h:600-666 apus_f32_linear / apus_bf16_linear,
+ * the wo_a rows of the f32_linear hook, c/model.h:585-647 apus_head_gemv):
+ * FP32 or BF16 weights, FP32 accumulation. A wave owns 4 output rows and
+ * sweeps K in 512-element steps, each lane taking 8 consecutive elements
+ * per row (one 16-byte BF16 load or two FP32 loads), against up to 8 rows
+ * of x; lane partials meet in a fixed xor-shuffle tree. The CPU sums each
+ * row sequentially, so results agree within FP32 summation error, not
+ * bitwise. Launch row y covers x rows [8y, 8y + 8). */
+#define APUS_WG_NR 4
+template <bool WB>
+__global__ __launch_bounds__(256) void apus_wgemv_kernel(const void *__restrict__ w,
+                                                         const float *__restrict__ x,
+                                                         float *__restrict__ out, int M, int K,
+                                                         int O, int flags) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int o0 = (blockIdx.x * 4 + wave) * APUS_WG_NR;
+    const int m0 = blockIdx.y * 8;
+    const int mb = min(8, M - m0);
+    const bool rin = flags & 1;
+    float acc[8][APUS_WG_NR];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int r = 0; r < APUS_WG_NR; ++r) acc[m][r] = 0.0f;
+    for (int k = lane * 8; k < K; k += 512) {
+        float wv[APUS_WG_NR][8];
+#pragma unroll
+        for (int r = 0; r < APUS_WG_NR; ++r) {
+            const int o = min(o0 + r, O - 1);
+            if constexpr (WB) {
+                const uint4 u = apus_gld<uint4>((const uint16_t *)w + (size_t)o * K + k);
+                const unsigned q[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    wv[r][2 * i] = __uint_as_float(q[i] << 16);
+                    wv[r][2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
+                }
+            } else {
+                const float *p = (const float *)w + (size_t)o * K + k;
+                const float4 a = apus_gld<float4>(p), b = apus_gld<float4>(p + 4);
+                wv[r][0] = a.x; wv[r][1] = a.y; wv[r][2] = a.z; wv[r][3] = a.w;
+                wv[r][4] = b.x; wv[r][5] = b.y; wv[r][6] = b.z; wv[r][7] = b.w;
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            if (m < mb) {
+                const float *p = x + (size_t)(m0 + m) * K + k;
+                const float4 a = apus_gld<float4>(p), b = apus_gld<float4>(p + 4);
+                float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                if (rin) {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xv[i] = apus_bf16_rne(xv[i]);
+                }
+#pragma unroll
+                for (int r = 0; r < APUS_WG_NR; ++r)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) acc[m][r] = __builtin_fmaf(wv[r][i], xv[i], acc[m][r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        if (m < mb) {
+#pragma unroll
+            for (int r = 0; r < APUS_WG_NR; ++r) {
+                float v = acc[m][r];
+#pragma unroll
+                for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+                if (lane == 0 && o0 + r < O)
+                    out[(size_t)(m0 + m) * O + o0 + r] = (flags & 2) ? apus_bf16_rne(v) : v;
+            }
+        }
+    }
+}
+
+hipError_t apus_launch_wgemv(const void *w, const float *x, float *out, int M, int K, int O,
+                             int flags, hipStream_t st) {
+    if (M <= 0 || O <= 0) return hipSuccess;
+    if (K <= 0 || K % 8) return hipErrorInvalidValue;
+    dim3 grid((O + 4 * APUS_WG_NR - 1) / (4 * APUS_WG_NR), (M + 7) / 8), block(256);
+    if (flags & 4) hipLaunchKernelGGL(apus_wgemv_kernel<true>, grid, block, 0, st, w, x, out, M, K, O, flags);
+    else           hipLaunchKernelGGL(apus_wgemv_kernel<false>, grid, block, 0, st, w, x, out, M, K, O, flags);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------- E4M3 conversion check */
 
 /* Every fp32 input x with |x| <= 448 (both signs): the hardware conversion

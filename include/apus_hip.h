@@ -46,7 +46,26 @@ extern "C" {
 /* c/st.h:88-89 */
 typedef struct { const uint8_t *codes, *scales; int64_t O, K; } ApusFp8W;
 typedef struct { const uint8_t *packed, *scales; int64_t O, K; } ApusFp4W;
+/* c/st.h:40-53 — a tensor view (the head GEMV hook takes one) */
+typedef enum {
+    APUS_ST_I8, APUS_ST_U8, APUS_ST_F8_E8M0, APUS_ST_F8_E4M3,
+    APUS_ST_BF16, APUS_ST_F16, APUS_ST_F32, APUS_ST_I32, APUS_ST_I64,
+    APUS_ST_OTHER
+} ApusStDtype;
+typedef struct {
+    char        name[160];
+    ApusStDtype dtype;
+    int         ndim;
+    int64_t     shape[8];
+    const void *data;
+    size_t      nbytes;
+} ApusStTensor;
 #endif
+
+/* f32_linear hook flags (c/backend_metal.h:56-61) */
+#define APUS_HIP_R_IN   1      /* BF16-round the input elements */
+#define APUS_HIP_R_OUT  2      /* BF16-round the output */
+#define APUS_HIP_W_BF16 4      /* w holds BF16 bits (uint16), not FP32 */
 
 #ifndef APUS_FP4_H
 /* c/fp4.h:184-188 — one entry of a grouped same-(O,K) MXFP4 GEMM */
@@ -89,7 +108,7 @@ typedef struct {
                       int M, int K, int O);
     int (*f32_linear)(const float *w, const float *x, float *out,
                       int M, int K, int O, int flags);
-    int (*head_gemv)(const void *head, const float *x, float *out,
+    int (*head_gemv)(const ApusStTensor *head, const float *x, float *out,
                      int64_t O, int64_t K);
     int (*fp4_linear)(const ApusFp4W *w, const float *x, float *out,
                       int M, int K, int O);
@@ -123,6 +142,16 @@ int apus_hip_fp8_linear(const ApusFp8W *w, const float *x, float *out,
 /* c/attn.h:432-448 apus_fp4_linear: same with an MXFP4 weight. */
 int apus_hip_fp4_linear(const ApusFp4W *w, const float *x, float *out,
                         int M, int K, int O);
+/* c/attn.h:600-666 plain-weight linears (the f32_linear hook): FP32
+ * accumulate over w [O, K] (FP32, or BF16 bits with APUS_HIP_W_BF16) and
+ * x [M, K]; APUS_HIP_R_IN / R_OUT round input / output to BF16 (router gate:
+ * 0; apus_bf16_linear: R_IN|R_OUT; wo_a groups: R_OUT|W_BF16). K % 8 == 0. */
+int apus_hip_f32_linear(const float *w, const float *x, float *out, int M, int K, int O,
+                        int flags);
+/* c/model.h:638-647 apus_head_gemv: out [O] = head [O, K] (BF16 or F32 view)
+ * times x [K], FP32 accumulate, unrounded. */
+int apus_hip_head_gemv(const ApusStTensor *head, const float *x, float *out, int64_t O,
+                       int64_t K);
 /* c/fp4.h:936-986 apus_fp4_gemm_mt_grouped on pre-quantised activations
  * acodes [rows, K] / as [rows, K/128]; entry i writes ents[i].out [M, O]
  * (unrounded FP32) from activation rows [m0, m0+M). */
@@ -254,6 +283,11 @@ int      apus_hip_moe_routed_dev(const ApusHipStore *st, int layer,
                                  const float *x, const int32_t *idx,
                                  const float *wgt, int s, int topk,
                                  float limit, float *y, void *workspace);
+
+/* Plain-weight linear on device pointers (asynchronous): same semantics and
+ * flags as apus_hip_f32_linear. */
+int      apus_hip_wlinear_dev(const void *w, const float *x, float *out, int M, int K,
+                              int O, int flags);
 
 /* ---- apus model containers: routed-expert slabs on disk -> the store ----
  *

@@ -483,3 +483,49 @@ void orc_fill_bytes(uint64_t seed, uint64_t stream, uint64_t first,
         }
     }
 }
+
+
+/* ---- plain-weight linears (c/attn.h:600-666, c/model.h:585-647) ---- */
+
+static float orc_wl_weight(const void *w, size_t i, int bf16) {
+    if (!bf16) return ((const float *)w)[i];
+    const uint32_t u = (uint32_t)((const uint16_t *)w)[i] << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+void orc_wlinear(const void *w, const float *x, float *out, int M, int K, int O, int flags) {
+    const int bf16 = (flags & ORC_W_BF16) != 0;
+    for (int m = 0; m < M; m++) {
+        for (int o = 0; o < O; o++) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; k++) {
+                float xv = x[(size_t)m * K + k];
+                if (flags & ORC_W_R_IN) xv = orc_bf16_round(xv);
+                const float p = orc_wl_weight(w, (size_t)o * K + k, bf16) * xv;
+                acc = acc + p;
+            }
+            out[(size_t)m * O + o] = (flags & ORC_W_R_OUT) ? orc_bf16_round(acc) : acc;
+        }
+    }
+}
+
+void orc_wlinear_truth_f64(const void *w, const float *x, double *truth, double *esc,
+                           int M, int K, int O, int flags) {
+    const int bf16 = (flags & ORC_W_BF16) != 0;
+    for (int m = 0; m < M; m++) {
+        for (int o = 0; o < O; o++) {
+            double t = 0.0, e = 0.0;
+            for (int k = 0; k < K; k++) {
+                float xv = x[(size_t)m * K + k];
+                if (flags & ORC_W_R_IN) xv = orc_bf16_round(xv);
+                const double p = (double)orc_wl_weight(w, (size_t)o * K + k, bf16) * (double)xv;
+                t += p;
+                e += fabs(p);
+            }
+            truth[(size_t)m * O + o] = t;
+            esc[(size_t)m * O + o] = e;
+        }
+    }
+}

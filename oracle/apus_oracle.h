@@ -28,6 +28,9 @@
  *       reference MoE on the same libm.
  *   orc_moe_routed: bitwise vs the compiled reference apus_moe_forward's
  *       routed output (ApusMoeInterm.moe_routed) on the same routing.
+ *   orc_wlinear: bitwise vs the compiled reference apus_f32_linear,
+ *       apus_bf16_linear and apus_head_gemv (F32 and BF16 views); the BF16
+ *       weight form equals the FP32 form on exactly widened weights.
  */
 #ifndef APUS_ORACLE_H
 #define APUS_ORACLE_H
@@ -123,6 +126,21 @@ void    orc_moe_forward(const float *gate_w, const float *gate_bias, int hash,
                         int E, int topk, int dim, int inter, const float *x, int s,
                         float *out, float *routed, float *shared, float *sp,
                         int32_t *idx, float *wgt);
+/* Plain-weight linears: c/attn.h:600-666 apus_bf16_linear / apus_f32_linear
+ * (and the wo_a rows of the f32_linear hook, c/attn.h:1690-1735),
+ * c/model.h:585-647 apus_head_gemv. out[m, o] = sum_k w[o, k] * x'[m, k]
+ * in k order from +0, each product and sum rounded to FP32; x' = bf16(x)
+ * with ORC_W_R_IN, out rounded to BF16 with ORC_W_R_OUT; w is FP32, or BF16
+ * bits widened exactly with ORC_W_BF16 (the hook flags of
+ * c/backend_metal.h:56-61). */
+#define ORC_W_R_IN  1
+#define ORC_W_R_OUT 2
+#define ORC_W_BF16  4
+void    orc_wlinear(const void *w, const float *x, float *out, int M, int K, int O,
+                    int flags);
+/* float64 truth of the same products (x' as above) and esc = sum |w x'| */
+void    orc_wlinear_truth_f64(const void *w, const float *x, double *truth, double *esc,
+                              int M, int K, int O, int flags);
 void    orc_fp4_truth_f64(const uint8_t *w, const uint8_t *ws,
                           const uint8_t *acodes, const float *as,
                           double *out, double *esc,

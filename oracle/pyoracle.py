@@ -60,6 +60,9 @@ class Oracle:
                                            C.POINTER(C.c_uint32)]),
             "orc_hash64": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
             "orc_fill_bytes": (None, [C.c_uint64, C.c_uint64, C.c_uint64, u8p, sz, C.c_int]),
+            "orc_wlinear": (None, [C.c_void_p, f32p, f32p, C.c_int, C.c_int, C.c_int, C.c_int]),
+            "orc_wlinear_truth_f64": (None, [C.c_void_p, f32p, f64p, f64p, C.c_int, C.c_int,
+                                             C.c_int, C.c_int]),
             "orc_moe_forward": (None, [f32p, f32p, C.c_int, i64p, i64p, C.c_float, C.c_float]
                                 + [u8pp] * 6 + [u8p] * 6 + [C.c_int] * 4
                                 + [f32p, C.c_int, f32p, f32p, f32p, f32p, i32p, f32p]),
@@ -183,6 +186,27 @@ class Oracle:
                                _p(idx, i32p), _p(wgt, f32p))
         return (*res, sp, idx, wgt)
 
+    def wlinear(self, w, x, flags):
+        """orc_wlinear: w [O, K] float32, or uint16 BF16 bits (flag 4)."""
+        w = np.ascontiguousarray(w)
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        O = w.shape[0]
+        assert (w.dtype == np.uint16) == bool(flags & 4)
+        out = np.empty((M, O), np.float32)
+        self.L.orc_wlinear(w.ctypes.data, _p(x, f32p), _p(out, f32p), M, K, O, flags)
+        return out
+
+    def wlinear_truth(self, w, x, flags):
+        w = np.ascontiguousarray(w)
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        O = w.shape[0]
+        t, e = np.empty((M, O), np.float64), np.empty((M, O), np.float64)
+        self.L.orc_wlinear_truth_f64(w.ctypes.data, _p(x, f32p), _p(t, f64p), _p(e, f64p), M, K, O,
+                                     flags)
+        return t, e
+
     def fill_bytes(self, seed, stream, n, kind, first=0):
         out = np.empty(n, np.uint8)
         self.L.orc_fill_bytes(seed, stream, first, _p(out, u8p), n, kind)
@@ -192,6 +216,15 @@ class Oracle:
         bad = C.c_uint32()
         n = self.L.orc_pin_unary(which, fnptr, lo, hi, C.byref(bad))
         return n, bad.value
+
+
+ST_BF16, ST_F32 = 4, 6   # c/st.h:40-44 ApusStDtype
+
+
+class StTensor(C.Structure):
+    """c/st.h:46-53 ApusStTensor (a tensor view; the head GEMV hook takes one)."""
+    _fields_ = [("name", C.c_char * 160), ("dtype", C.c_int), ("ndim", C.c_int),
+                ("shape", C.c_int64 * 8), ("data", C.c_void_p), ("nbytes", C.c_size_t)]
 
 
 class _WeightView(C.Structure):
@@ -255,6 +288,9 @@ class Reference:
             "ref_moe_forward": (None, [C.c_int] * 4 + [C.c_float, C.c_float, C.c_int, f32p, f32p,
                                                         i64p, i64p] + [u8pp] * 6 + [u8p] * 6
                                 + [f32p, C.c_int, f32p, f32p, f32p, f32p, i32p, f32p]),
+            "apus_f32_linear": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
+            "apus_bf16_linear": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
+            "apus_head_gemv": (None, [C.c_void_p, f32p, f32p, C.c_int64, C.c_int64]),
             "ref_store_index": (C.c_int, [C.c_char_p, C.c_int, C.c_int, C.c_int, i32p, u64p, u64p,
                                           u32p, i64p, i64p, C.c_char_p, C.c_int,
                                           C.POINTER(C.c_int), u8p, C.c_char_p, C.c_size_t]),
@@ -306,6 +342,38 @@ class Reference:
         h = np.empty_like(g)
         self.L.ref_swiglu(_p(g, f32p), _p(u, f32p), _p(h, f32p), g.size, limit)
         return h
+
+    def f32_linear(self, w, x):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        out = np.empty((M, w.shape[0]), np.float32)
+        self.L.apus_f32_linear(_p(np.ascontiguousarray(w, np.float32), f32p), _p(x, f32p),
+                               _p(out, f32p), M, K, w.shape[0])
+        return out
+
+    def bf16_linear(self, w, x):
+        x = np.ascontiguousarray(x, np.float32)
+        M, K = x.shape
+        out = np.empty((M, w.shape[0]), np.float32)
+        self.L.apus_bf16_linear(_p(np.ascontiguousarray(w, np.float32), f32p), _p(x, f32p),
+                                _p(out, f32p), M, K, w.shape[0])
+        return out
+
+    def head_gemv(self, w, x):
+        """apus_head_gemv over an F32 (float32 w) or BF16 (uint16 w) view."""
+        w = np.ascontiguousarray(w)
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        O, K = w.shape
+        t = StTensor()
+        t.name = b"head"
+        t.dtype = ST_BF16 if w.dtype == np.uint16 else ST_F32
+        t.ndim = 2
+        t.shape[0], t.shape[1] = O, K
+        t.data = w.ctypes.data
+        t.nbytes = w.nbytes
+        out = np.empty(O, np.float32)
+        self.L.apus_head_gemv(C.byref(t), _p(x, f32p), _p(out, f32p), O, K)
+        return out
 
     def store_index(self, path, n_layers, n_mtp, E, with_slabs=False):
         """The reference expert store's slab records (apus_store_open):

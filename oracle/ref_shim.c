@@ -1,6 +1,7 @@
 /*
  * oracle/ref_shim.c — builds the reference's OWN CPU kernels (c/fp4.h,
  * c/fp8.h, c/attn.h linears, c/moe.h dispatch, c/cache.h expert store,
+ * c/model.h head GEMV (with c/layer.h, which it needs),
  * c/pool.h, c/x86.h) from the
  * sources where they lie under the apus checkout (-I <apus>/c) into
  * oracle/_ref/libapus_ref.so. Nothing from the reference is copied here:
@@ -19,6 +20,8 @@
 #define APUS_ATTN_IMPLEMENTATION
 #define APUS_MOE_IMPLEMENTATION
 #define APUS_CACHE_IMPLEMENTATION
+#define APUS_LAYER_IMPLEMENTATION
+#define APUS_MODEL_IMPLEMENTATION
 #include "compat.h"
 #include "fp4.h"
 #include "fp8.h"
@@ -28,6 +31,8 @@
 #include "attn.h"
 #include "moe.h"
 #include "cache.h"
+#include "layer.h"
+#include "model.h"
 
 #include <stdlib.h>
 #include <string.h>

@@ -327,3 +327,28 @@ def test_router_edges_restatement_vs_reference(oracle, ref, rng, case):
     else:
         dots = x.astype(np.float64) @ cfg["gate_w"].T.astype(np.float64)
         assert (dots > 20).any()
+
+
+@pytest.mark.parametrize("M,K,O", [(1, 256, 37), (3, 1000, 20), (5, 4096, 9)])
+def test_wlinear_restatement_vs_reference(oracle, ref, rng, M, K, O):
+    """orc_wlinear equals the reference's plain-weight linears bit for bit:
+    apus_f32_linear (flags 0), apus_bf16_linear (R_IN | R_OUT),
+    apus_head_gemv over F32 and BF16 views (M = 1), and the BF16-weight form
+    (W_BF16, used by the wo_a hook) equals apus_f32_linear on the exactly
+    widened weights."""
+    from helpers import bf16
+    w = (rng.standard_normal((O, K)) / np.sqrt(K)).astype(np.float32)
+    x = (rng.standard_normal((M, K)) * 3).astype(np.float32)
+    assert np.array_equal(oracle.wlinear(w, x, 0).view(np.uint32), ref.f32_linear(w, x).view(np.uint32))
+    assert np.array_equal(oracle.wlinear(w, x, 3).view(np.uint32), ref.bf16_linear(w, x).view(np.uint32))
+    wb = (w.view(np.uint32) >> 16).astype(np.uint16)            # BF16 bits (truncated)
+    widened = (wb.astype(np.uint32) << 16).view(np.float32)
+    assert np.array_equal(oracle.wlinear(wb, x, 6).view(np.uint32),
+                          bf16(ref.f32_linear(widened, x)).view(np.uint32))
+    assert np.array_equal(oracle.wlinear(w, x[:1], 0)[0].view(np.uint32),
+                          ref.head_gemv(w, x[:1]).view(np.uint32))
+    assert np.array_equal(oracle.wlinear(wb, x[:1], 4)[0].view(np.uint32),
+                          ref.head_gemv(wb, x[:1]).view(np.uint32))
+    truth, esc = oracle.wlinear_truth(w, x, 0)
+    got = oracle.wlinear(w, x, 0).astype(np.float64)
+    assert np.all(np.abs(got - truth) <= K * 2.0 ** -24 * esc + 1e-30)
