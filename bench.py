@@ -284,6 +284,26 @@ def bench_attn_fp8(H, dev, steps=64, M=1, copies=8, tiled=True):
     return out
 
 
+def bench_head(H, dev, steps=16, O=129280, K=4096):
+    """LM-head GEMV (reference/config.json vocab 129280 x dim 4096, BF16
+    weights, 1.06 GB: far beyond the 256 MB Infinity Cache), one token,
+    FP32 accumulate, through apus_hip_wlinear_dev."""
+    L = H.lib()
+    wb = O * K * 2
+    w = dev.alloc(wb)
+    H._check(L.apus_hip_fill_random(w.ptr, wb, 5, 7, 1), "fill")   # finite BF16 patterns
+    x = dev.upload(np.random.default_rng(2).standard_normal((1, K)).astype(np.float32))
+    y = dev.alloc(O * 4)
+
+    def step(i):
+        H._check(L.apus_hip_wlinear_dev(w.ptr, x.ptr, y.ptr, 1, K, O, 4), "head")
+
+    step(0)
+    H.synchronize()
+    us = timed_graph(H, step, steps) * 1e3 / steps
+    return {"us": us, "GBs": wb / us / 1e3}
+
+
 def zipf_routing(rng, s, E, topk, a):
     """top-k distinct experts per token with popularity ~ rank^-a (random rank order)."""
     p = 1.0 / np.arange(1, E + 1) ** a
@@ -581,6 +601,9 @@ def main():
         extras["config1_fp8_M1_us"] = round(f8["M1"]["us"], 2)
         extras["config1_fp8_M512_TFLOPs"] = round(f8["M512"]["tflops"], 1)
         extras["config1_fp8_M512_us"] = round(f8["M512"]["us"], 2)
+        hd = bench_head(H, dev)
+        extras["lm_head_bf16_us"] = round(hd["us"], 1)
+        extras["lm_head_bf16_GBs"] = round(hd["GBs"], 1)
         for name, r in bench_attn_fp8(H, dev).items():
             extras[f"attn_{name}_M1_us"] = round(r["us"], 2)
             extras[f"attn_{name}_M1_GBs"] = round(r["GBs"], 1)
