@@ -363,7 +363,7 @@ __device__ __forceinline__ ApusGemmEnt apus_entry_of(const ApusGemmArgs &a, int 
     return ent;
 }
 
-/* Quantising staging of activation rows into LDS (codes [R][K + 16], E8M0
+/* Quantising staging of activation rows into LDS (codes [R][K + 32], E8M0
  * bytes [R][K/128]). Eight lanes own one 128-group (16 elements each); a
  * wave covers 8 groups per pass, a pass 32 groups. The loads of a pass and
  * its quantisation are separate steps so that the first pass's loads can be
@@ -402,7 +402,7 @@ __device__ __forceinline__ void apus_stage_load(const ApusGemmArgs &a, const int
 template <int K, int ASRC>
 __device__ __forceinline__ void apus_stage_quant(const ApusGemmArgs &a, const ApusStageRaw<ASRC> &r,
                                                  uint8_t *lcodes, uint8_t *lsc) {
-    constexpr int NQ = K / 128, LDK = K + 16;
+    constexpr int NQ = K / 128, LDK = K + 32;
     const int sub = threadIdx.x & 7;
     if (!r.ok) return;
     float v[16];
@@ -440,7 +440,7 @@ template <int WF, int R, int NS, int PD, int KS, int ASRC>
 __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int last_ticket;
-    constexpr int K = NS * 512, NQ = NS * 4, K16 = K / 16, LDK = K + 16;
+    constexpr int K = NS * 512, NQ = NS * 4, K16 = K / 16, LDK = K + 32;
     constexpr int NSW = NS / KS;                       /* slices per wave */
     constexpr int TPW = APUS_DEC_WAVES / KS;           /* row tiles per workgroup */
     static_assert(NS % KS == 0 && PD <= NSW && APUS_DEC_WAVES % KS == 0, "decode shape");
@@ -675,7 +675,7 @@ template <int WF, int NS, int TT, int PD>
 __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs args) {
     constexpr int K = NS * 512, NQ = NS * 4;
     constexpr int ROWS = 16 * TT;                 /* activation rows per chunk */
-    constexpr int PITCH = 512 + 16;               /* LDS bytes per row per slice */
+    constexpr int PITCH = 512 + 32;               /* LDS bytes per row per slice (measured best of 8..96 pad) */
     constexpr int CHUNKS = ROWS * 32 / 512;       /* 16-byte loads per thread per slice */
     static_assert(WF != APUS_W_FP4 || ROWS == APUS_PREFILL_ROWS, "work-list chunk");
     __shared__ __align__(16) uint8_t abuf[2][ROWS * PITCH];
@@ -1073,7 +1073,7 @@ __device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const
 
 template <int NS, bool SH>
 __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args) {
-    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 16;
+    constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 32;
     __shared__ __align__(16) uint8_t lcodes[LDK];
     __shared__ uint8_t lsc[NQ];
     __shared__ float lgu[2][2][64];            /* [mat][tile][lane] */
@@ -1308,7 +1308,7 @@ void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
     constexpr int NSW = NS / KS, PDD = WF == APUS_W_FP4 ? 3 : 2;
     constexpr int PD = PDD < NSW ? PDD : NSW;
     constexpr int K = NS * 512, NQ = NS * 4;
-    const size_t lds = (((size_t)R * (K + 16) + (size_t)R * NQ + 15) & ~(size_t)15) +
+    const size_t lds = (((size_t)R * (K + 32) + (size_t)R * NQ + 15) & ~(size_t)15) +
                        (KS > 1 ? 256 * sizeof(float) * 4 : 0);
     if (lds > 65536) {
         /* eight staged rows of K = 8192 need more than the default 64 KB */
