@@ -968,17 +968,18 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
  * FP8 shared w2 in the same workgroup: sh = bf16(w2 h) and the sublayer
  * output bf16(y + sh) (c/moe.h:588-589) are written too.
  */
-template <int WF, int NS>
+template <int WF, int NS, int TILES>
 __device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const ApusStageRaw<APUS_A_F32> &raw,
                                                  const ApusGemmEnt &ent, bool tiled, bool ok,
                                                  int hrow, uint8_t *lcodes, uint8_t *lsc,
-                                                 float (*lgu)[2][64]) {
+                                                 float (*lgu)[TILES][64]) {
     constexpr int K = NS * 512;
-    constexpr int PD = 3;
+    /* 16-wave workgroups get at most 128 registers a lane: a shorter FP8 ring */
+    constexpr int PD = (TILES == 8 && WF == APUS_W_FP8) ? 2 : 3;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int mat = wave & 1, tile = wave >> 1;
-    const int o = blockIdx.x * 32 + tile * 16 + r;
+    const int o = blockIdx.x * (16 * TILES) + tile * 16 + r;
     const ApusWLane wl = apus_wlane<WF>(ent, tiled, o, lane, K);
     ApusBFrag<WF> ring[PD];
 #pragma unroll
@@ -1020,6 +1021,28 @@ __device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const
      * pick the g == 0 lanes of the w1 and w3 waves */
     lgu[mat][tile][lane] = apus_bf16_rne(acc[0]);
     __syncthreads();
+    if constexpr (TILES == 8) {
+        /* the workgroup holds a whole 128-column group of h: quantise it
+         * here as the activation quantiser does (c/fp4.h:293-321: BF16,
+         * amax, E8M0 scale, E4M3 codes); threads 0..127 own one column */
+        __shared__ float lmax[2];
+        const int t = threadIdx.x >> 4, rr = threadIdx.x & 15;
+        float h = 0.0f;
+        if (threadIdx.x < 128)
+            h = ok ? apus_swiglu_h(lgu[0][t & 7][rr], lgu[1][t & 7][rr], args.limit) : 0.0f;
+        const float m = apus_wave_max(fabsf(h));
+        if (threadIdx.x < 128 && (threadIdx.x & 63) == 0) lmax[threadIdx.x >> 6] = m;
+        __syncthreads();
+        if (threadIdx.x < 128) {
+            const uint32_t e = apus_act_scale_exp(fmaxf(lmax[0], lmax[1]));
+            const float inv = apus_inv_pow2_from_exp(e);
+            const int G = args.O >> 7;
+            apus_gst<uint8_t>(args.hq + (size_t)hrow * args.O + blockIdx.x * 128 + threadIdx.x,
+                              (uint8_t)apus_e4m3_pack2_hw(h * inv, 0.0f));
+            if (threadIdx.x == 0) apus_gst<uint8_t>(args.hqs + (size_t)hrow * G + blockIdx.x, (uint8_t)e);
+        }
+        return;
+    }
     float *hdst = args.pout[0] + (size_t)hrow * args.O;
     if (threadIdx.x < 32) {
         const int t = threadIdx.x >> 4, rr = threadIdx.x & 15;
@@ -1071,14 +1094,14 @@ __device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const
     }
 }
 
-template <int NS, bool SH>
-__global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args) {
+template <int NS, bool SH, int TILES>
+__global__ __launch_bounds__(128 * TILES) void apus_moe_pair13_kernel(ApusGemmArgs args) {
     constexpr int K = NS * 512, NQ = NS * 4, LDK = K + 32;
     __shared__ __align__(16) uint8_t lcodes[LDK];
     __shared__ uint8_t lsc[NQ];
-    __shared__ float lgu[2][2][64];            /* [mat][tile][lane] */
+    __shared__ float lgu[2][TILES][64];        /* [mat][tile][lane] */
     if (args.zero && blockIdx.y == 0) {
-        for (int i = blockIdx.x * 256 + threadIdx.x; i < args.nzero; i += gridDim.x * 256)
+        for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < args.nzero; i += gridDim.x * blockDim.x)
             args.zero[i] = 0u;
     }
     const int mat = (threadIdx.x >> 6) & 1;
@@ -1091,7 +1114,7 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
         ApusGemmEnt ent;
         ent.w = mat ? args.shw[2] : args.shw[0];
         ent.ws = mat ? args.shws[2] : args.shws[0];
-        apus_pair13_body<APUS_W_FP8, NS>(args, raw, ent, args.sh_tiled, true, p, lcodes, lsc, lgu);
+        apus_pair13_body<APUS_W_FP8, NS, TILES>(args, raw, ent, args.sh_tiled, true, p, lcodes, lsc, lgu);
         return;
     }
     /* the pair's x row: its loads go out first */
@@ -1117,7 +1140,7 @@ __global__ __launch_bounds__(256) void apus_moe_pair13_kernel(ApusGemmArgs args)
     const bool ok = (unsigned)e < (unsigned)args.pE;
     ApusGemmEnt ent;
     apus_expert_ptrs(args, mat, ok ? e : 0, ent.w, ent.ws);
-    apus_pair13_body<APUS_W_FP4, NS>(args, raw, ent, args.wtiled, ok, p, lcodes, lsc, lgu);
+    apus_pair13_body<APUS_W_FP4, NS, TILES>(args, raw, ent, args.wtiled, ok, p, lcodes, lsc, lgu);
 }
 
 template <int NS, int NP, bool SH>
@@ -1255,22 +1278,33 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
 
 hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t st) {
     if (npairs <= 0) return hipSuccess;
-    if ((a->K != 2048 && a->K != 4096) || a->O % 128 || a->npairs != npairs ||
-        (a->hq && (!a->hqs || !a->hq_tk)))
-        return hipErrorInvalidValue;
+    if ((a->K != 2048 && a->K != 4096) || a->O % 32 || a->npairs != npairs) return hipErrorInvalidValue;
     const bool sh = a->shw[0] != nullptr;
     if (sh && (a->acc_s <= 0 || a->O % 128)) return hipErrorInvalidValue;
     if (a->rsp && (a->rE <= 0 || a->rE > 1024 || a->adiv > 16 || a->adiv > a->rE || !a->ridx ||
                    !a->rwgt || (!a->rt2e && !a->rsel) || (a->rt2e && !a->rids)))
         return hipErrorInvalidValue;
-    dim3 grid(a->O / 32, npairs + (sh ? a->acc_s : 0)), block(256);
-    if (a->K == 4096) {
-        if (sh) hipLaunchKernelGGL((apus_moe_pair13_kernel<8, true>), grid, block, 0, st, *a);
-        else    hipLaunchKernelGGL((apus_moe_pair13_kernel<8, false>), grid, block, 0, st, *a);
+    const int rows = npairs + (sh ? a->acc_s : 0);
+    /* 128-column workgroups (16 waves) quantise h themselves; 32-column ones
+     * hand it over through counters. The wide ones win once they give at
+     * least one workgroup per CU (4 tokens of top-6: 3.7 us less per
+     * layer), the narrow ones below that (one token: 5 us less).
+     * APUS_HIP_PAIR13_WIDE = 0 / 1 forces one. */
+    static const int force = [] {
+        const char *v = getenv("APUS_HIP_PAIR13_WIDE");
+        return v ? atoi(v) : -1;
+    }();
+    const bool wide = force >= 0 ? force != 0 : (size_t)(a->O / 128) * rows >= 256;
+#define APUS_P13(NS, SH, T) hipLaunchKernelGGL((apus_moe_pair13_kernel<NS, SH, T>), \
+        dim3(a->O / (16 * T), rows), dim3(128 * T), 0, st, *a)
+    if (wide && a->hq && a->O % 128 == 0 && !a->zero) {
+        if (a->K == 4096) { if (sh) APUS_P13(8, true, 8); else APUS_P13(8, false, 8); }
+        else              { if (sh) APUS_P13(4, true, 8); else APUS_P13(4, false, 8); }
     } else {
-        if (sh) hipLaunchKernelGGL((apus_moe_pair13_kernel<4, true>), grid, block, 0, st, *a);
-        else    hipLaunchKernelGGL((apus_moe_pair13_kernel<4, false>), grid, block, 0, st, *a);
+        if (a->K == 4096) { if (sh) APUS_P13(8, true, 2); else APUS_P13(8, false, 2); }
+        else              { if (sh) APUS_P13(4, true, 2); else APUS_P13(4, false, 2); }
     }
+#undef APUS_P13
     return hipGetLastError();
 }
 

@@ -180,13 +180,15 @@ def test_moe_forward_dev_exact_ties_pick_lowest_index(hip, oracle, store1, rng):
 
 
 @pytest.mark.parametrize("hash_,shared_tiled,s,topk", [(0, True, 2, 6), (1, False, 1, 6),
-                                                      (0, True, 12, 6), (0, False, 3, 4)])
+                                                      (0, True, 4, 6), (0, True, 12, 6),
+                                                      (0, False, 3, 4)])
 def test_moe_forward_dev_model_shape(hip, oracle, store1, rng, hash_, shared_tiled, s, topk):
     """Decode tokens at the model's shape (256 experts, dim 4096, inter 2048),
     the store filled on the device; host copies of only the experts the
     routing picks (the rest share a placeholder, which the dispatch never
     reads). The cases cover each routed mode's fused final sum (per-pair
-    kernels for top-6, the sorted pipeline for 72 pairs, the ticket path for
+    kernels for top-6, with 32-column w1/w3 workgroups for 1-2 tokens and
+    128-column ones, which quantise h themselves, for 4, the sorted pipeline for 72 pairs, the ticket path for
     top-4) and both shared-expert paths (up to 8 tokens: two fused launches;
     more: quantise, GEMMs, SwiGLU)."""
     from test_gpu_store import host_expert
