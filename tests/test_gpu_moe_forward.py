@@ -188,9 +188,9 @@ def test_moe_forward_dev_model_shape(hip, oracle, store1, rng, hash_, shared_til
     routing picks (the rest share a placeholder, which the dispatch never
     reads). The cases cover each routed mode's fused final sum (per-pair
     kernels for top-6, with 32-column w1/w3 workgroups for 1-2 tokens and
-    128-column ones, which quantise h themselves, for 4, the sorted pipeline for 72 pairs, the ticket path for
-    top-4) and both shared-expert paths (up to 8 tokens: two fused launches;
-    more: quantise, GEMMs, SwiGLU)."""
+    128-column ones, which quantise h themselves, for 4; the sorted pipeline
+    for 72 pairs; the ticket path for top-4) and both shared-expert paths (up
+    to 8 tokens: two fused launches; more: quantise, GEMMs, SwiGLU)."""
     from test_gpu_store import host_expert
     E, dim, inter, seed = 256, 4096, 2048, 3
     cfg, shared, x = _case(rng, E, dim, inter, s, topk, hash_)
