@@ -36,7 +36,7 @@ METRIC = "MXFP4 expert GEMV GB/s (%HBM peak) @M=1; MoE grouped-GEMM TFLOP/s @512
 # HBM bytes per grouped 12-GEMV launch measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (FETCH scaled x2.0 from a 256 MiB copy calibration); command and
 # counts in profiles/config0_mxfp4_gemv_m1.txt. Re-measure when the kernel changes.
-CONFIG0_TRAFFIC_BYTES = 53755063
+CONFIG0_TRAFFIC_BYTES = 53752438
 
 
 def log(*a):
