@@ -553,6 +553,57 @@ def cpu_baseline(O=2048, K=4096, budget_s=12.0):
                       f"reps, {best * 1e3:.3f} ms/GEMV"}
 
 
+def cpu_extras(budget_s=4.0):
+    """apus's own CPU kernels on the other GEMM configs (reported beside the
+    GPU extras, same host cores): config 1 FP8 M=1 and M=512
+    (apus_fp8_gemm_mt) and one config-3 expert's w1 at 64 rows
+    (apus_fp4_gemm_mt). Each is the best of 3 timings within ~budget_s."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    if not pyoracle.have_ref():
+        return {}
+    R = pyoracle.Reference()
+    rng = np.random.default_rng(1)
+
+    def best_of(fn):
+        fn()
+        t0 = time.perf_counter()
+        fn()
+        one = max(time.perf_counter() - t0, 1e-6)
+        reps = max(1, int(budget_s / 3 / one))
+        best = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fn()
+            dt = (time.perf_counter() - t0) / reps
+            best = dt if best is None else min(best, dt)
+        return best
+
+    out = {}
+    O = K = 4096
+    w8 = rng.integers(0, 0x7e, (O, K), dtype=np.uint8)
+    ws8 = rng.integers(117, 124, (O // 128, K // 128), dtype=np.uint8)
+    for M in (1, 512):
+        c, sc = R.act_quant(rng.standard_normal((M, K)).astype(np.float32))
+        t = best_of(lambda c=c, sc=sc: R.fp8_gemm_mt(w8, ws8, c, sc))
+        if M == 1:
+            out["cpu_config1_fp8_M1_us"] = round(t * 1e6, 1)
+            out["cpu_config1_fp8_M1_GBs"] = round((O * K + (O // 128) * (K // 128)) / t / 1e9, 2)
+        else:
+            out["cpu_config1_fp8_M512_us"] = round(t * 1e6, 1)
+            out["cpu_config1_fp8_M512_TFLOPs"] = round(2.0 * M * O * K / t / 1e12, 4)
+    O4, K4, M4 = 2048, 4096, 64
+    w4 = rng.integers(0, 256, (O4, K4 // 2), dtype=np.uint8)
+    ws4 = rng.integers(118, 131, (O4, K4 // 32), dtype=np.uint8)
+    c, sc = R.act_quant(rng.standard_normal((M4, K4)).astype(np.float32))
+    t = best_of(lambda: R.fp4_gemm_mt(w4, ws4, c, sc))
+    out["cpu_config3_expert_w1_M64_us"] = round(t * 1e6, 1)
+    out["cpu_config3_expert_w1_M64_TFLOPs"] = round(2.0 * M4 * O4 * K4 / t / 1e12, 4)
+    out["cpu_threads"] = int(R.L.ref_pool_threads())
+    return out
+
+
 # ------------------------------------------------------------------ main
 
 def main():
@@ -664,6 +715,9 @@ def main():
         H.synchronize()
         log(f"[bench] calibration copy: 2 x {nb} bytes")
     cpu = None if args.no_cpu else cpu_baseline()
+    if cpu is not None and not args.skip_extras:
+        log("[bench] CPU reference on configs 1 and 3 (samples)")
+        extras.update(cpu_extras())
     if g is None:
         print(json.dumps({"metric": METRIC, "extras": extras, "cpu_baseline": cpu}))
         return
