@@ -280,7 +280,10 @@ __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args
  * the same per-element steps as the standalone kernels, so the codes are
  * identical.
  */
+#ifndef APUS_DEC_WAVES
 #define APUS_DEC_WAVES 4
+#endif
+#define APUS_DEC_NT (64 * APUS_DEC_WAVES)
 
 /* The weight stream of one lane of a 16-row tile: the address of its
  * 16 bytes of 128-group 0 and the distance between consecutive groups (qs)
@@ -382,7 +385,7 @@ __device__ __forceinline__ void apus_stage_load(const ApusGemmArgs &a, const int
     constexpr int NQ = K / 128;
     const int sub = threadIdx.x & 7;
     /* rows * NQ is a multiple of 16, so this test is uniform over each wave */
-    const int gi = pass * 32 + (threadIdx.x >> 3);
+    const int gi = pass * (APUS_DEC_NT / 8) + (threadIdx.x >> 3);
     r.ok = gi < rows * NQ;
     r.row = gi / NQ;
     r.q = gi - r.row * NQ;
@@ -437,7 +440,7 @@ __device__ __forceinline__ void apus_stage_quant(const ApusGemmArgs &a, const Ap
 }
 
 template <int WF, int R, int NS, int PD, int KS, int ASRC>
-__global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args) {
+__global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmArgs args) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int last_ticket;
     constexpr int K = NS * 512, NQ = NS * 4, K16 = K / 16, LDK = K + 32;
@@ -445,7 +448,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
     constexpr int TPW = APUS_DEC_WAVES / KS;           /* row tiles per workgroup */
     static_assert(NS % KS == 0 && PD <= NSW && APUS_DEC_WAVES % KS == 0, "decode shape");
     if (args.zero && blockIdx.y == 0) {
-        for (int i = blockIdx.x * 256 + threadIdx.x; i < args.nzero; i += gridDim.x * 256)
+        for (int i = blockIdx.x * APUS_DEC_NT + threadIdx.x; i < args.nzero; i += gridDim.x * APUS_DEC_NT)
             args.zero[i] = 0u;
     }
     /* quantising staging: when the first chunk's activation rows are known
@@ -492,23 +495,23 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
 #pragma unroll
                 for (int j = 0; j < R; ++j) ridx[j] = ent.a0 + c0 + min(j, rows - 1);
             }
-            /* a row is K16 16-byte pieces: RPJ rows per pass of the 256
-             * threads when K16 <= 256, else CPR passes per row */
-            constexpr int RPJ = K16 <= 256 ? 256 / K16 : 1;
-            constexpr int CPR = K16 <= 256 ? 1 : K16 / 256;
-            constexpr int STAGE = K16 <= 256 ? R * K16 / 256 : R * CPR;
-            static_assert(RPJ >= 1 && R % RPJ == 0 && (K16 <= 256 || K16 % 256 == 0), "staging shape");
+            /* a row is K16 16-byte pieces: RPJ rows per pass of the APUS_DEC_NT
+             * threads when K16 <= APUS_DEC_NT, else CPR passes per row */
+            constexpr int RPJ = K16 <= APUS_DEC_NT ? APUS_DEC_NT / K16 : 1;
+            constexpr int CPR = K16 <= APUS_DEC_NT ? 1 : K16 / APUS_DEC_NT;
+            constexpr int STAGE = K16 <= APUS_DEC_NT ? R * K16 / APUS_DEC_NT : R * CPR;
+            static_assert(RPJ >= 1 && R % RPJ == 0 && (K16 <= APUS_DEC_NT || K16 % APUS_DEC_NT == 0), "staging shape");
             uint4 v[STAGE];
 #pragma unroll
             for (int j = 0; j < STAGE; ++j) {
                 int row, cc;
-                if constexpr (K16 <= 256) {
+                if constexpr (K16 <= APUS_DEC_NT) {
                     const int rsub = threadIdx.x / K16;         /* 0..RPJ-1 */
                     row = j * RPJ + rsub;
                     cc = threadIdx.x - rsub * K16;
                 } else {
                     row = j / CPR;
-                    cc = (j % CPR) * 256 + threadIdx.x;
+                    cc = (j % CPR) * APUS_DEC_NT + threadIdx.x;
                 }
                 int ar = ridx[0];
 #pragma unroll
@@ -518,11 +521,11 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
                 if (row < rows) v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);
                 else v[j] = uint4{0u, 0u, 0u, 0u};
             }
-            constexpr int SPT = (R * NQ + 255) / 256;          /* scales per thread */
+            constexpr int SPT = (R * NQ + APUS_DEC_NT - 1) / APUS_DEC_NT;   /* scales per thread */
             float scv[SPT];
 #pragma unroll
             for (int k = 0; k < SPT; ++k) {
-                const int si = threadIdx.x + 256 * k, srr = si / NQ;
+                const int si = threadIdx.x + APUS_DEC_NT * k, srr = si / NQ;
                 int sar = ridx[0];
 #pragma unroll
                 for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
@@ -536,19 +539,19 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
 #pragma unroll
             for (int j = 0; j < STAGE; ++j) {
                 int row, cc;
-                if constexpr (K16 <= 256) {
+                if constexpr (K16 <= APUS_DEC_NT) {
                     const int rsub = threadIdx.x / K16;
                     row = j * RPJ + rsub;
                     cc = threadIdx.x - rsub * K16;
                 } else {
                     row = j / CPR;
-                    cc = (j % CPR) * 256 + threadIdx.x;
+                    cc = (j % CPR) * APUS_DEC_NT + threadIdx.x;
                 }
                 if (row < rows) *reinterpret_cast<uint4 *>(lcodes + row * LDK + cc * 16) = v[j];
             }
 #pragma unroll
             for (int k = 0; k < SPT; ++k) {
-                const int si = threadIdx.x + 256 * k;
+                const int si = threadIdx.x + APUS_DEC_NT * k;
                 if (si < R * NQ && si / NQ < rows) lsc[si] = (uint8_t)apus_e8m0_of(scv[k]);
             }
         } else {
@@ -561,7 +564,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
 #pragma unroll
             for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, sbase + u);
             apus_stage_quant<K, ASRC>(args, r0, lcodes, lsc);
-            constexpr int PASSES = (R * NQ + 31) / 32;
+            constexpr int PASSES = (R * NQ + APUS_DEC_NT / 8 - 1) / (APUS_DEC_NT / 8);
 #pragma unroll
             for (int pass = 1; pass < PASSES; ++pass) {
                 ApusStageRaw<ASRC> rp;
@@ -643,7 +646,7 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
             constexpr int TW = 16 * TPW;
             const float *eo = args.pout[0];
             const int topk = args.acc_topk;
-            for (int i = threadIdx.x; i < args.acc_s * TW; i += 256) {
+            for (int i = threadIdx.x; i < args.acc_s * TW; i += APUS_DEC_NT) {
                 const int t = i / TW, oo = blockIdx.x * TW + (i - t * TW);
                 float y = 0.0f;
                 for (int j = 0; j < topk; ++j) {
@@ -669,14 +672,17 @@ __global__ __launch_bounds__(256) void apus_gemm_decode_kernel(ApusGemmArgs args
  * token tiles, so the weights are streamed from HBM once per chunk.
  * K = 512 * NS is a template constant (straight-line slice loop).
  */
+#ifndef APUS_PRE_WAVES
 #define APUS_PRE_WAVES 8
+#endif
+#define APUS_PRE_THREADS (64 * APUS_PRE_WAVES)
 
 template <int WF, int NS, int TT, int PD>
-__global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs args) {
+__global__ __launch_bounds__(APUS_PRE_THREADS, 2) void apus_gemm_prefill_kernel(ApusGemmArgs args) {
     constexpr int K = NS * 512, NQ = NS * 4;
     constexpr int ROWS = 16 * TT;                 /* activation rows per chunk */
     constexpr int PITCH = 512 + 32;               /* LDS bytes per row per slice (measured best of 8..96 pad) */
-    constexpr int CHUNKS = ROWS * 32 / 512;       /* 16-byte loads per thread per slice */
+    constexpr int CHUNKS = ROWS * 32 / APUS_PRE_THREADS;   /* 16-byte loads per thread per slice */
     static_assert(WF != APUS_W_FP4 || ROWS == APUS_PREFILL_ROWS, "work-list chunk");
     __shared__ __align__(16) uint8_t abuf[2][ROWS * PITCH];
     __shared__ uint8_t sbuf[2][ROWS * 4];
@@ -696,12 +702,13 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
 
     for (int c0 = cfirst; c0 < ent.M; c0 += cstep) {
         const int rows = min(ROWS, ent.M - c0);
+        const int ntile = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
         /* the activation rows this thread stages (rows past the entry repeat
          * its last row; their outputs are never stored) */
         const uint8_t *abase[CHUNKS];
 #pragma unroll
         for (int j = 0; j < CHUNKS; ++j) {
-            const int i = threadIdx.x + j * 512;
+            const int i = threadIdx.x + j * APUS_PRE_THREADS;
             const int rr = min(i >> 5, rows - 1);
             const int ar = ent.arows ? apus_gld<int>(ent.arows + (c0 + rr)) : ent.a0 + c0 + rr;
             abase[j] = args.acodes + (size_t)ar * K + (i & 31) * 16;
@@ -720,7 +727,7 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
 #define APUS_PRE_STORE(B)                                                      \
         do {                                                                   \
             _Pragma("unroll") for (int j = 0; j < CHUNKS; ++j) {               \
-                const int i = threadIdx.x + j * 512;                           \
+                const int i = threadIdx.x + j * APUS_PRE_THREADS;              \
                 *reinterpret_cast<uint4 *>(&abuf[B][(i >> 5) * PITCH + (i & 31) * 16]) = v[j]; \
             }                                                                  \
             if (threadIdx.x < ROWS * 4) sbuf[B][threadIdx.x] = (uint8_t)apus_e8m0_of(sv); \
@@ -745,10 +752,12 @@ __global__ __launch_bounds__(512) void apus_gemm_prefill_kernel(ApusGemmArgs arg
             const uint8_t *ab = abuf[s & 1];
             const uint8_t *sb8 = sbuf[s & 1];
             {
-                /* all TT tiles every time: a partial chunk multiplies repeated
-                 * rows whose outputs are not stored (no branch in the loop) */
+                /* only the chunk's token tiles (a wave-uniform test); the
+                 * rows of a partial last tile repeat the chunk's last row and
+                 * their outputs are not stored */
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
+                    if (t >= ntile) break;
                     const uint8_t *ap = ab + (t * 16 + r) * PITCH + g * 16;
 #pragma unroll
                     for (int st = 0; st < 4; ++st) {
@@ -1339,11 +1348,14 @@ namespace {
 
 template <int WF, int R, int NS, int KS, int ASRC>
 void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
-    constexpr int NSW = NS / KS, PDD = WF == APUS_W_FP4 ? 3 : 2;
+#ifndef APUS_DEC_PD_FP4
+#define APUS_DEC_PD_FP4 3
+#endif
+    constexpr int NSW = NS / KS, PDD = WF == APUS_W_FP4 ? APUS_DEC_PD_FP4 : 2;
     constexpr int PD = PDD < NSW ? PDD : NSW;
     constexpr int K = NS * 512, NQ = NS * 4;
     const size_t lds = (((size_t)R * (K + 32) + (size_t)R * NQ + 15) & ~(size_t)15) +
-                       (KS > 1 ? 256 * sizeof(float) * 4 : 0);
+                       (KS > 1 ? APUS_DEC_NT * sizeof(float) * 4 : 0);
     if (lds > 65536) {
         /* eight staged rows of K = 8192 need more than the default 64 KB */
         static const hipError_t attr = hipFuncSetAttribute(
@@ -1351,7 +1363,7 @@ void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         (void)attr;
     }
-    dim3 gd(d.O / (16 * APUS_DEC_WAVES / KS), n_ent), bd(256);
+    dim3 gd(d.O / (16 * APUS_DEC_WAVES / KS), n_ent), bd(APUS_DEC_NT);
     hipLaunchKernelGGL((apus_gemm_decode_kernel<WF, R, NS, PD, KS, ASRC>), gd, bd, lds, st, d);
 }
 
@@ -1360,7 +1372,7 @@ void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
  * slice's weight loads and runs out of registers) */
 template <int WF, int R, int NS, int ASRC>
 void apus_launch_dec_ns(const ApusGemmArgs &d, int n_ent, int ks, hipStream_t st) {
-    if constexpr (NS >= 4) {
+    if constexpr (NS >= 4 && APUS_DEC_WAVES % 4 == 0) {
         if (ks == 4) { apus_launch_dec<WF, R, NS, 4, ASRC>(d, n_ent, st); return; }
     }
     if constexpr (R != 1) {
@@ -1478,10 +1490,14 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
         p.m_min = R;
         p.m_max = 0;
         /* with a work list, n_ent counts its items */
-        dim3 gp(a->O / (16 * APUS_PRE_WAVES), n_ent), bp(512);
+        dim3 gp(a->O / (16 * APUS_PRE_WAVES), n_ent), bp(APUS_PRE_THREADS);
         if (wfmt == APUS_W_FP4) {
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, 4, 2>), gp, bp, 0, st, p);
-            else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, 4, 2>), gp, bp, 0, st, p);
+#ifndef APUS_PRE_PD4
+#define APUS_PRE_PD4 2
+#endif
+            constexpr int TT4 = APUS_PREFILL_ROWS / 16;
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4>), gp, bp, 0, st, p);
+            else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4>), gp, bp, 0, st, p);
         } else {
             if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 8, 2, 2>), gp, bp, 0, st, p);
             else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 4, 2, 2>), gp, bp, 0, st, p);

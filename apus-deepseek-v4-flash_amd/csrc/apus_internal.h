@@ -116,7 +116,9 @@ static inline bool apus_group_k(int K) { return K == 2048 || K == 4096; }
 
 /* rows (tokens) per chunk of the many-row (prefill) schedule for MXFP4
  * weights: one work-list item */
+#ifndef APUS_PREFILL_ROWS
 #define APUS_PREFILL_ROWS 64
+#endif
 
 /* One-token-chunk MoE dispatch for few routed pairs (decode), MXFP4 experts
  * with dim and inter in {2048, 4096}, topk 6 or 8, in two launches:
