@@ -811,22 +811,30 @@ __global__ __launch_bounds__(APUS_PRE_THREADS, 2) void apus_gemm_prefill_kernel(
  * Tile schedule (dense GEMMs with more than 8 rows, e.g. a 512-token FP8
  * projection). A workgroup computes 64 rows (tokens) x 128 columns (weight
  * rows) over the whole K, one accumulation chain per output in 128-group
- * order. Four waves in a 2 x 2 arrangement own 32 tokens x 64 weight rows
- * each (2 x 4 MFMA tiles, 8 instructions per 128-group). The 64 activation
+ * order. Four waves own TM x TN MFMA tiles each (8 instructions per
+ * 128-group): in a 1 x 4 arrangement (TM = 4, the default) every wave takes
+ * all 64 tokens x 32 weight rows, so each weight fragment is loaded by one
+ * wave only; in 2 x 2 (TM = 2) 32 tokens x 64 weight rows, and the two
+ * waves of a column load the same fragments (measured on gfx950 at M = 512,
+ * K = N = 4096: 21.9 against 22.7 us). The 64 activation
  * rows of each group are staged in LDS (double buffered, loaded DA groups
  * ahead through a register ring); each wave streams its weight fragments straight into a register
  * ring PD groups ahead. The activation loads of a step are issued before
  * that step's weight loads, so waiting for them never waits for the ring.
  * K = 128 * NQ is a template constant (the group loop is straight-line).
  */
-template <int WF>
+template <int WF, int TN>
 struct ApusTileB {
-    apus_v4u w[4][WF == APUS_W_FP4 ? 1 : 2];
-    unsigned s[4];           /* FP4: the row's 4 group-scale bytes of this step */
+    apus_v4u w[TN][WF == APUS_W_FP4 ? 1 : 2];
+    unsigned s[TN];          /* FP4: the row's 4 group-scale bytes of this step */
 };
 
-template <int WF, int NQ, int PD, int DA>
+/* TM: 16-token fragments per wave (2: waves in 2 x 2, 4: waves in 1 x 4);
+ * each wave then owns TN = 8 / TM 16-row weight tiles */
+template <int WF, int NQ, int PD, int DA, int TM>
 __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) {
+    constexpr int WMW = TM == 4 ? 1 : 2;       /* waves along tokens */
+    constexpr int TN = TM == 4 ? 2 : 4;        /* weight tiles per wave */
     constexpr int BM = 64, BN = 128, LDA = 128 + 16;
     constexpr int K = NQ * 128;
     constexpr size_t RB = WF == APUS_W_FP4 ? K / 2 : K;     /* weight row bytes */
@@ -837,8 +845,8 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
     if (m0 >= ent.M) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int nbase = blockIdx.x * BN + wn * 64;
+    const int wm = WMW == 1 ? 0 : wave >> 1, wn = WMW == 1 ? wave : wave & 1;
+    const int nbase = blockIdx.x * BN + wn * (16 * TN);
     /* activation staging: thread t loads bytes [(t%4)*32, +32) of token row t/4 */
     const int srow = threadIdx.x >> 2, spart = threadIdx.x & 3;
     const int sm = m0 + srow;
@@ -859,9 +867,9 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
 #pragma unroll
         for (int i = 0; i < NQ / 4; ++i) sb8[i] = apus_gld<unsigned>(wsrow + 4 * i);
     }
-    auto load_b = [&](ApusTileB<WF> &f, int q) {
+    auto load_b = [&](ApusTileB<WF, TN> &f, int q) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TN; ++i) {
             const uint8_t *p = wl.w + i * tstride + (size_t)q * wl.qs;
             if constexpr (WF == APUS_W_FP4) {
                 f.w[i][0] = apus_gld<apus_v4u>(p);
@@ -886,7 +894,7 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
         if (spart == 0) lsa[q & 1][srow] = (uint8_t)apus_e8m0_of(sreg[slot]);
     };
 
-    ApusTileB<WF> ring[PD];
+    ApusTileB<WF, TN> ring[PD];
 #pragma unroll
     for (int u = 0; u < DA; ++u)
         if (u < NQ) load_a(u, u);
@@ -895,20 +903,20 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
     store_a(0, 0);
     apus_lds_barrier();
 
-    apus_v4f acc[2][4];
+    apus_v4f acc[TM][TN];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TM; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < TN; ++i) acc[t][i] = apus_v4f{0.f, 0.f, 0.f, 0.f};
 
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
         /* activation rows of step q + DA (slot of step q, written last step) */
         if (q + DA < NQ) load_a(q + DA, q % DA);
-        ApusTileB<WF> &cur = ring[q % PD];
+        ApusTileB<WF, TN> &cur = ring[q % PD];
         const uint8_t *ab = la[q & 1];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < TM; ++t) {
             const int row = wm * 32 + t * 16 + r;
             const uint4 a0 = *reinterpret_cast<const uint4 *>(ab + row * LDA + g * 16);
             const uint4 a1 = *reinterpret_cast<const uint4 *>(ab + row * LDA + 64 + g * 16);
@@ -916,7 +924,7 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
                                         (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
             const int sa = lsa[q & 1][row];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < TN; ++i) {
                 if constexpr (WF == APUS_W_FP4) {
                     const apus_v4u w = cur.w[i][0];
                     const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
@@ -937,7 +945,7 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
     }
     /* lane holds D[4g + j][r]: token m0 + 32 wm + 16 t + 4g + j, weight row nbase + 16 i + r */
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < TM; ++t) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int mm = m0 + wm * 32 + t * 16 + 4 * g + j;
@@ -945,7 +953,7 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
                 const int orow = ent.orows ? apus_gld<int>(ent.orows + mm) : ent.o0 + mm;
                 float *dst = ent.out + (size_t)orow * args.ldo + nbase + r;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < TN; ++i) {
                     float v = acc[t][i][j];
                     if (args.round_out) v = apus_bf16_rne(v);
                     apus_gst<float>(dst + i * 16, v);
@@ -1507,7 +1515,16 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
     /* dense GEMMs with more than 8 rows: the tile schedule */
     if (!grouped && a->ent0.M > R && apus_fast_k(a->K) && a->O % 128 == 0) {
         dim3 gt(a->O / 128, (a->ent0.M + 63) / 64, 1), bt(256);
-#define APUS_TILE(NQ, PD) hipLaunchKernelGGL((apus_gemm_tile_kernel<WFC, NQ, PD, 6>), gt, bt, 0, st, *a)
+#ifndef APUS_TILE_TM
+#define APUS_TILE_TM 4
+#endif
+#ifndef APUS_TILE_DA
+#define APUS_TILE_DA 6
+#endif
+#ifndef APUS_TILE_PDX
+#define APUS_TILE_PDX 1
+#endif
+#define APUS_TILE(NQ, PD) hipLaunchKernelGGL((apus_gemm_tile_kernel<WFC, NQ, (PD * APUS_TILE_PDX < NQ ? PD * APUS_TILE_PDX : NQ), APUS_TILE_DA, APUS_TILE_TM>), gt, bt, 0, st, *a)
         if (wfmt == APUS_W_FP4) {
             constexpr int WFC = APUS_W_FP4;
             switch (a->K) {
