@@ -512,6 +512,42 @@ def bench_store_load(H, experts=64, dim=4096, inter=2048, threads=8):
         shutil.rmtree(d, ignore_errors=True)
 
 
+_HOST_KEEP = []
+
+
+def bench_hostptr(H, O=2048, K=4096, calls=400):
+    """Config 0 through the host-pointer hook (apus_hip_fp4_linear, the
+    c/attn.h:432 call site): weights in host memory (uploaded once into the
+    backend's dense cache, keyed by pointer), x and out in host memory, so
+    every call pays the x upload, the out download and a stream sync. This
+    is the PCIe-inclusive rate of the boundary, reported beside `value`."""
+    import ctypes as C
+    rng = np.random.default_rng(0)
+    w = rng.integers(0, 256, (O, K // 2), dtype=np.uint8)
+    ws = rng.integers(118, 131, (O, K // 32), dtype=np.uint8)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    out = np.empty((1, O), np.float32)
+    W = H.fp4_weight(w, ws)
+    # the backend keys cached weights by host pointer: keep the arrays alive
+    # for the whole process so no later allocation reuses their addresses
+    _HOST_KEEP.extend([w, ws])
+    L = H.lib()
+    xp = x.ctypes.data_as(C.POINTER(C.c_float))
+    op = out.ctypes.data_as(C.POINTER(C.c_float))
+
+    def call():
+        H._check(L.apus_hip_fp4_linear(C.byref(W), xp, op, 1, K, O), "fp4_linear (host)")
+
+    for _ in range(20):
+        call()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        call()
+    us = (time.perf_counter() - t0) / calls * 1e6
+    nbytes = O * K // 2 + O * K // 32 + 4 * K + 4 * O
+    return {"us": us, "GBs": nbytes / us / 1e3}
+
+
 def cpu_baseline(O=2048, K=4096, budget_s=12.0):
     """apus's own apus_fp4_gemm_mt (AVX2 rows + pthread pool) on config 0."""
     threads = min(os.cpu_count() or 1, 16)
@@ -645,6 +681,9 @@ def main():
             extras["config0_linear_GBs"] = round(g["linear_gbs"], 1)
             extras["config0_linear_us"] = round(g["linear_us"], 3)
             extras["config0_eager_launch_GBs"] = round(g["eager_gbs"], 1)
+            hp = bench_hostptr(H)
+            extras["config0_hostptr_linear_us"] = round(hp["us"], 2)
+            extras["config0_hostptr_linear_GBs"] = round(hp["GBs"], 1)
     if not args.skip_extras and want("fp8"):
         log("[bench] config 1 FP8 GEMV/GEMM")
         f8 = bench_fp8(H, dev, min(args.steps, 512))
