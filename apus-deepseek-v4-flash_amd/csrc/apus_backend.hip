@@ -90,6 +90,15 @@ struct State {
     std::unordered_map<const void *, DenseW> dense;
     std::unordered_map<uint64_t, ExpertW> experts;
     DevBuf scratch[8];
+    /* pinned staging of the host-pointer calls' small transfers (x, out,
+     * ids, ...): filled from offset 0 after every finish(), so a region is
+     * never rewritten before the copy that reads it has run; downloads land
+     * here and are copied to the caller's buffers after the sync */
+    uint8_t *pin = nullptr;
+    size_t pin_used = 0;
+    bool pin_failed = false;
+    std::vector<std::pair<void *, size_t>> pin_out;   /* (caller dst, bytes) per staged download */
+    std::vector<size_t> pin_out_off;
     uint64_t bytes_uploaded = 0, bytes_resident = 0, dispatches = 0;
     size_t dense_budget = 0;
     ApusHipHooks hooks{};
@@ -117,8 +126,13 @@ bool alloc_pair_tickets(int lane) {
     return true;
 }
 
+void pin_reset();
+
 bool ensure_init() {
-    if (g.inited) return true;
+    if (g.inited) {
+        pin_reset();
+        return true;
+    }
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
         set_err("no HIP device visible");
@@ -168,15 +182,71 @@ unsigned *pair_tickets(hipStream_t st) {
     return g.pair_tk[0];
 }
 
+constexpr size_t PIN_CAP = (size_t)8 << 20;     /* pinned staging bytes */
+constexpr size_t PIN_SMALL = (size_t)1 << 20;   /* transfers up to this size are staged */
+
+/* a 256-aligned region of the pinned staging buffer, or null (then the
+ * transfer goes straight from or to pageable memory) */
+uint8_t *pin_take(size_t n) {
+    if (n > PIN_SMALL || g.pin_failed) return nullptr;
+    if (!g.pin) {
+        if (hipHostMalloc((void **)&g.pin, PIN_CAP, hipHostMallocDefault) != hipSuccess) {
+            (void)hipGetLastError();
+            g.pin = nullptr;
+            g.pin_failed = true;
+            return nullptr;
+        }
+    }
+    const size_t off = (g.pin_used + 255) & ~(size_t)255;
+    if (off + n > PIN_CAP) return nullptr;
+    g.pin_used = off + n;
+    return g.pin + off;
+}
+
 bool upload(void *dst, const void *src, size_t n) {
+    if (uint8_t *p = pin_take(n)) {
+        memcpy(p, src, n);
+        return ok(hipMemcpyAsync(dst, p, n, hipMemcpyHostToDevice, g.stream), "H2D");
+    }
     return ok(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g.stream), "H2D");
 }
 
 bool download(void *dst, const void *src, size_t n) {
+    if (uint8_t *p = pin_take(n)) {
+        g.pin_out.emplace_back(dst, n);
+        g.pin_out_off.push_back((size_t)(p - g.pin));
+        return ok(hipMemcpyAsync(p, src, n, hipMemcpyDeviceToHost, g.stream), "D2H");
+    }
     return ok(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g.stream), "D2H");
 }
 
-bool finish() { return ok(hipStreamSynchronize(g.stream), "hipStreamSynchronize"); }
+/* at the start of a call: staging left over by a call that failed before
+ * its finish() is dropped once the stream has drained (its downloads never
+ * reach the caller that gave up on them). Skipped while the stream is being
+ * captured (no host call is in flight then). */
+void pin_reset() {
+    if (g.pin_used == 0 && g.pin_out.empty()) return;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g.stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+    (void)hipStreamSynchronize(g.stream);
+    g.pin_out.clear();
+    g.pin_out_off.clear();
+    g.pin_used = 0;
+}
+
+/* wait for the stream, then hand staged downloads to their callers' buffers
+ * and release the staging buffer */
+bool finish() {
+    const bool r = ok(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    if (r) {
+        for (size_t i = 0; i < g.pin_out.size(); ++i)
+            memcpy(g.pin_out[i].first, g.pin + g.pin_out_off[i], g.pin_out[i].second);
+    }
+    g.pin_out.clear();
+    g.pin_out_off.clear();
+    g.pin_used = 0;
+    return r;
+}
 
 bool launched(hipError_t e, const char *what) {
     g.dispatches++;
@@ -643,6 +713,11 @@ void apus_hip_disable(void) {
     for (auto &kv : g.experts) hipFree(kv.second.p[0]);
     g.experts.clear();
     for (auto &b : g.scratch) { if (b.p) hipFree(b.p); b.p = nullptr; b.n = 0; }
+    if (g.pin) (void)hipHostFree(g.pin);
+    g.pin = nullptr;
+    g.pin_used = 0;
+    g.pin_out.clear();
+    g.pin_out_off.clear();
     g.bytes_resident = 0;
     g.hooks = ApusHipHooks{};
     g.enabled = false;
