@@ -95,6 +95,7 @@ struct State {
      * never rewritten before the copy that reads it has run; downloads land
      * here and are copied to the caller's buffers after the sync */
     uint8_t *pin = nullptr;
+    uint8_t *pin_dev = nullptr;   /* the buffer's device address (kernels write results there) */
     size_t pin_used = 0;
     bool pin_failed = false;
     std::vector<std::pair<void *, size_t>> pin_out;   /* (caller dst, bytes) per staged download */
@@ -201,6 +202,28 @@ uint8_t *pin_take(size_t n) {
     if (off + n > PIN_CAP) return nullptr;
     g.pin_used = off + n;
     return g.pin + off;
+}
+
+/* a device-visible region of the staging buffer for a call's result: the
+ * last kernel writes it there (no download copy) and it reaches dst at
+ * finish(); null when staging is not available (then download as usual) */
+void *out_direct(void *dst, size_t n) {
+    if (!dst || n > PIN_SMALL || g.pin_failed) return nullptr;
+    const size_t used0 = g.pin_used;
+    uint8_t *p = pin_take(n);
+    if (!p) return nullptr;
+    if (!g.pin_dev) {
+        void *d = nullptr;
+        if (hipHostGetDevicePointer(&d, g.pin, 0) != hipSuccess || !d) {
+            (void)hipGetLastError();
+            g.pin_used = used0;
+            return nullptr;
+        }
+        g.pin_dev = (uint8_t *)d;
+    }
+    g.pin_out.emplace_back(dst, n);
+    g.pin_out_off.push_back((size_t)(p - g.pin));
+    return g.pin_dev + (p - g.pin);
 }
 
 bool upload(void *dst, const void *src, size_t n) {
@@ -384,7 +407,9 @@ int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
     float *dx = (float *)scratch(0, (size_t)M * K * 4);
     uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
     float *dsc = (float *)scratch(2, (size_t)M * nab * 4);
-    float *dout = (float *)scratch(3, (size_t)M * O * 4);
+    float *dout = (float *)out_direct(out, (size_t)M * O * 4);
+    const bool direct = dout != nullptr;
+    if (!direct) dout = (float *)scratch(3, (size_t)M * O * 4);
     if (!dx || !dc || !dsc || !dout) return 1;
     if (!upload(dx, x, (size_t)M * K * 4)) return 1;
     const int f = linear_fused(wf, d->w, d->ws, dx, dout, M, K, O, g.stream);
@@ -393,7 +418,7 @@ int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
         if (!launched(apus_launch_act_quant(dx, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
         if (gemm_dev(wf, d->w, d->ws, dc, dsc, dout, M, O, K, 1, g.stream)) return 1;
     }
-    if (!download(out, dout, (size_t)M * O * 4) || !finish()) return 1;
+    if ((!direct && !download(out, dout, (size_t)M * O * 4)) || !finish()) return 1;
     return 0;
 }
 
@@ -715,6 +740,7 @@ void apus_hip_disable(void) {
     for (auto &b : g.scratch) { if (b.p) hipFree(b.p); b.p = nullptr; b.n = 0; }
     if (g.pin) (void)hipHostFree(g.pin);
     g.pin = nullptr;
+    g.pin_dev = nullptr;
     g.pin_used = 0;
     g.pin_out.clear();
     g.pin_out_off.clear();
@@ -780,12 +806,14 @@ static int wlinear_host(const void *w, bool bf16, const float *x, float *out, in
                                    wbytes, 0, O, K);
     if (!d) return 1;
     float *dx = (float *)scratch(0, (size_t)M * K * 4);
-    float *dout = (float *)scratch(3, (size_t)M * O * 4);
+    float *dout = (float *)out_direct(out, (size_t)M * O * 4);
+    const bool direct = dout != nullptr;
+    if (!direct) dout = (float *)scratch(3, (size_t)M * O * 4);
     if (!dx || !dout || !upload(dx, x, (size_t)M * K * 4)) return 1;
     if (!launched(apus_launch_wgemv(d->w, dx, dout, M, K, O, (flags & 3) | (bf16 ? 4 : 0), g.stream),
                   "wgemv"))
         return 1;
-    return download(out, dout, (size_t)M * O * 4) && finish() ? 0 : 1;
+    return (direct || download(out, dout, (size_t)M * O * 4)) && finish() ? 0 : 1;
 }
 
 int apus_hip_f32_linear(const float *w, const float *x, float *out, int M, int K, int O,
@@ -937,7 +965,9 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
     float *dx = (float *)scratch(0, (size_t)s * dim * 4);
     int32_t *didx = (int32_t *)scratch(1, (size_t)nj * 4 + (size_t)nj * 4);
     float *dwgt = (float *)((uint8_t *)didx + (size_t)nj * 4);
-    float *dy = (float *)scratch(3, (size_t)s * dim * 4);
+    float *dy = (float *)out_direct(y, (size_t)s * dim * 4);
+    const bool direct = dy != nullptr;
+    if (!direct) dy = (float *)scratch(3, (size_t)s * dim * 4);
     if (!ws || !dx || !didx || !dy) return 1;
     MoeWs mw = moe_carve(ws, s, topk, E, dim, inter);
     if (!upload(mw.tab, tab.data(), tab.size() * sizeof(void *)) ||
@@ -948,7 +978,7 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
     if (moe_pipeline(E, dim, inter, w->limit, mw.tab, dx, didx, dwgt, s, topk, dy, mw, etiled,
                      nullptr, g.stream))
         return 1;
-    if (!download(y, dy, (size_t)s * dim * 4) || !finish()) return 1;
+    if ((!direct && !download(y, dy, (size_t)s * dim * 4)) || !finish()) return 1;
     return 0;
 }
 
