@@ -811,12 +811,12 @@ __global__ __launch_bounds__(APUS_PRE_THREADS, 2) void apus_gemm_prefill_kernel(
  * Tile schedule (dense GEMMs with more than 8 rows, e.g. a 512-token FP8
  * projection). A workgroup computes 64 rows (tokens) x 128 columns (weight
  * rows) over the whole K, one accumulation chain per output in 128-group
- * order. Four waves own TM x TN MFMA tiles each (8 instructions per
- * 128-group): in a 1 x 4 arrangement (TM = 4, the default) every wave takes
- * all 64 tokens x 32 weight rows, so each weight fragment is loaded by one
- * wave only; in 2 x 2 (TM = 2) 32 tokens x 64 weight rows, and the two
- * waves of a column load the same fragments (measured on gfx950 at M = 512,
- * K = N = 4096: 21.9 against 22.7 us). The 64 activation
+ * order. NW waves own TM x TN MFMA tiles each, all 64 tokens per wave (each
+ * weight fragment loaded by one wave only): 4 waves of 64 x 32 weight rows
+ * for K >= 4096, 8 waves of 64 x 16 for K <= 2048. Measured on gfx950: M =
+ * 512, K = N = 4096: 4 waves of 32 tokens x 64 rows 22.7 us, of 64 x 32
+ * 22.0 us, 8 waves of 64 x 16 22.5 us; K = 2048 (64 tokens): 4 waves 28.1
+ * us, 8 waves 24.3 us. The 64 activation
  * rows of each group are staged in LDS (double buffered, loaded DA groups
  * ahead through a register ring); each wave streams its weight fragments straight into a register
  * ring PD groups ahead. The activation loads of a step are issued before
@@ -829,12 +829,16 @@ struct ApusTileB {
     unsigned s[TN];          /* FP4: the row's 4 group-scale bytes of this step */
 };
 
-/* TM: 16-token fragments per wave (2: waves in 2 x 2, 4: waves in 1 x 4);
- * each wave then owns TN = 8 / TM 16-row weight tiles */
-template <int WF, int NQ, int PD, int DA, int TM>
-__global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) {
-    constexpr int WMW = TM == 4 ? 1 : 2;       /* waves along tokens */
-    constexpr int TN = TM == 4 ? 2 : 4;        /* weight tiles per wave */
+/* NW waves; TM: 16-token fragments per wave, so 4 / TM waves along the
+ * tokens and NW * TM / 4 along the weight rows, each owning TN 16-row tiles */
+template <int WF, int NQ, int PD, int DA, int TM, int NW>
+__global__ __launch_bounds__(64 * NW) void apus_gemm_tile_kernel(ApusGemmArgs args) {
+    constexpr int WMW = 4 / TM;                /* waves along tokens */
+    constexpr int WNW = NW / WMW;              /* waves along weight rows */
+    constexpr int TN = 8 / WNW;                /* weight tiles per wave */
+    constexpr int SP = NW;                     /* staging threads per token row */
+    constexpr int SB = 128 / SP;               /* staged bytes per thread per group */
+    static_assert(WMW * TM == 4 && WNW * TN == 8 && SB % 16 == 0, "tile shape");
     constexpr int BM = 64, BN = 128, LDA = 128 + 16;
     constexpr int K = NQ * 128;
     constexpr size_t RB = WF == APUS_W_FP4 ? K / 2 : K;     /* weight row bytes */
@@ -845,14 +849,14 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
     if (m0 >= ent.M) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int wm = WMW == 1 ? 0 : wave >> 1, wn = WMW == 1 ? wave : wave & 1;
+    const int wm = wave / WNW, wn = wave % WNW;
     const int nbase = blockIdx.x * BN + wn * (16 * TN);
-    /* activation staging: thread t loads bytes [(t%4)*32, +32) of token row t/4 */
-    const int srow = threadIdx.x >> 2, spart = threadIdx.x & 3;
+    /* activation staging: thread t loads bytes [(t%SP)*SB, +SB) of token row t/SP */
+    const int srow = threadIdx.x / SP, spart = threadIdx.x % SP;
     const int sm = m0 + srow;
     const int sar = sm < ent.M ? (ent.arows ? apus_gld<int>(ent.arows + sm) : ent.a0 + sm)
                                : (ent.arows ? apus_gld<int>(ent.arows) : ent.a0);
-    const uint8_t *sap = args.acodes + (size_t)sar * K + spart * 32;
+    const uint8_t *sap = args.acodes + (size_t)sar * K + spart * SB;
     const float *ssp = args.ascale + (size_t)sar * NQ;
     /* lane stream of the first of the wave's four 16-row tiles; the others
      * follow at tstride (weights) and sstride (FP4 scales) */
@@ -880,17 +884,17 @@ __global__ __launch_bounds__(256) void apus_gemm_tile_kernel(ApusGemmArgs args) 
             }
         }
     };
-    uint4 areg[DA][2];        /* activation ring: DA groups ahead */
+    uint4 areg[DA][SB / 16];  /* activation ring: DA groups ahead */
     float sreg[DA];
     auto load_a = [&](int q, int slot) {
-        areg[slot][0] = apus_ld16(sap + q * 128);
-        areg[slot][1] = apus_ld16(sap + q * 128 + 16);
+#pragma unroll
+        for (int i = 0; i < SB / 16; ++i) areg[slot][i] = apus_ld16(sap + q * 128 + 16 * i);
         sreg[slot] = apus_gld<float>(ssp + q);    /* unconditional: no branch around a load */
     };
     auto store_a = [&](int q, int slot) {
-        uint8_t *d = la[q & 1] + srow * LDA + spart * 32;
-        *reinterpret_cast<uint4 *>(d) = areg[slot][0];
-        *reinterpret_cast<uint4 *>(d + 16) = areg[slot][1];
+        uint8_t *d = la[q & 1] + srow * LDA + spart * SB;
+#pragma unroll
+        for (int i = 0; i < SB / 16; ++i) *reinterpret_cast<uint4 *>(d + 16 * i) = areg[slot][i];
         if (spart == 0) lsa[q & 1][srow] = (uint8_t)apus_e8m0_of(sreg[slot]);
     };
 
@@ -1514,7 +1518,9 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
     }
     /* dense GEMMs with more than 8 rows: the tile schedule */
     if (!grouped && a->ent0.M > R && apus_fast_k(a->K) && a->O % 128 == 0) {
-        dim3 gt(a->O / 128, (a->ent0.M + 63) / 64, 1), bt(256);
+        /* waves per workgroup: 8 for K <= 2048, 4 above (measured best) */
+#define APUS_TILE_NW(NQ) ((NQ) <= 16 ? 8 : 4)
+        dim3 gt(a->O / 128, (a->ent0.M + 63) / 64, 1), bt(64 * APUS_TILE_NW(a->K / 128));
 #ifndef APUS_TILE_TM
 #define APUS_TILE_TM 4
 #endif
@@ -1524,7 +1530,8 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
 #ifndef APUS_TILE_PDX
 #define APUS_TILE_PDX 1
 #endif
-#define APUS_TILE(NQ, PD) hipLaunchKernelGGL((apus_gemm_tile_kernel<WFC, NQ, (PD * APUS_TILE_PDX < NQ ? PD * APUS_TILE_PDX : NQ), APUS_TILE_DA, APUS_TILE_TM>), gt, bt, 0, st, *a)
+
+#define APUS_TILE(NQ, PD) hipLaunchKernelGGL((apus_gemm_tile_kernel<WFC, NQ, (PD * APUS_TILE_PDX < NQ ? PD * APUS_TILE_PDX : NQ), APUS_TILE_DA, APUS_TILE_TM, APUS_TILE_NW(NQ)>), gt, bt, 0, st, *a)
         if (wfmt == APUS_W_FP4) {
             constexpr int WFC = APUS_W_FP4;
             switch (a->K) {
