@@ -18,6 +18,14 @@
  * In all of them, every output is one accumulation chain over its 128-groups
  * in a fixed order, so results do not depend on M, on the position of a row
  * within its entry, or on timing.
+ *
+ * Build-time tuning constants (defaults are the measured best on gfx950;
+ * -D overrides exist for measurements only): APUS_DEC_WAVES (decode
+ * workgroup waves, 4), APUS_DEC_PD_FP4 (decode FP4 weight ring slices, 3),
+ * APUS_PRE_WAVES (prefill workgroup waves, 8), APUS_PRE_PD4 (prefill FP4
+ * ring slices, 2), APUS_PREFILL_ROWS (rows per many-row work item, 64),
+ * APUS_TILE_TM (tile schedule token fragments per wave, 4), APUS_TILE_DA
+ * (activation ring groups, 6), APUS_TILE_PDX (weight ring multiplier, 1).
  */
 #include "apus_device.h"
 #include "apus_internal.h"
