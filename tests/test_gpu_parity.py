@@ -169,3 +169,19 @@ def test_dense_cache_same_bytes_other_shape(hip, oracle, rng):
     x2 = acts(rng, 3, 2048)
     got2 = hip.fp4_linear(w2, ws2, x2)
     assert max_rel(got2, oracle.fp4_linear(w2, ws2, x2)) <= 1e-3 + 2.0 ** -8
+
+
+def test_linear_host_staging_sizes(hip, oracle, rng):
+    """Host-pointer calls alternate between transfers that go through the
+    library's pinned staging buffer (up to 1 MB each) and larger ones that go
+    straight to and from the caller's memory (x of 80 x 4096 fp32 = 1.3 MB,
+    out of 80 x 4096 fp32), each result checked against the oracle, so a
+    result staged for one call can never land in another call's buffer."""
+    K = 4096
+    w, ws = fp4_weights(rng, 4096, K)
+    for M in (1, 80, 3, 80, 1):
+        x = acts(rng, M, K)
+        want = oracle.fp4_linear(w, ws, x)
+        c, s = oracle.act_quant(x)
+        got = hip.fp4_linear(w, ws, x)
+        _check_linear(got, want, oracle.fp4_gemm(w, ws, c, s), f"fp4 linear staging M={M}")
