@@ -115,6 +115,7 @@ SIGNATURES = {
     "apus_hip_act_quant": (C.c_int, [f32p, C.c_int, C.c_int, u8p, f32p]),
     "apus_hip_fp4_gemm": (C.c_int, [u8p, u8p, u8p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
     "apus_hip_fp8_gemm": (C.c_int, [u8p, u8p, u8p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
+    "apus_hip_swiglu_dev": (C.c_int, [vp, vp, C.c_size_t, C.c_float, vp]),
     "apus_hip_act_quant_dev": (C.c_int, [vp, C.c_int, C.c_int, vp, vp]),
     "apus_hip_fp4_gemm_dev": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int]),
     "apus_hip_fp8_gemm_dev": (C.c_int, [vp, vp, vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int]),
@@ -137,6 +138,7 @@ SIGNATURES = {
     "apus_hip_moe_workspace": (C.c_size_t, [vp, C.c_int, C.c_int]),
     "apus_hip_moe_routed_dev": (C.c_int, [vp, C.c_int, vp, vp, vp, C.c_int, C.c_int, C.c_float,
                                           vp, vp]),
+    "apus_hip_moe_routed_h": (C.c_int, [vp, C.c_int, C.c_int, vp, vp, vp]),
     "apus_hip_moe_forward_workspace": (C.c_size_t, [vp, C.c_int, C.c_int]),
     "apus_hip_moe_forward_dev": (C.c_int, [vp, C.c_int, C.POINTER(ApusHipMoeLayer), vp, vp,
                                            C.c_int, C.c_int, vp, C.POINTER(ApusHipMoeInterm),
@@ -156,6 +158,7 @@ SIGNATURES = {
     "apus_hip_fill_random": (C.c_int, [vp, C.c_size_t, C.c_uint64, C.c_uint64, C.c_int]),
     "apus_hip_synchronize": (C.c_int, []),
     "apus_hip_timer_start": (C.c_int, []),
+    "apus_hip_stream_delay": (C.c_int, [C.c_int]),
     "apus_hip_timer_stop": (C.c_float, []),
     "apus_hip_lanes": (C.c_int, [C.c_int]),
     "apus_hip_lane": (C.c_int, [C.c_int]),

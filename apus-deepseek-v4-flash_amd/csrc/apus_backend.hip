@@ -320,6 +320,62 @@ bool upload_weights(int wfmt, uint8_t *dw, uint8_t *dws, const void *w, const vo
     return finish();
 }
 
+/* ---- input domain of the host-pointer entry points. The matrix cores
+ * read E8M0 byte 255 and E4M3 codes 0x7F / 0xFF as NaN, where the reference
+ * decodes +inf and +-480 (c/fp4.h:209-217, :255-260); a non-finite
+ * activation makes the reference's group scale +inf (c/fp4.h:300-317). Such
+ * inputs are refused (nonzero: the caller runs its CPU kernel, which gives
+ * the reference's result); the *_dev entry points document them as outside
+ * their contract instead (a row with a non-finite activation comes out NaN). */
+bool x_finite(const float *x, size_t n, const char *what) {
+    const uint32_t *u = (const uint32_t *)x;
+    for (size_t i = 0; i < n; i++)
+        if ((u[i] & 0x7f800000u) == 0x7f800000u) {
+            set_err("%s: non-finite activation at element %zu (outside the GPU contract; "
+                    "the CPU kernel handles it)", what, i);
+            return false;
+        }
+    return true;
+}
+
+bool e8m0_ok(const uint8_t *s, size_t n, const char *what) {
+    if (n && memchr(s, 0xff, n)) {
+        set_err("%s: E8M0 scale byte 255 (+inf in the reference, NaN on the matrix cores)", what);
+        return false;
+    }
+    return true;
+}
+
+bool e4m3_ok(const uint8_t *c, size_t n, const char *what) {
+    for (size_t i = 0; i < n; i++)
+        if ((c[i] & 0x7f) == 0x7f) {
+            set_err("%s: E4M3 code %#x at %zu (+-480 in the reference, NaN on the matrix cores)",
+                    what, c[i], i);
+            return false;
+        }
+    return true;
+}
+
+/* activation scales of pre-quantised rows: finite powers of two */
+bool pow2_ok(const float *s, size_t n, const char *what) {
+    const uint32_t *u = (const uint32_t *)s;
+    for (size_t i = 0; i < n; i++) {
+        const uint32_t e = (u[i] >> 23) & 0xffu;
+        if ((u[i] & 0x807fffffu) || e == 0 || e == 0xffu) {
+            set_err("%s: activation scale %zu is not a positive finite power of two", what, i);
+            return false;
+        }
+    }
+    return true;
+}
+
+/* the stored weight bytes the matrix cores decode as the reference does */
+bool weights_ok(int wfmt, const uint8_t *w, const uint8_t *ws, size_t wbytes, size_t sbytes,
+                const char *what) {
+    if (wfmt == APUS_W_FP8 && !e4m3_ok(w, wbytes, what)) return false;
+    return wfmt > APUS_W_FP8 || e8m0_ok(ws, sbytes, what);
+}
+
 const DenseW *dense_weight(int wfmt, const uint8_t *w, const uint8_t *ws, size_t wbytes,
                            size_t sbytes, int O, int K) {
     const uint64_t fp = fingerprint(w, wbytes) ^ (ws && sbytes ? fingerprint(ws, sbytes) * 31 : 0);
@@ -339,6 +395,7 @@ const DenseW *dense_weight(int wfmt, const uint8_t *w, const uint8_t *ws, size_t
         set_err("dense weight budget exhausted (APUS_HIP_DENSE_MB)");
         return nullptr;
     }
+    if (!weights_ok(wfmt, w, ws, wbytes, sbytes, "weight upload")) return nullptr;
     DenseW d{ws, nullptr, nullptr, wbytes, sbytes, fp, wfmt, O, K, false};
     if (!ok(hipMalloc(&d.w, wbytes), "hipMalloc weight")) return nullptr;
     if (!ok(hipMalloc(&d.ws, sbytes), "hipMalloc scales")) { hipFree(d.w); return nullptr; }
@@ -400,6 +457,7 @@ int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
     const size_t wbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 2 : (size_t)O * K;
     const size_t sbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 32
                                              : (size_t)((O + 127) / 128) * (K / 128);
+    if (!x_finite(x, (size_t)M * K, "linear")) return 1;
     const DenseW *d = dense_weight(wfmt, w, ws, wbytes, sbytes, O, K);
     if (!d) return 1;
     const int wf = wfmt | (d->tiled ? APUS_HIP_W_TILED : 0);
@@ -430,6 +488,9 @@ int gemm_host(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acod
     const size_t sbytes = wfmt == APUS_W_FP4 ? (size_t)O * K / 32
                                              : (size_t)((O + 127) / 128) * (K / 128);
     const size_t nab = K / 128;
+    if (!weights_ok(wfmt, w, ws, wbytes, sbytes, "gemm") || !e4m3_ok(acodes, (size_t)M * K, "gemm") ||
+        !pow2_ok(as, (size_t)M * nab, "gemm"))
+        return 1;
     uint8_t *dw = (uint8_t *)scratch(4, wbytes);
     uint8_t *dws = (uint8_t *)scratch(5, sbytes);
     uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
@@ -616,33 +677,6 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         if (add_out && !wait_add()) return 1;
         return launched(apus_launch_moe_pair2(&b, st), "pair w2") ? 0 : 1;
     }
-    /* few pairs, other topk: one launch entry per routed pair and matrix.
-     * w1/w3 quantise x while staging, w2 computes and quantises h = swiglu(g,
-     * u) while staging and accumulates y in (t, j) order in its last
-     * workgroup per column tile: two launches */
-    if (pair_shape) {
-        ApusGemmArgs a{};
-        a.wtiled = wtiled;
-        a.O = inter; a.K = dim; a.ldo = inter; a.round_out = 1;
-        a.asrc = APUS_A_F32; a.ax = x;
-        a.pidx = idx; a.nmat = 2; a.adiv = topk; a.pE = E;
-        a.pw[0] = t.w1; a.pws[0] = t.w1s; a.pout[0] = w.gm;
-        a.pw[1] = t.w3; a.pws[1] = t.w3s; a.pout[1] = w.um;
-        a.zero = w.tickets; a.nzero = dim / 16;
-        if (!launched(apus_launch_gemm_few(APUS_W_FP4, &a, 2 * nj, 1, 0, st), "pair w1/w3"))
-            return 1;
-        ApusGemmArgs b{};
-        b.wtiled = wtiled;
-        b.O = dim; b.K = inter; b.ldo = dim; b.round_out = 1;
-        b.asrc = APUS_A_SWIGLU; b.ax = w.gm; b.au = w.um; b.limit = limit;
-        b.pidx = idx; b.nmat = 1; b.adiv = 1; b.pE = E;
-        b.pw[0] = t.w2; b.pws[0] = t.w2s; b.pout[0] = w.eo;
-        b.acc_w = wgt; b.acc_y = y; b.tickets = w.tickets; b.acc_topk = topk; b.acc_s = s;
-        if (!launched(apus_launch_gemm_few(APUS_W_FP4, &b, nj, 1, 0, st), "pair w2")) return 1;
-        if (!add_out) return 0;
-        return wait_add() && launched(apus_launch_add_bf16(y, add_src, add_out, (size_t)s * dim, st),
-                                      "add") ? 0 : 1;
-    }
     /* experts with at most SMALL pairs take the few-row GEMM schedule; at
      * most min(E, nj) experts are small and at most nj / (SMALL + 1) are
      * large, so the launches cover only that many table slots */
@@ -666,6 +700,12 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
      * APUS_PREFILL_ROWS-row chunk per launch row, balanced) where the
      * many-row schedule applies */
     const bool use_items = (dim == 2048 || dim == 4096) && (inter == 2048 || inter == 4096);
+    /* at these shapes the grouped GEMMs keep the accumulation orders of the
+     * one-token kernels (w1/w3: one chain over K; w2: four K-quarter chains
+     * added in order), so every token's y is bit-identical to dispatching it
+     * alone, whatever the batch around it (the reference's batched ==
+     * per-token property, tests/m9b/test_m9b.c:1-20) */
+    if (use_items) { a.kchain = 1; b.kchain = 4; }
     for (int pass = 0; pass < 2; ++pass) {
         const int n = pass ? n_large : n_small;
         if (!n) continue;
@@ -694,6 +734,19 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
                                         add_out, st), "moe_accum"))
         return 1;
     return 0;
+}
+
+/* true (with the error set) while a graph capture is open on the backend
+ * stream or the selected lane */
+bool capturing(const char *what) {
+    for (hipStream_t st : {g.stream, dev_stream()}) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+            set_err("%s: not allowed while a graph capture is open", what);
+            return true;
+        }
+    }
+    return false;
 }
 
 }  // namespace
@@ -768,7 +821,7 @@ int apus_hip_fp4_linear(const ApusFp4W *w, const float *x, float *out, int M, in
 
 int apus_hip_act_quant(const float *x, int M, int K, uint8_t *codes, float *scales) {
     std::lock_guard<std::mutex> lk(g_mu);
-    if (!ensure_init() || !shape_ok(M, K, 1)) return 1;
+    if (!ensure_init() || !shape_ok(M, K, 1) || !x_finite(x, (size_t)M * K, "act_quant")) return 1;
     const size_t nab = K / 128;
     float *dx = (float *)scratch(0, (size_t)M * K * 4);
     uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
@@ -857,6 +910,8 @@ int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent, const ui
         outrows += ents[i].M;
     }
     const size_t nab = K / 128;
+    if (!e4m3_ok(acodes, rows * K, "grouped gemm") || !pow2_ok(as, rows * nab, "grouped gemm"))
+        return 1;
     uint8_t *dc = (uint8_t *)scratch(1, rows * K + 1);
     float *dsc = (float *)scratch(2, rows * nab * 4 + 4);
     float *dout = (float *)scratch(3, outrows * O * 4 + 4);
@@ -902,6 +957,7 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
     const int nj = s * topk;
     for (int q = 0; q < nj; q++)
         if (idx[q] < 0 || idx[q] >= E) { set_err("moe_routed: expert id out of range"); return 1; }
+    if (!x_finite(x, (size_t)s * dim, "moe_routed")) return 1;
     /* resident expert slabs keyed by (layer, eid) */
     std::vector<uint8_t *> tab(6 * (size_t)E, nullptr);
     const size_t sz[6] = {(size_t)inter * dim / 2, (size_t)inter * dim / 32,
@@ -930,6 +986,8 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
                 r1 = w->w1[e]; r2 = w->w2[e]; r3 = w->w3[e];
             }
             const void *src[6] = {r1.packed, r1.scales, r2.packed, r2.scales, r3.packed, r3.scales};
+            for (int i = 1; i < 6; i += 2)
+                if (!e8m0_ok((const uint8_t *)src[i], sz[i], "moe_routed expert")) return 1;
             ExpertW ew{};
             size_t tot = 0;
             for (int i = 0; i < 6; i++) tot += align256(sz[i]);
@@ -983,6 +1041,12 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
 }
 
 /* ---------------------------------------------------- device entry points */
+
+int apus_hip_swiglu_dev(const float *g, const float *u, size_t n, float limit, float *h) {
+    if (!ensure_init()) return 1;
+    if (!g || !u || !h) { set_err("swiglu_dev: bad arguments"); return 1; }
+    return launched(apus_launch_swiglu(g, u, n, limit, h, dev_stream()), "swiglu") ? 0 : 1;
+}
 
 int apus_hip_act_quant_dev(const float *x, int M, int K, uint8_t *codes, float *scales) {
     if (!ensure_init() || !shape_ok(M, K, 1)) return 1;
@@ -1183,6 +1247,8 @@ int apus_hip_store_put(ApusHipStore *st, int layer, int eid, const ApusFp4W *w1,
     if (!st || layer < 0 || layer >= st->L || eid < 0 || eid >= st->E) return 1;
     std::lock_guard<std::mutex> lk(g_mu);
     const void *src[6] = {w1->packed, w1->scales, w2->packed, w2->scales, w3->packed, w3->scales};
+    for (int i = 1; i < 6; i += 2)
+        if (!e8m0_ok((const uint8_t *)src[i], st->sz[i], "store_put")) return 1;
     const int mo[3] = {st->inter, st->dim, st->inter}, mk[3] = {st->dim, st->inter, st->dim};
     uint8_t *p[6];
     size_t off = 0;
@@ -1320,6 +1386,16 @@ int apus_hip_store_load(ApusHipStore *st, const ApusHipContainer *c, int io_thre
         if (!d.ok) { rc = 2; failed_idx = d.idx; break; }
         const int layer = (int)(d.idx / c->E), eid = (int)(d.idx % c->E);
         const ApusHipSlabRec &r = c->recs[d.idx];
+        bool scales_ok = true;
+        for (int m = 0; m < 3; m++)
+            scales_ok = scales_ok && !memchr(hbuf[d.buf] + r.rel[2 * m + 1], 0xff, st->sz[2 * m + 1]);
+        if (!scales_ok) {
+            rc = 3;
+            failed_idx = d.idx;
+            std::lock_guard<std::mutex> l(mu);
+            free_bufs.push_back(d.buf);
+            break;
+        }
         uint8_t *dst[6];
         size_t off = 0;
         for (int i = 0; i < 6; i++) {
@@ -1371,6 +1447,9 @@ int apus_hip_store_load(ApusHipStore *st, const ApusHipContainer *c, int io_thre
     if (rc == 2)
         return fail("store_load: read of expert %zu.%zu failed (%s)", failed_idx / c->E,
                     failed_idx % c->E, c->shards[c->recs[failed_idx].shard].c_str());
+    if (rc == 3)
+        return fail("store_load: expert %zu.%zu has an E8M0 scale byte 255 (+inf in the reference, "
+                    "NaN on the matrix cores)", failed_idx / c->E, failed_idx % c->E);
     if (rc) return fail("store_load: %s", g_err);
     return 0;
 }
@@ -1407,6 +1486,23 @@ int apus_hip_moe_routed_dev(const ApusHipStore *st, int layer, const float *x, c
                         topk, y, mw, st->tiled, &slab, dev_stream());
 }
 
+int apus_hip_moe_routed_h(const ApusHipStore *st, int s, int topk, const void *workspace,
+                          uint8_t *codes, uint8_t *e8m0) {
+    if (!ensure_init()) return 1;
+    if (!st || s <= 0 || topk <= 0 || !workspace || !codes || !e8m0) {
+        set_err("moe_routed_h: bad arguments");
+        return 1;
+    }
+    MoeWs mw = moe_carve(const_cast<void *>(workspace), s, topk, st->E, st->dim, st->inter);
+    const int nj = s * topk;
+    /* the one-token kernels leave h by pair with E8M0 bytes; the sorted
+     * pipeline by sorted position with fp32 scales */
+    const bool pair = moe_pair_mode(st->dim, st->inter, s, topk);
+    return launched(apus_launch_moe_h_gather(mw.hc, mw.hs, pair ? 0 : 1, pair ? nullptr : mw.pair, nj,
+                                             st->inter, codes, e8m0, dev_stream()),
+                    "moe_h_gather") ? 0 : 1;
+}
+
 /* --------------------------------------------------------------- helpers */
 
 void *apus_hip_malloc(size_t bytes) {
@@ -1435,6 +1531,10 @@ int apus_hip_d2d(void *dst, const void *src, size_t bytes) {
 
 int apus_hip_memset(void *dst, int value, size_t bytes) {
     if (!ensure_init()) return 1;
+    /* a memset node in a captured graph has given wrong results on replays
+     * after the first on this hardware: refuse it (kernels that need zeroed
+     * memory inside a graph clear it themselves) */
+    if (capturing("apus_hip_memset")) return 1;
     return ok(hipMemsetAsync(dst, value, bytes, g.stream), "hipMemsetAsync") ? 0 : 1;
 }
 
@@ -1452,6 +1552,18 @@ int apus_hip_synchronize(void) {
 int apus_hip_timer_start(void) {
     if (!ensure_init()) return 1;
     return ok(hipEventRecord(g.ev0, g.stream), "hipEventRecord") ? 0 : 1;
+}
+
+int apus_hip_stream_delay(int delay_us) {
+    if (!ensure_init()) return 1;
+    if (delay_us < 0 || delay_us > 1000000) { set_err("stream_delay: 0..1000000 us"); return 1; }
+    if (capturing("apus_hip_stream_delay")) return 1;
+    int khz = 0;
+    if (!ok(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, 0), "hipDeviceGetAttribute"))
+        return 1;
+    if (khz <= 0) khz = 100000;
+    const unsigned long long ticks = (unsigned long long)delay_us * (unsigned long long)khz / 1000ull;
+    return launched(apus_launch_delay(ticks, g.stream), "delay") ? 0 : 1;
 }
 
 float apus_hip_timer_stop(void) {

@@ -447,7 +447,7 @@ __device__ __forceinline__ void apus_stage_quant(const ApusGemmArgs &a, const Ap
     if (sub == 0) lsc[r.row * NQ + r.q] = (uint8_t)e;
 }
 
-template <int WF, int R, int NS, int PD, int KS, int ASRC>
+template <int WF, int R, int NS, int PD, int KS, int ASRC, bool FOLD>
 __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmArgs args) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int last_ticket;
@@ -455,6 +455,10 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
     constexpr int NSW = NS / KS;                       /* slices per wave */
     constexpr int TPW = APUS_DEC_WAVES / KS;           /* row tiles per workgroup */
     static_assert(NS % KS == 0 && PD <= NSW && APUS_DEC_WAVES % KS == 0, "decode shape");
+    /* FOLD: the K-quarter order (four chains from zero over the quarters of
+     * K, added left to right), with whole-K waves */
+    static_assert(!FOLD || (KS == 1 && NS % 4 == 0), "K-quarter fold needs whole-K waves");
+    constexpr int QS = NS / 4;                         /* slices per K quarter */
     if (args.zero && blockIdx.y == 0) {
         for (int i = blockIdx.x * APUS_DEC_NT + threadIdx.x; i < args.nzero; i += gridDim.x * APUS_DEC_NT)
             args.zero[i] = 0u;
@@ -587,6 +591,7 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
         const uint8_t *asrow = lsc + rr * NQ;
         const int z = rvalid ? -1 : 0;
         apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
+        apus_v4f tot = {-0.f, -0.f, -0.f, -0.f};      /* -0 + x == x for every x */
 #pragma unroll
         for (int si = 0; si < NSW; ++si) {
             const int s = sbase + si;
@@ -613,7 +618,14 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
                 }
             }
             if (si + PD < NSW) apus_load_b_full<WF>(cur, wl, s + PD);
+            if constexpr (FOLD) {
+                if ((si + 1) % QS == 0) {
+                    tot += acc;
+                    acc = apus_v4f{0.f, 0.f, 0.f, 0.f};
+                }
+            }
         }
+        if constexpr (FOLD) acc = tot;
         if (KS > 1) {
             /* the K parts of a tile meet in LDS; part 0 adds them in part order */
             lred[wave * 64 + lane] = acc;
@@ -685,9 +697,13 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
 #endif
 #define APUS_PRE_THREADS (64 * APUS_PRE_WAVES)
 
-template <int WF, int NS, int TT, int PD>
+template <int WF, int NS, int TT, int PD, bool FOLD>
 __global__ __launch_bounds__(APUS_PRE_THREADS, 2) void apus_gemm_prefill_kernel(ApusGemmArgs args) {
     constexpr int K = NS * 512, NQ = NS * 4;
+    /* FOLD: the K-quarter order (four chains from zero over the quarters of
+     * K, added left to right) */
+    static_assert(!FOLD || NS % 4 == 0, "K-quarter fold");
+    constexpr int QS = NS / 4;
     constexpr int ROWS = 16 * TT;                 /* activation rows per chunk */
     constexpr int PITCH = 512 + 32;               /* LDS bytes per row per slice (measured best of 8..96 pad) */
     constexpr int CHUNKS = ROWS * 32 / APUS_PRE_THREADS;   /* 16-byte loads per thread per slice */
@@ -743,9 +759,11 @@ __global__ __launch_bounds__(APUS_PRE_THREADS, 2) void apus_gemm_prefill_kernel(
         apus_lds_barrier();           /* previous chunk's readers are done */
         APUS_PRE_FETCH(0);
         APUS_PRE_STORE(0);
-        apus_v4f acc[TT];
+        apus_v4f acc[TT], tot[FOLD ? TT : 1];
 #pragma unroll
         for (int t = 0; t < TT; ++t) acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < (FOLD ? TT : 1); ++t) tot[t] = apus_v4f{-0.f, -0.f, -0.f, -0.f};
         ApusBFrag<WF> ring[PD];
 #pragma unroll
         for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, u);
@@ -793,8 +811,21 @@ __global__ __launch_bounds__(APUS_PRE_THREADS, 2) void apus_gemm_prefill_kernel(
                 }
             }
             if (s + PD < NS) apus_load_b_full<WF>(cur, wl, s + PD);
+            if constexpr (FOLD) {
+                if ((s + 1) % QS == 0) {
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) {
+                        tot[t] += acc[t];
+                        acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+                    }
+                }
+            }
             if (s + 1 < NS) APUS_PRE_STORE((s + 1) & 1);
             apus_lds_barrier();
+        }
+        if constexpr (FOLD) {
+#pragma unroll
+            for (int t = 0; t < TT; ++t) acc[t] = tot[t];
         }
         {
 #pragma unroll
@@ -1366,7 +1397,7 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
 
 namespace {
 
-template <int WF, int R, int NS, int KS, int ASRC>
+template <int WF, int R, int NS, int KS, int ASRC, bool FOLD = false>
 void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
 #ifndef APUS_DEC_PD_FP4
 #define APUS_DEC_PD_FP4 3
@@ -1379,12 +1410,12 @@ void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
     if (lds > 65536) {
         /* eight staged rows of K = 8192 need more than the default 64 KB */
         static const hipError_t attr = hipFuncSetAttribute(
-            reinterpret_cast<const void *>(&apus_gemm_decode_kernel<WF, R, NS, PD, KS, ASRC>),
+            reinterpret_cast<const void *>(&apus_gemm_decode_kernel<WF, R, NS, PD, KS, ASRC, FOLD>),
             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         (void)attr;
     }
     dim3 gd(d.O / (16 * APUS_DEC_WAVES / KS), n_ent), bd(APUS_DEC_NT);
-    hipLaunchKernelGGL((apus_gemm_decode_kernel<WF, R, NS, PD, KS, ASRC>), gd, bd, lds, st, d);
+    hipLaunchKernelGGL((apus_gemm_decode_kernel<WF, R, NS, PD, KS, ASRC, FOLD>), gd, bd, lds, st, d);
 }
 
 /* the K split for K = 512 * NS: KS divides NS; single-row chunks always split
@@ -1396,7 +1427,15 @@ void apus_launch_dec_ns(const ApusGemmArgs &d, int n_ent, int ks, hipStream_t st
         if (ks == 4) { apus_launch_dec<WF, R, NS, 4, ASRC>(d, n_ent, st); return; }
     }
     if constexpr (R != 1) {
-        if (ks == 1) { apus_launch_dec<WF, R, NS, 1, ASRC>(d, n_ent, st); return; }
+        if (ks == 1) {
+            /* the K-quarter order with whole-K waves: MXFP4 expert GEMMs on
+             * pre-quantised rows (the routed w2 in sorted order) */
+            if constexpr (WF == APUS_W_FP4 && ASRC == APUS_A_CODES && NS % 4 == 0) {
+                if (d.kchain == 4) { apus_launch_dec<WF, R, NS, 1, ASRC, true>(d, n_ent, st); return; }
+            }
+            apus_launch_dec<WF, R, NS, 1, ASRC>(d, n_ent, st);
+            return;
+        }
     }
     apus_launch_dec<WF, R, NS, 2, ASRC>(d, n_ent, st);
 }
@@ -1443,6 +1482,19 @@ hipError_t apus_launch_gemm_few(int wfmt, const ApusGemmArgs *a, int n_ent, int 
                                       a->ent1.M != a->ent0.M))))
         return hipErrorInvalidValue;
     if (!ks) ks = apus_dec_ks((size_t)n_ent * (a->O / 16));
+    /* a required accumulation order (kchain) fixes the K split: one chain
+     * needs whole-K waves; the K-quarter order takes whole-K waves (folded
+     * per quarter) or one quarter per wave */
+    if (a->kchain == 1) {
+        if (rows == 1) return hipErrorInvalidValue;   /* single-row chunks always split K */
+        ks = 1;
+    } else if (a->kchain == 4) {
+        if (a->K < 2048) return hipErrorInvalidValue;
+        const bool fold = rows == 8 && a->asrc == APUS_A_CODES && wfmt == APUS_W_FP4;
+        ks = (ks == 1 && fold) ? 1 : 4;
+    } else if (a->kchain != 0) {
+        return hipErrorInvalidValue;
+    }
     const bool fp4 = wfmt == APUS_W_FP4;
     switch (a->asrc) {
     case APUS_A_CODES:
@@ -1516,14 +1568,23 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
 #define APUS_PRE_PD4 2
 #endif
             constexpr int TT4 = APUS_PREFILL_ROWS / 16;
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4>), gp, bp, 0, st, p);
-            else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4>), gp, bp, 0, st, p);
+            if (a->kchain == 4) {
+                if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);
+                else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);
+            } else {
+                if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4, false>), gp, bp, 0, st, p);
+                else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4, false>), gp, bp, 0, st, p);
+            }
         } else {
-            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 8, 2, 2>), gp, bp, 0, st, p);
-            else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 4, 2, 2>), gp, bp, 0, st, p);
+            if (a->kchain == 4) return hipErrorInvalidValue;
+            if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 8, 2, 2, false>), gp, bp, 0, st, p);
+            else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP8, 4, 2, 2, false>), gp, bp, 0, st, p);
         }
         return hipGetLastError();
     }
+    /* a required accumulation order is kept by the decode and prefill
+     * schedules only */
+    if (a->kchain) return hipErrorInvalidValue;
     /* dense GEMMs with more than 8 rows: the tile schedule */
     if (!grouped && a->ent0.M > R && apus_fast_k(a->K) && a->O % 128 == 0) {
         /* waves per workgroup: 8 for K <= 2048, 4 above (measured best) */

@@ -42,6 +42,15 @@ typedef struct {
     int min_m;               /* every entry has M = 0 or M > min_m (0 = unknown) */
     int m_min, m_max;        /* set by the launcher: a kernel computes only the
                               * entries with m_min < M <= m_max (m_max 0: no cap) */
+    int kchain;              /* required accumulation order over K (grouped MXFP4
+                              * launches with K 2048 / 4096 and the few-row
+                              * schedule): 0 = the schedule's own; 1 = one chain
+                              * over the 128-groups in order; 4 = four chains from
+                              * zero over the quarters of K, added left to right.
+                              * The routed MoE uses 1 for w1/w3 and 4 for w2, the
+                              * orders of its one-token kernels, so a token's
+                              * result does not depend on the batch around it. */
+    int pad3;
     /* --- few-row schedule only (apus_launch_gemm_few) --- */
     int asrc;                /* APUS_A_*: where the activation rows come from */
     const float *ax, *au;    /* F32: rows of x [*, K]; SWIGLU: rows of g and u [*, K] */
@@ -225,5 +234,19 @@ hipError_t apus_launch_fill(uint8_t *dst, size_t n, uint64_t seed,
 
 /* elementwise BF16 rounding in place */
 hipError_t apus_launch_bf16_round(float *v, size_t n, hipStream_t st);
+
+/* a one-wave kernel that holds the stream for `ticks` wall-clock ticks */
+hipError_t apus_launch_delay(unsigned long long ticks, hipStream_t st);
+
+/* row r of h codes / scales (fp32 when hs_f32, else E8M0 bytes) to row
+ * pair_of_row[r] (identity when null) of codes / e8m0 */
+hipError_t apus_launch_moe_h_gather(const uint8_t *hc, const void *hs, int hs_f32,
+                                    const int32_t *pair_of_row, int rows, int N, uint8_t *codes,
+                                    uint8_t *e8m0, hipStream_t st);
+
+/* h = bf16(silu(min(g, limit)) * clamp(u, +-limit)) elementwise (no clamp
+ * when limit <= 0) */
+hipError_t apus_launch_swiglu(const float *g, const float *u, size_t n, float limit, float *h,
+                              hipStream_t st);
 
 #endif /* APUS_INTERNAL_H */

@@ -585,3 +585,71 @@ hipError_t apus_launch_bf16_round(float *v, size_t n, hipStream_t st) {
     hipLaunchKernelGGL(apus_bf16_round_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, v, n);
     return hipGetLastError();
 }
+
+/* ------------------------------------------------------------ delay */
+
+/* One wave that sleeps until `ticks` of the constant-rate wall clock have
+ * passed (bounded: at most 2^20 sleep rounds of ~3 us, so it ends even if
+ * the clock were to stand still). Used by the timer to hold the stream
+ * while the host queues the work to be timed. */
+__global__ __launch_bounds__(64) void apus_delay_kernel(unsigned long long ticks) {
+    const unsigned long long t0 = wall_clock64();
+    for (unsigned it = 0; it < (1u << 20); ++it) {
+        if (wall_clock64() - t0 >= ticks) break;
+        __builtin_amdgcn_s_sleep(127);
+    }
+}
+
+hipError_t apus_launch_delay(unsigned long long ticks, hipStream_t st) {
+    hipLaunchKernelGGL(apus_delay_kernel, dim3(1), dim3(64), 0, st, ticks);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------- MoE h read-back */
+
+/* Copies row r of the quantised SwiGLU activations (codes hc [rows, N],
+ * scales hs as fp32 powers of two or E8M0 bytes [rows, N/128]) to row
+ * pair_of_row[r] (identity when null) of codes / e8m0. One workgroup per
+ * row; rows whose pair lies outside [0, rows) are skipped. */
+__global__ __launch_bounds__(256) void apus_moe_h_gather_kernel(
+    const uint8_t *__restrict__ hc, const void *__restrict__ hs, int hs_f32,
+    const int32_t *__restrict__ pair_of_row, int rows, int N, uint8_t *__restrict__ codes,
+    uint8_t *__restrict__ e8m0) {
+    const int r = blockIdx.x;
+    const int p = pair_of_row ? pair_of_row[r] : r;
+    if ((unsigned)p >= (unsigned)rows) return;
+    const int G = N >> 7;
+    for (int i = threadIdx.x; i < N; i += 256) codes[(size_t)p * N + i] = hc[(size_t)r * N + i];
+    for (int i = threadIdx.x; i < G; i += 256)
+        e8m0[(size_t)p * G + i] = hs_f32 ? (uint8_t)apus_e8m0_of(((const float *)hs)[(size_t)r * G + i])
+                                         : ((const uint8_t *)hs)[(size_t)r * G + i];
+}
+
+hipError_t apus_launch_moe_h_gather(const uint8_t *hc, const void *hs, int hs_f32,
+                                    const int32_t *pair_of_row, int rows, int N, uint8_t *codes,
+                                    uint8_t *e8m0, hipStream_t st) {
+    if (rows <= 0) return hipSuccess;
+    if (N % 128) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(apus_moe_h_gather_kernel, dim3(rows), dim3(256), 0, st, hc, hs, hs_f32,
+                       pair_of_row, rows, N, codes, e8m0);
+    return hipGetLastError();
+}
+
+/* ------------------------------------------------------------ SwiGLU */
+
+/* h[i] = bf16(silu(min(g, L)) * clamp(u, +-L)) elementwise (c/moe.h:113-126):
+ * the element function every fused MoE kernel applies, on its own. */
+__global__ __launch_bounds__(256) void apus_swiglu_kernel(const float *__restrict__ g,
+                                                          const float *__restrict__ u, size_t n,
+                                                          float limit, float *__restrict__ h) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) h[i] = apus_swiglu_h(g[i], u[i], limit);
+}
+
+hipError_t apus_launch_swiglu(const float *g, const float *u, size_t n, float limit, float *h,
+                              hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(apus_swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g, u,
+                       n, limit, h);
+    return hipGetLastError();
+}

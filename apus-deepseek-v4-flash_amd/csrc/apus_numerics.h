@@ -64,8 +64,13 @@ APUS_HD uint32_t apus_act_scale_exp(float amax) {
 /* Power of two with biased exponent e (1..254) as fp32. */
 APUS_HD float apus_pow2_from_exp(uint32_t e) { return apus_u2f(e << 23); }
 
-/* Reciprocal of that power of two, 2^(127-e); exact while 1 <= e <= 253. */
-APUS_HD float apus_inv_pow2_from_exp(uint32_t e) { return apus_u2f((254u - e) << 23); }
+/* Reciprocal of that power of two, 2^(127-e); exact while 1 <= e <= 253.
+ * An activation scale exponent is at most 247 for finite input (amax <=
+ * FLT_MAX) and 255 when the group holds an infinity (the reference's scale
+ * is then +inf, c/fp4.h:300-317): 0 is returned for e >= 254, so every
+ * finite element quantises to a signed zero as x / inf does, and the E8M0
+ * byte 255 makes the matrix cores return NaN for the row. */
+APUS_HD float apus_inv_pow2_from_exp(uint32_t e) { return e >= 254u ? 0.0f : apus_u2f((254u - e) << 23); }
 
 /* E8M0 byte of a power-of-two fp32 scale (its biased exponent). */
 APUS_HD uint32_t apus_e8m0_of(float s) { return (apus_f2u(s) >> 23) & 0xffu; }

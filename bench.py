@@ -4,12 +4,14 @@
 Headline (BASELINE.json metric "MXFP4 expert GEMV GB/s (%HBM peak) @M=1; MoE
 grouped-GEMM TFLOP/s @512 tok"):
   value  = config 0: batch-1 MXFP4 expert GEMV, W [2048, 4096] (E2M1 + E8M0 per 32),
-           E4M3 activations quantised per 128 as apus does. One step = one GEMV on
-           its own HBM-resident weight copy (1.1 GB in rotation, so the 256 MB
-           Infinity Cache cannot serve them); 12 steps per grouped launch, as the
-           decode MoE issues the gate+up GEMVs of one token's 6 experts. Launches
-           are captured in one HIP graph on the backend stream and timed with HIP
-           events on that stream. Single-GEMV-per-launch rates are in extras.
+           E4M3 activations quantised per 128 as apus does. One step = one grouped
+           launch of 12 GEMVs (the gate+up GEMVs of one token's 6 routed experts, as
+           the decode MoE issues them), each GEMV on its own HBM-resident weight copy
+           (1.1 GB in rotation, so the 256 MB Infinity Cache cannot serve them).
+           Exactly --steps launches are captured in one HIP graph on the backend
+           stream and timed with HIP events on that stream; the stream is held on
+           the device while the host queues the replay, so the interval is device
+           time only. Single-GEMV-per-launch rates are in extras.
   extras = the other BASELINE configs (FP8 GEMV/GEMM, 64-token decode MoE,
            512-token prefill MoE grouped GEMM with TFLOP/s vs the FP4/FP8 MFMA peaks).
   cpu_baseline = apus's own CPU kernel (apus_fp4_gemm_mt, AVX2 + pthread pool,
@@ -61,14 +63,30 @@ class Dev:
         return b
 
 
-def timed_graph(H, launch, steps):
-    """Capture `steps` launches into one graph, replay once under HIP events."""
+def queue_delay_us(launches):
+    """Device-side hold before the timed work: long enough for the host to
+    queue the warm-up launches and a graph of `launches` kernels (a few us
+    each) before the device reaches them."""
+    return min(200000, 2000 + 40 * launches)
+
+
+def timed_graph(H, launch, steps, warm=0, warm_launch=None):
+    """Capture `steps` launches into one graph and time one replay between
+    two HIP events on the backend stream. The stream is first held on the
+    device (apus_hip_stream_delay) while the host queues `warm` untimed
+    warm-up launches (eager, through warm_launch or launch), the start
+    event and the replay, so the device runs them back to back: the
+    interval holds the timed launches only, with the clocks already up
+    from the warm-up and no host-side submission latency."""
     L = H.lib()
     H._check(L.apus_hip_graph_begin(), "graph_begin")
     for i in range(steps):
         launch(i)
     H._check(L.apus_hip_graph_end(), "graph_end")
     H.synchronize()
+    H._check(L.apus_hip_stream_delay(queue_delay_us(steps + warm)), "stream_delay")
+    for i in range(warm):
+        (warm_launch or launch)(steps + i)
     H._check(L.apus_hip_timer_start(), "timer_start")
     H._check(L.apus_hip_graph_replay(1), "graph_replay")
     ms = L.apus_hip_timer_stop()
@@ -91,18 +109,20 @@ def timed_eager(H, launch, steps):
 
 # ------------------------------------------------------------------ config 0
 
-def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12, extras=True):
-    """Config 0. A step is one M=1 expert GEMV (W [O, K] MXFP4) on its own weight
-    copy (256 copies, 1.1 GB in rotation, so no cache level holds them).
-    Measured three ways:
-      grouped : `group` consecutive steps per launch through the grouped GEMM
-                (the decode MoE issues exactly this: gate+up of one token's 6
-                routed experts = 12 such GEMVs per launch) -> `value`;
-      serial  : one launch per step, serialized on one stream (kernel duration);
-      lanes   : one launch per step, round-robin on 4 concurrent streams.
-    The grouped launch runs on MFMA-tiled weights (the layout the backend keeps
-    resident) for `value`; with extras, also on row-major weights. Without
-    extras only the tiled grouped launch runs (for a profile of that kernel)."""
+def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12, extras=True,
+                   singles=768):
+    """Config 0. A step is one grouped launch of `group` M=1 expert GEMVs
+    (W [O, K] MXFP4), each on its own weight copy (256 copies, 1.1 GB in
+    rotation, so no cache level holds them): the decode MoE issues exactly
+    this launch per token and layer (gate+up of the token's 6 routed experts
+    = 12 GEMVs). `steps` launches are captured in one graph and timed as one
+    replay with HIP events on the backend stream -> `value`.
+    Extras (single GEMVs, `singles` of them):
+      serial  : one launch per GEMV, serialized on one stream;
+      lanes   : one launch per GEMV, round-robin on 4 concurrent streams;
+      eager   : one launch per GEMV without a graph;
+      rowmajor: the grouped launch on row-major weights.
+    `value` uses the MFMA-tiled layout the backend keeps resident."""
     import ctypes as C
     L = H.lib()
     wbytes, sbytes = O * K // 2, O * K // 32
@@ -158,24 +178,27 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12, 
         H._check(L.apus_hip_fp4_linear_dev(w.ptr + c * wbytes, ws.ptr + c * sbytes, dx.ptr,
                                            out.ptr + c * O * 4, 1, K, O, ws_lin.ptr), "linear")
 
-    for i in range(warmup):
-        grouped_tiled(i)
-        if extras:
+    grouped_tiled(0)          # first launch of the kernel (code object set-up), untimed
+    if extras:
+        for i in range(warmup):
             gemv(i)
             grouped(i)
     H.synchronize()
-    launches = max(1, steps // group)
-    ms_tiled = timed_graph(H, grouped_tiled, launches)
+    launches = steps
+    # the warm-up steps run right before the timed replay (same launch,
+    # further weight copies), after the device-side hold
+    ms_tiled = timed_graph(H, grouped_tiled, launches, warm=warmup)
     gemv_bytes = wbytes + sbytes + K + (K // 128) * 4 + O * 4
     gsteps = launches * group
-    res = {"steps_timed": gsteps, "group": group, "launches": launches, "bytes": gemv_bytes,
-           "launch_bytes": gemv_bytes * group, "flops": 2 * O * K,
+    res = {"steps_timed": launches, "gemvs_timed": gsteps, "group": group, "launches": launches,
+           "bytes": gemv_bytes, "launch_bytes": gemv_bytes * group, "flops": 2 * O * K,
            "tiled_gbs": gemv_bytes * gsteps / (ms_tiled * 1e-3) / 1e9,
            "tiled_launch_us": ms_tiled / launches * 1e3,
-           "tiled_ms_per_step": ms_tiled / gsteps}
+           "tiled_ms_per_step": ms_tiled / launches}
     if not extras:
         return res
     ms_group = timed_graph(H, grouped, launches)
+    steps = singles
     ms_serial = timed_graph(H, gemv, steps)
     ms_eager = timed_eager(H, gemv, steps)
     ms_lin = timed_graph(H, linear, steps)
@@ -195,7 +218,7 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12, 
     # act scales + fp32 outputs; the linear reads x in fp32 instead of codes
     lin_bytes = wbytes + sbytes + K * 4 + O * 4
     res.update({
-        "ms_total": ms_group, "ms_per_step": ms_group / gsteps,
+        "ms_total": ms_group,
         "gbs": gemv_bytes * gsteps / (ms_group * 1e-3) / 1e9,
         "launch_us": ms_group / launches * 1e3,
         "serial_us": ms_serial / steps * 1e3,
@@ -645,8 +668,9 @@ def cpu_extras(budget_s=4.0):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048)
-    ap.add_argument("--warmup", type=int, default=64)
+    ap.add_argument("--steps", type=int, default=256,
+                    help="config-0 grouped launches timed (12 GEMVs each)")
+    ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="", help="comma list: gemv,fp8,decode,prefill,full,load")
@@ -774,25 +798,28 @@ def main():
         "dtype": "e4m3 x e2m1 (fp32 accumulate)",
         "data": "synthetic: weights from a counter hash on device (uniform nibbles, E8M0 "
                 "118..130), x ~ N(0,1) seed 0",
-        "config": {"workload": "config 0: MXFP4 expert GEMV O=2048 K=4096 M=1 (one step = one "
-                               "GEMV on its own HBM-resident weight copy, 256 copies in "
-                               f"rotation), {g['group']} steps per grouped launch as the decode "
-                               "MoE issues them (gate+up of one token's 6 routed experts); "
-                               "weights in the MFMA-tiled layout the backend's caches and "
-                               "expert store keep them in",
-                   "group": g["group"], "launches": g["launches"],
+        "config": {"workload": "config 0: MXFP4 expert GEMV O=2048 K=4096 M=1; one step = one "
+                               f"grouped launch of {g['group']} such GEMVs (gate+up of one token's 6 "
+                               "routed experts, as the decode MoE issues them), each on its own "
+                               "HBM-resident weight copy (256 copies, 1.1 GB in rotation); weights "
+                               "in the MFMA-tiled layout the backend's caches and expert store keep",
+                   "group": g["group"], "gemvs_timed": g["gemvs_timed"],
                    "hbm_frac": round(g["tiled_gbs"] / HBM_PEAK_GBS, 4),
                    },
-        # the dominant kernel is the grouped GEMM launch; launches are
-        # serialized on one stream, so per-launch time = kernel duration plus
-        # the graph's inter-kernel gap (compare rocprofv3's average)
+        # the dominant kernel is the grouped GEMM launch; the steps run back
+        # to back in one graph replay (the device holds the stream until the
+        # host has queued the replay), so per-launch time = kernel duration
+        # plus the graph's inter-kernel gap (compare rocprofv3's average)
         "roofline": {"bound": "hbm",
                      "achieved": round(g["launch_bytes"] / (g["tiled_launch_us"] * 1e-6) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["launch_bytes"] / (g["tiled_launch_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "kernel": "apus_gemm_decode_kernel (grouped, 12 GEMVs, tiled weights)",
                      "launch_us": round(g["tiled_launch_us"], 3), "bytes_per_launch": g["launch_bytes"],
-                     "traffic": CONFIG0_TRAFFIC_BYTES},
+                     "traffic": CONFIG0_TRAFFIC_BYTES,
+                     "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, calibrated "
+                                       "against a 256 MiB copy (profiles/config0_mxfp4_gemv_m1.txt); "
+                                       "not measured in this run"},
         "cpu_baseline": cpu,
         "extras": extras,
     }

@@ -134,7 +134,13 @@ uint64_t apus_hip_bytes_uploaded(void);   /* weight bytes copied to HBM */
 uint64_t apus_hip_bytes_resident(void);   /* weight bytes held in HBM */
 uint64_t apus_hip_dispatches(void);       /* kernel launches issued */
 
-/* ---- hooks, also callable directly. Host pointers; synchronous. ---- */
+/* ---- hooks, also callable directly. Host pointers; synchronous. ----
+ * Inputs the matrix cores would read differently from the reference are
+ * refused with a nonzero return (the caller then runs its CPU kernel): a
+ * non-finite activation, an E8M0 scale byte 255 (+inf in c/fp4.h:209-217,
+ * NaN on the matrix cores), an E4M3 weight or activation code 0x7F / 0xFF
+ * (+-480 in c/fp4.h:255-260, NaN on the matrix cores), and pre-quantised
+ * activation scales that are not finite powers of two. */
 /* c/attn.h:408-430 apus_fp8_linear: bf16(x) -> act quant -> FP8 GEMM ->
  * bf16(out). x [M,K], out [M,O]. */
 int apus_hip_fp8_linear(const ApusFp8W *w, const float *x, float *out,
@@ -189,8 +195,20 @@ int apus_hip_fp8_gemm(const uint8_t *w, const uint8_t *ws,
  * Same semantics as the host versions; all pointers are device pointers.
  * They exist for callers that keep activations in HBM between layers and
  * for measurement with inputs already resident. */
+/* A group holding +-inf gets the scale +inf (as the reference's does) and
+ * signed-zero codes for its finite elements; the GEMMs then return NaN for
+ * that row (E8M0 255 is NaN on the matrix cores). Non-finite activations are
+ * outside the contract of the *_dev entry points; the host-pointer entry
+ * points refuse them (nonzero), so the caller's CPU kernel handles them. */
 int apus_hip_act_quant_dev(const float *x, int M, int K, uint8_t *codes,
                            float *scales);
+/* c/moe.h:113-135 apus_expert_swiglu: h[i] = bf16((g' * (1 / (1 + expf(-g'))))
+ * * u') with g' = min(g, limit), u' = clamp(u, +-limit) when limit > 0, each
+ * step rounded as written; n elements, device pointers, asynchronous. The
+ * element function of every fused MoE kernel here; expf is ROCm's, so a
+ * result can differ from the CPU's by one BF16 ulp where the product lies
+ * within a few fp32 ulps of a BF16 rounding boundary. */
+int apus_hip_swiglu_dev(const float *g, const float *u, size_t n, float limit, float *h);
 /* round_out: bit 0 BF16-rounds the outputs; | APUS_HIP_W_TILED for weights
  * in the MFMA-tiled layout (K 2048/4096, O % 128 == 0). */
 int apus_hip_fp4_gemm_dev(const uint8_t *w, const uint8_t *ws,
@@ -284,6 +302,18 @@ int      apus_hip_moe_routed_dev(const ApusHipStore *st, int layer,
                                  const float *wgt, int s, int topk,
                                  float limit, float *y, void *workspace);
 
+/* Read-back of the routed dispatch's quantised SwiGLU activations (the w2
+ * input h = act_quant(swiglu(bf16 g, bf16 u)), c/moe.h:113-126, :309-314)
+ * from the workspace of the latest apus_hip_moe_routed_dev call with the same
+ * store, s, topk and workspace: codes [s*topk, inter] E4M3 and e8m0
+ * [s*topk, inter/128] scale bytes, row p = t*topk + j (device pointers,
+ * asynchronous, stream-ordered after that call). No counterpart in the
+ * reference (which keeps h internal): it lets a checker test the w1/w3 and
+ * w2 stages of the dispatch separately. Pairs with an expert id outside
+ * [0, E) are not written. */
+int      apus_hip_moe_routed_h(const ApusHipStore *st, int s, int topk, const void *workspace,
+                               uint8_t *codes, uint8_t *e8m0);
+
 /* Plain-weight linear on device pointers (asynchronous): same semantics and
  * flags as apus_hip_f32_linear. */
 int      apus_hip_wlinear_dev(const void *w, const float *x, float *out, int M, int K,
@@ -360,6 +390,9 @@ void *apus_hip_malloc(size_t bytes);
 int   apus_hip_free(void *p);
 int   apus_hip_h2d(void *dst, const void *src, size_t bytes);
 int   apus_hip_d2h(void *dst, const void *src, size_t bytes);
+/* Asynchronous memset on the backend stream; returns nonzero (and does
+ * nothing) while a graph capture is open on the backend stream or the
+ * selected lane: memset nodes are not recorded into graphs. */
 int   apus_hip_memset(void *dst, int value, size_t bytes);
 /* device-to-device copy on the current lane (asynchronous) */
 int   apus_hip_d2d(void *dst, const void *src, size_t bytes);
@@ -370,6 +403,13 @@ int   apus_hip_synchronize(void);
  * milliseconds since it (synchronises on the end event). */
 int   apus_hip_timer_start(void);
 float apus_hip_timer_stop(void);
+/* Hold the backend stream on the device for delay_us microseconds
+ * (0..10^6): a one-wave kernel sleeps that long. Work the host queues right
+ * after this call (warm-up launches, a timer start, a graph replay) then
+ * runs back to back once the delay ends, so a timed interval measures the
+ * device's execution, not the host's submission. No counterpart in the
+ * reference (measurement helper). */
+int   apus_hip_stream_delay(int delay_us);
 /* Concurrency lanes: extra HIP streams for the *_dev entry points, so that
  * independent work (e.g. GEMVs of different experts) can overlap. Lane 0 is
  * the backend stream. apus_hip_lanes(n) creates lanes 1..n-1 (n <= 8);
