@@ -37,6 +37,15 @@
 
 /* ------------------------------------------------------------------ state */
 
+/* Workspace of the allocation-free routed dispatch
+ * (apus_hip_moe_routed_dev_noalloc): one statically sized array in device
+ * memory, which every GPU the library runs on holds until the process ends.
+ * In host code the name is only a stand-in: its device address comes from
+ * hipGetSymbolAddress at initialisation (per device) and only that address
+ * is ever passed to kernels. */
+#define APUS_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+static __device__ __align__(256) uint8_t scratch[APUS_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local char g_err[512];
@@ -89,7 +98,7 @@ struct State {
     unsigned *pair_tk[8] = {};
     std::unordered_map<const void *, DenseW> dense;
     std::unordered_map<uint64_t, ExpertW> experts;
-    DevBuf scratch[8];
+    DevBuf slots[8];          /* grow-only device scratch of the host-pointer calls */
     /* pinned staging of the host-pointer calls' small transfers (x, out,
      * ids, ...): filled from offset 0 after every finish(), so a region is
      * never rewritten before the copy that reads it has run; downloads land
@@ -100,6 +109,9 @@ struct State {
     bool pin_failed = false;
     std::vector<std::pair<void *, size_t>> pin_out;   /* (caller dst, bytes) per staged download */
     std::vector<size_t> pin_out_off;
+    /* device address of `scratch` per device ordinal (this backend runs on
+     * device 0) */
+    uint8_t *noalloc_scratch[16] = {};
     uint64_t bytes_uploaded = 0, bytes_resident = 0, dispatches = 0;
     size_t dense_budget = 0;
     ApusHipHooks hooks{};
@@ -146,6 +158,12 @@ bool ensure_init() {
         return false;
     }
     if (!ok(hipSetDevice(0), "hipSetDevice")) return false;
+    {
+        void *p = nullptr;
+        if (!ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)") || !p)
+            return false;
+        g.noalloc_scratch[0] = (uint8_t *)p;
+    }
     if (!ok(hipStreamCreateWithFlags(&g.stream, hipStreamNonBlocking), "hipStreamCreate")) return false;
     if (!ok(hipEventCreate(&g.ev0), "hipEventCreate")) return false;
     if (!ok(hipEventCreate(&g.ev1), "hipEventCreate")) return false;
@@ -163,8 +181,8 @@ bool ensure_init() {
 }
 
 /* grow-only device scratch slot i of at least n bytes */
-void *scratch(int i, size_t n) {
-    DevBuf &b = g.scratch[i];
+void *scratch_slot(int i, size_t n) {
+    DevBuf &b = g.slots[i];
     if (b.n >= n && b.p) return b.p;
     if (b.p) { hipStreamSynchronize(g.stream); hipFree(b.p); b.p = nullptr; b.n = 0; }
     size_t want = n < 4096 ? 4096 : n;
@@ -309,8 +327,8 @@ bool moe_tiled(int dim, int inter) {
 bool upload_weights(int wfmt, uint8_t *dw, uint8_t *dws, const void *w, const void *ws,
                     size_t wbytes, size_t sbytes, int O, int K, bool tiled) {
     if (!tiled) return upload(dw, w, wbytes) && upload(dws, ws, sbytes);
-    uint8_t *sw = (uint8_t *)scratch(4, wbytes);
-    uint8_t *ss = (uint8_t *)scratch(5, sbytes);
+    uint8_t *sw = (uint8_t *)scratch_slot(4, wbytes);
+    uint8_t *ss = (uint8_t *)scratch_slot(5, sbytes);
     if (!sw || !ss || !upload(sw, w, wbytes) || !upload(ss, ws, sbytes)) return false;
     if (!launched(apus_launch_pack(wfmt, sw, ss, dw, dws, O, K, 0, g.stream), "pack")) return false;
     if (wfmt == APUS_W_FP8 && !ok(hipMemcpyAsync(dws, ss, sbytes, hipMemcpyDeviceToDevice, g.stream),
@@ -462,12 +480,12 @@ int linear_host(int wfmt, const uint8_t *w, const uint8_t *ws, const float *x,
     if (!d) return 1;
     const int wf = wfmt | (d->tiled ? APUS_HIP_W_TILED : 0);
     const size_t nab = K / 128;
-    float *dx = (float *)scratch(0, (size_t)M * K * 4);
-    uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
-    float *dsc = (float *)scratch(2, (size_t)M * nab * 4);
+    float *dx = (float *)scratch_slot(0, (size_t)M * K * 4);
+    uint8_t *dc = (uint8_t *)scratch_slot(1, (size_t)M * K);
+    float *dsc = (float *)scratch_slot(2, (size_t)M * nab * 4);
     float *dout = (float *)out_direct(out, (size_t)M * O * 4);
     const bool direct = dout != nullptr;
-    if (!direct) dout = (float *)scratch(3, (size_t)M * O * 4);
+    if (!direct) dout = (float *)scratch_slot(3, (size_t)M * O * 4);
     if (!dx || !dc || !dsc || !dout) return 1;
     if (!upload(dx, x, (size_t)M * K * 4)) return 1;
     const int f = linear_fused(wf, d->w, d->ws, dx, dout, M, K, O, g.stream);
@@ -491,11 +509,11 @@ int gemm_host(int wfmt, const uint8_t *w, const uint8_t *ws, const uint8_t *acod
     if (!weights_ok(wfmt, w, ws, wbytes, sbytes, "gemm") || !e4m3_ok(acodes, (size_t)M * K, "gemm") ||
         !pow2_ok(as, (size_t)M * nab, "gemm"))
         return 1;
-    uint8_t *dw = (uint8_t *)scratch(4, wbytes);
-    uint8_t *dws = (uint8_t *)scratch(5, sbytes);
-    uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
-    float *dsc = (float *)scratch(2, (size_t)M * nab * 4);
-    float *dout = (float *)scratch(3, (size_t)M * O * 4);
+    uint8_t *dw = (uint8_t *)scratch_slot(4, wbytes);
+    uint8_t *dws = (uint8_t *)scratch_slot(5, sbytes);
+    uint8_t *dc = (uint8_t *)scratch_slot(1, (size_t)M * K);
+    float *dsc = (float *)scratch_slot(2, (size_t)M * nab * 4);
+    float *dout = (float *)scratch_slot(3, (size_t)M * O * 4);
     if (!dw || !dws || !dc || !dsc || !dout) return 1;
     if (!upload(dw, w, wbytes) || !upload(dws, ws, sbytes) ||
         !upload(dc, acodes, (size_t)M * K) || !upload(dsc, as, (size_t)M * nab * 4))
@@ -790,7 +808,7 @@ void apus_hip_disable(void) {
     g.dense.clear();
     for (auto &kv : g.experts) hipFree(kv.second.p[0]);
     g.experts.clear();
-    for (auto &b : g.scratch) { if (b.p) hipFree(b.p); b.p = nullptr; b.n = 0; }
+    for (auto &b : g.slots) { if (b.p) hipFree(b.p); b.p = nullptr; b.n = 0; }
     if (g.pin) (void)hipHostFree(g.pin);
     g.pin = nullptr;
     g.pin_dev = nullptr;
@@ -823,9 +841,9 @@ int apus_hip_act_quant(const float *x, int M, int K, uint8_t *codes, float *scal
     std::lock_guard<std::mutex> lk(g_mu);
     if (!ensure_init() || !shape_ok(M, K, 1) || !x_finite(x, (size_t)M * K, "act_quant")) return 1;
     const size_t nab = K / 128;
-    float *dx = (float *)scratch(0, (size_t)M * K * 4);
-    uint8_t *dc = (uint8_t *)scratch(1, (size_t)M * K);
-    float *dsc = (float *)scratch(2, (size_t)M * nab * 4);
+    float *dx = (float *)scratch_slot(0, (size_t)M * K * 4);
+    uint8_t *dc = (uint8_t *)scratch_slot(1, (size_t)M * K);
+    float *dsc = (float *)scratch_slot(2, (size_t)M * nab * 4);
     if (!dx || !dc || !dsc) return 1;
     if (!upload(dx, x, (size_t)M * K * 4)) return 1;
     if (!launched(apus_launch_act_quant(dx, K, nullptr, M, K, dc, dsc, g.stream), "act_quant")) return 1;
@@ -858,10 +876,10 @@ static int wlinear_host(const void *w, bool bf16, const float *x, float *out, in
     const DenseW *d = dense_weight(bf16 ? APUS_W_BF16 : APUS_W_F32, (const uint8_t *)w, nullptr,
                                    wbytes, 0, O, K);
     if (!d) return 1;
-    float *dx = (float *)scratch(0, (size_t)M * K * 4);
+    float *dx = (float *)scratch_slot(0, (size_t)M * K * 4);
     float *dout = (float *)out_direct(out, (size_t)M * O * 4);
     const bool direct = dout != nullptr;
-    if (!direct) dout = (float *)scratch(3, (size_t)M * O * 4);
+    if (!direct) dout = (float *)scratch_slot(3, (size_t)M * O * 4);
     if (!dx || !dout || !upload(dx, x, (size_t)M * K * 4)) return 1;
     if (!launched(apus_launch_wgemv(d->w, dx, dout, M, K, O, (flags & 3) | (bf16 ? 4 : 0), g.stream),
                   "wgemv"))
@@ -912,10 +930,10 @@ int apus_hip_fp4_gemm_grouped(const ApusFp4GemmEnt *ents, size_t n_ent, const ui
     const size_t nab = K / 128;
     if (!e4m3_ok(acodes, rows * K, "grouped gemm") || !pow2_ok(as, rows * nab, "grouped gemm"))
         return 1;
-    uint8_t *dc = (uint8_t *)scratch(1, rows * K + 1);
-    float *dsc = (float *)scratch(2, rows * nab * 4 + 4);
-    float *dout = (float *)scratch(3, outrows * O * 4 + 4);
-    ApusGemmEnt *dents = (ApusGemmEnt *)scratch(6, n_ent * sizeof(ApusGemmEnt));
+    uint8_t *dc = (uint8_t *)scratch_slot(1, rows * K + 1);
+    float *dsc = (float *)scratch_slot(2, rows * nab * 4 + 4);
+    float *dout = (float *)scratch_slot(3, outrows * O * 4 + 4);
+    ApusGemmEnt *dents = (ApusGemmEnt *)scratch_slot(6, n_ent * sizeof(ApusGemmEnt));
     if (!dc || !dsc || !dout || !dents) return 1;
     if (!upload(dc, acodes, rows * K) || !upload(dsc, as, rows * nab * 4)) return 1;
     std::vector<ApusGemmEnt> he(n_ent);
@@ -1019,13 +1037,13 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
         for (int i = 0; i < 6; i++) tab[(size_t)i * E + e] = it->second.p[i];
     }
     MoeWs sizes = moe_carve(nullptr, s, topk, E, dim, inter);
-    void *ws = scratch(7, sizes.total);
-    float *dx = (float *)scratch(0, (size_t)s * dim * 4);
-    int32_t *didx = (int32_t *)scratch(1, (size_t)nj * 4 + (size_t)nj * 4);
+    void *ws = scratch_slot(7, sizes.total);
+    float *dx = (float *)scratch_slot(0, (size_t)s * dim * 4);
+    int32_t *didx = (int32_t *)scratch_slot(1, (size_t)nj * 4 + (size_t)nj * 4);
     float *dwgt = (float *)((uint8_t *)didx + (size_t)nj * 4);
     float *dy = (float *)out_direct(y, (size_t)s * dim * 4);
     const bool direct = dy != nullptr;
-    if (!direct) dy = (float *)scratch(3, (size_t)s * dim * 4);
+    if (!direct) dy = (float *)scratch_slot(3, (size_t)s * dim * 4);
     if (!ws || !dx || !didx || !dy) return 1;
     MoeWs mw = moe_carve(ws, s, topk, E, dim, inter);
     if (!upload(mw.tab, tab.data(), tab.size() * sizeof(void *)) ||
@@ -1214,8 +1232,8 @@ int apus_hip_store_fill_random(ApusHipStore *st, uint64_t seed) {
     const int mo[3] = {st->inter, st->dim, st->inter}, mk[3] = {st->dim, st->inter, st->dim};
     /* tiled stores: each matrix is generated row-major into staging (stream
      * ordered, so the staging is reused) and packed into place */
-    uint8_t *sw = st->tiled ? (uint8_t *)scratch(4, st->sz[0] > st->sz[2] ? st->sz[0] : st->sz[2]) : nullptr;
-    uint8_t *ss = st->tiled ? (uint8_t *)scratch(5, st->sz[1] > st->sz[3] ? st->sz[1] : st->sz[3]) : nullptr;
+    uint8_t *sw = st->tiled ? (uint8_t *)scratch_slot(4, st->sz[0] > st->sz[2] ? st->sz[0] : st->sz[2]) : nullptr;
+    uint8_t *ss = st->tiled ? (uint8_t *)scratch_slot(5, st->sz[1] > st->sz[3] ? st->sz[1] : st->sz[3]) : nullptr;
     if (st->tiled && (!sw || !ss)) return 1;
     for (int l = 0; l < st->L; l++)
         for (int e = 0; e < st->E; e++) {
@@ -1471,6 +1489,16 @@ size_t apus_hip_moe_workspace(const ApusHipStore *st, int s, int topk) {
     return moe_carve(nullptr, s, topk, st->E, st->dim, st->inter).total;
 }
 
+static int routed_dev(const ApusHipStore *st, int layer, const float *x, const int32_t *idx,
+                      const float *wgt, int s, int topk, float limit, float *y, void *workspace) {
+    MoeWs mw = moe_carve(workspace, s, topk, st->E, st->dim, st->inter);
+    MoeSlab slab{st->layer_base[layer], st->expert_bytes, {}};
+    size_t off = 0;
+    for (int i = 0; i < 6; i++) { slab.off[i] = off; off += align256(st->sz[i]); }
+    return moe_pipeline(st->E, st->dim, st->inter, limit, st->layer_tab[layer], x, idx, wgt, s,
+                        topk, y, mw, st->tiled, &slab, dev_stream());
+}
+
 int apus_hip_moe_routed_dev(const ApusHipStore *st, int layer, const float *x, const int32_t *idx,
                             const float *wgt, int s, int topk, float limit, float *y,
                             void *workspace) {
@@ -1478,12 +1506,32 @@ int apus_hip_moe_routed_dev(const ApusHipStore *st, int layer, const float *x, c
         set_err("moe_routed_dev: bad arguments");
         return 1;
     }
-    MoeWs mw = moe_carve(workspace, s, topk, st->E, st->dim, st->inter);
-    MoeSlab slab{st->layer_base[layer], st->expert_bytes, {}};
-    size_t off = 0;
-    for (int i = 0; i < 6; i++) { slab.off[i] = off; off += align256(st->sz[i]); }
-    return moe_pipeline(st->E, st->dim, st->inter, limit, st->layer_tab[layer], x, idx, wgt, s,
-                        topk, y, mw, st->tiled, &slab, dev_stream());
+    return routed_dev(st, layer, x, idx, wgt, s, topk, limit, y, workspace);
+}
+
+size_t apus_hip_moe_noalloc_max(void) { return APUS_NOALLOC_SCRATCH_BYTES; }
+
+int apus_hip_moe_routed_dev_noalloc(const ApusHipStore *st, int layer, const float *x,
+                                    const int32_t *idx, const float *wgt, int s, int topk,
+                                    float limit, float *y) {
+    /* set-up (streams, counters, the scratch address) happens in
+     * apus_hip_enable / the store's creation: this call allocates nothing */
+    if (!g.inited || !g.noalloc_scratch[0]) {
+        set_err("moe_routed_dev_noalloc: call apus_hip_enable first");
+        return 1;
+    }
+    if (!st || layer < 0 || layer >= st->L || s <= 0 || topk <= 0) {
+        set_err("moe_routed_dev_noalloc: bad arguments");
+        return 1;
+    }
+    const size_t need = moe_carve(nullptr, s, topk, st->E, st->dim, st->inter).total;
+    if (need > APUS_NOALLOC_SCRATCH_BYTES) {
+        set_err("moe_routed_dev_noalloc: %d tokens x top-%d need %zu bytes of workspace, the "
+                "static scratch holds %zu (use apus_hip_moe_routed_dev with a workspace)",
+                s, topk, need, (size_t)APUS_NOALLOC_SCRATCH_BYTES);
+        return 1;
+    }
+    return routed_dev(st, layer, x, idx, wgt, s, topk, limit, y, g.noalloc_scratch[0]);
 }
 
 int apus_hip_moe_routed_h(const ApusHipStore *st, int s, int topk, const void *workspace,
@@ -1796,7 +1844,7 @@ int apus_hip_moe_forward_dev(const ApusHipStore *st, int layer, const ApusHipMoe
 
 int apus_hip_check_e4m3_hw(unsigned *mismatches, unsigned *last_bad_bits) {
     if (!ensure_init()) return 1;
-    unsigned *d = (unsigned *)scratch(7, 2 * sizeof(unsigned));
+    unsigned *d = (unsigned *)scratch_slot(7, 2 * sizeof(unsigned));
     if (!d || !ok(hipMemsetAsync(d, 0, 2 * sizeof(unsigned), g.stream), "memset") ||
         !launched(apus_launch_e4m3_hw_check(d, d + 1, g.stream), "e4m3 check"))
         return 1;

@@ -302,6 +302,23 @@ int      apus_hip_moe_routed_dev(const ApusHipStore *st, int layer,
                                  const float *wgt, int s, int topk,
                                  float limit, float *y, void *workspace);
 
+/* apus_hip_moe_routed_dev without a caller workspace, for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * workspace is a library-owned static device array of
+ * apus_hip_moe_noalloc_max() bytes (64 MiB: the routed dispatch of up to
+ * ~256 tokens x top-6 at dim 4096, inter 2048; larger calls are refused
+ * with an error naming the bytes needed); the call itself allocates nothing
+ * (apus_hip_enable must have run first). Every call on a GPU shares that
+ * GPU's array and it keeps the last call's contents (nothing in it needs
+ * to start at zero): calls that overlap on one GPU (other lanes, other
+ * threads) race. Results are bit-identical to apus_hip_moe_routed_dev. */
+size_t   apus_hip_moe_noalloc_max(void);
+int      apus_hip_moe_routed_dev_noalloc(const ApusHipStore *st, int layer,
+                                         const float *x, const int32_t *idx,
+                                         const float *wgt, int s, int topk,
+                                         float limit, float *y);
+
 /* Read-back of the routed dispatch's quantised SwiGLU activations (the w2
  * input h = act_quant(swiglu(bf16 g, bf16 u)), c/moe.h:113-126, :309-314)
  * from the workspace of the latest apus_hip_moe_routed_dev call with the same
