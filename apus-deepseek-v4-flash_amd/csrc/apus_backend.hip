@@ -1228,34 +1228,20 @@ uint64_t apus_hip_store_bytes(const ApusHipStore *st) {
 int apus_hip_store_fill_random(ApusHipStore *st, uint64_t seed) {
     if (!st) return 1;
     std::lock_guard<std::mutex> lk(g_mu);
-    static const int kinds[6] = {0, 1, 0, 1, 0, 1};
+    if (!ensure_init()) return 1;
+    /* one launch per layer and tensor, generated straight into the store's
+     * layout (tensor i of expert e of layer l: stream ((l * E + e) * 8 + i)) */
     const int mo[3] = {st->inter, st->dim, st->inter}, mk[3] = {st->dim, st->inter, st->dim};
-    /* tiled stores: each matrix is generated row-major into staging (stream
-     * ordered, so the staging is reused) and packed into place */
-    uint8_t *sw = st->tiled ? (uint8_t *)scratch_slot(4, st->sz[0] > st->sz[2] ? st->sz[0] : st->sz[2]) : nullptr;
-    uint8_t *ss = st->tiled ? (uint8_t *)scratch_slot(5, st->sz[1] > st->sz[3] ? st->sz[1] : st->sz[3]) : nullptr;
-    if (st->tiled && (!sw || !ss)) return 1;
+    size_t off[6], o = 0;
+    for (int i = 0; i < 6; i++) { off[i] = o; o += align256(st->sz[i]); }
     for (int l = 0; l < st->L; l++)
-        for (int e = 0; e < st->E; e++) {
-            uint8_t *p[6];
-            size_t off = 0;
-            for (int i = 0; i < 6; i++) {
-                p[i] = st->layer_base[l] + st->expert_bytes * e + off;
-                off += align256(st->sz[i]);
-            }
-            for (int m = 0; m < 3; m++) {
-                for (int h = 0; h < 2; h++) {
-                    const int i = 2 * m + h;
-                    const uint64_t sid = ((uint64_t)l * st->E + e) * 8 + i;
-                    uint8_t *dst = st->tiled ? (h ? ss : sw) : p[i];
-                    if (!launched(apus_launch_fill(dst, st->sz[i], seed, sid, 0, kinds[i], g.stream), "fill"))
-                        return 1;
-                }
-                if (st->tiled &&
-                    !launched(apus_launch_pack(APUS_W_FP4, sw, ss, p[2 * m], p[2 * m + 1], mo[m], mk[m], 0,
-                                               g.stream), "pack"))
-                    return 1;
-            }
+        for (int i = 0; i < 6; i++) {
+            const int m = i / 2;
+            if (!launched(apus_launch_store_fill(st->layer_base[l] + off[i], st->expert_bytes, st->E, mo[m],
+                                                 mk[m], i & 1, st->tiled ? 1 : 0, seed,
+                                                 (uint64_t)l * st->E * 8 + i, g.stream),
+                          "store fill"))
+                return 1;
         }
     return finish() ? 0 : 1;
 }

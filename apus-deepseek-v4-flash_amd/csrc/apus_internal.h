@@ -249,4 +249,10 @@ hipError_t apus_launch_moe_h_gather(const uint8_t *hc, const void *hs, int hs_f3
 hipError_t apus_launch_swiglu(const float *g, const float *u, size_t n, float limit, float *h,
                               hipStream_t st);
 
+/* one tensor of every expert of a store layer, generated in place (MXFP4
+ * weights what 0 / E8M0 scales what 1; MFMA-tiled when tiled): equal to
+ * apus_launch_fill of stream sid0 + 8 e followed by apus_launch_pack */
+hipError_t apus_launch_store_fill(uint8_t *base, size_t stride, int E, int O, int K, int what,
+                                  int tiled, uint64_t seed, uint64_t sid0, hipStream_t st);
+
 #endif /* APUS_INTERNAL_H */

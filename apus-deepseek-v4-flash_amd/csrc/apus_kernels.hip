@@ -522,6 +522,70 @@ hipError_t apus_launch_fill(uint8_t *dst, size_t n, uint64_t seed,
     return hipGetLastError();
 }
 
+/* One tensor (w or its E8M0 scales) of every expert of an expert-store layer,
+ * generated straight into the store's layout: expert e's tensor at
+ * base + e * stride, stream id sid0 + 8 e. Each thread writes one 16-byte
+ * piece: it finds the piece's row-major position (the MFMA-tiled layout of
+ * apus_pack_kernel when tiled) and generates the 16 bytes the counter fill
+ * would have put there, so the result equals fill-then-pack byte for byte.
+ * what: 0 = MXFP4 weights [O, K/2] (kind 0), 1 = E8M0 scales [O, K/32]
+ * (kind 1). */
+__global__ __launch_bounds__(256) void apus_store_fill_kernel(uint8_t *base, size_t stride, int O,
+                                                              int K, int what, int tiled,
+                                                              uint64_t seed, uint64_t sid0) {
+    const int e = blockIdx.y;
+    const size_t c = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t rb = what ? (size_t)K / 32 : (size_t)K / 2, n = (size_t)O * rb;
+    if (c * 16 >= n) return;
+    size_t row = 0, col = c * 16;          /* row-major: position c * 16 */
+    if (!tiled) {
+    } else if (what == 0) {
+        const int NQ = K >> 7, lane = (int)(c & 63);
+        const size_t rest = c >> 6;
+        row = (rest / NQ) * 16 + (lane & 15);
+        col = (rest % NQ) * 64 + (lane >> 4) * 16;
+    } else {
+        const int NS = K >> 9;
+        const size_t rest = c >> 4;
+        row = (rest / NS) * 16 + (c & 15);
+        col = (rest % NS) * 16;
+    }
+    const uint64_t sid = sid0 + (uint64_t)e * 8, pos = row * rb + col;
+    uint32_t w[4];
+    if (what == 0) {
+        const uint64_t h0 = apus_hash64(seed, sid, pos >> 3), h1 = apus_hash64(seed, sid, (pos >> 3) + 1);
+        w[0] = (uint32_t)h0; w[1] = (uint32_t)(h0 >> 32); w[2] = (uint32_t)h1; w[3] = (uint32_t)(h1 >> 32);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint64_t h = apus_hash64(seed, sid, pos + 4 * i + k);
+                v |= (118u + (uint32_t)((h >> 32) % 13u)) << (8 * k);
+            }
+            w[i] = v;
+        }
+    }
+    uint8_t *dst = base + (size_t)e * stride + c * 16;
+    if (c * 16 + 16 <= n) {
+        *reinterpret_cast<uint4 *>(dst) = uint4{w[0], w[1], w[2], w[3]};
+    } else {
+        for (size_t k = 0; c * 16 + k < n; ++k) dst[k] = (uint8_t)(w[k >> 2] >> (8 * (k & 3)));
+    }
+}
+
+hipError_t apus_launch_store_fill(uint8_t *base, size_t stride, int E, int O, int K, int what,
+                                  int tiled, uint64_t seed, uint64_t sid0, hipStream_t st) {
+    if (E <= 0 || O <= 0 || K <= 0 || K % 32 || (tiled && (O % 16 || K % 512)) || stride % 16 ||
+        reinterpret_cast<uintptr_t>(base) % 16)
+        return hipErrorInvalidValue;
+    const size_t pieces = ((size_t)O * (what ? (size_t)K / 32 : (size_t)K / 2) + 15) / 16;
+    hipLaunchKernelGGL(apus_store_fill_kernel, dim3((unsigned)((pieces + 255) / 256), (unsigned)E),
+                       dim3(256), 0, st, base, stride, O, K, what, tiled, seed, sid0);
+    return hipGetLastError();
+}
+
 /* ------------------------------------------------- MFMA-tiled weight layout */
 
 /* One thread per 16-byte piece of the tiled layout: FP4 weights

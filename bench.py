@@ -673,7 +673,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--skip-extras", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="", help="comma list: gemv,fp8,decode,prefill,full,load")
+    ap.add_argument("--only", default="", help="comma list: gemv,fp8,attn,decode,prefill,full,load")
     ap.add_argument("--full-layers", type=int, default=43,
                     help="config 4: resident MoE layers (43 fill ~148 GB)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -715,6 +715,7 @@ def main():
         extras["config1_fp8_M1_us"] = round(f8["M1"]["us"], 2)
         extras["config1_fp8_M512_TFLOPs"] = round(f8["M512"]["tflops"], 1)
         extras["config1_fp8_M512_us"] = round(f8["M512"]["us"], 2)
+    if not args.skip_extras and want("attn"):
         hd = bench_head(H, dev)
         extras["lm_head_bf16_us"] = round(hd["us"], 1)
         extras["lm_head_bf16_GBs"] = round(hd["GBs"], 1)
@@ -732,18 +733,18 @@ def main():
         if want("decode"):
             log("[bench] config 2 decode MoE, 64 tokens top-6 of 256")
             idx, wgt = gate_routing(rng, 64, 256, 6)
-            d = bench_moe(H, dev, store, layers, 64, idx, wgt, 64)
+            d = bench_moe(H, dev, store, layers, 64, idx, wgt, min(64, args.steps))
             extras.update({"config2_decode_tok_s": round(d["tok_s"], 1),
                            "config2_decode_us": round(d["us"], 1),
                            "config2_decode_GBs": round(d["gbs"], 1),
                            "config2_unique_experts": d["unique_experts"]})
             for sl in (1, 64):
-                r = bench_moe_sublayer(H, dev, store, layers, sl, 64)
+                r = bench_moe_sublayer(H, dev, store, layers, sl, min(64, args.steps))
                 extras[f"moe_sublayer_s{sl}_us"] = round(r["us"], 1)
         if want("prefill"):
             log("[bench] config 3 prefill MoE, 512 tokens top-6 of 256, Zipf(1.1)")
             idx, wgt = zipf_routing(rng, 512, 256, 6, 1.1)
-            p = bench_moe(H, dev, store, layers, 512, idx, wgt, 16)
+            p = bench_moe(H, dev, store, layers, 512, idx, wgt, min(16, args.steps))
             extras.update({"config3_prefill_TFLOPs": round(p["tflops"], 2),
                            "config3_prefill_us": round(p["us"], 1),
                            "config3_frac_fp4_peak": round(p["frac_fp4_peak"], 5),
