@@ -138,6 +138,8 @@ SIGNATURES = {
     "apus_hip_moe_workspace": (C.c_size_t, [vp, C.c_int, C.c_int]),
     "apus_hip_moe_routed_dev": (C.c_int, [vp, C.c_int, vp, vp, vp, C.c_int, C.c_int, C.c_float,
                                           vp, vp]),
+    "apus_hip_moe_routed_dense_dev": (C.c_int, [vp, C.c_int, vp, vp, vp, C.c_int, C.c_int, C.c_float,
+                                                vp, vp, vp, vp, C.c_int, vp]),
     "apus_hip_moe_noalloc_max": (C.c_size_t, []),
     "apus_hip_moe_routed_dev_noalloc": (C.c_int, [vp, C.c_int, vp, vp, vp, C.c_int, C.c_int,
                                                   C.c_float, vp]),

@@ -619,12 +619,20 @@ struct SharedFuse {
     float *sh_out, *out;           /* sh = bf16(w2 h); out = bf16(y + sh) */
 };
 
+/* a dense FP8 linear of the same x co-scheduled in the one-token w1/w3
+ * launch: out [s, 2 inter] = bf16(W x), W [2 inter, dim] */
+struct DenseRider {
+    const uint8_t *w, *ws;
+    int tiled;
+    float *out;
+};
+
 int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
                  const float *x, const int32_t *idx, const float *wgt, int s,
                  int topk, float *y, const MoeWs &w, bool wtiled, const MoeSlab *slab,
                  hipStream_t st, const float *add_src = nullptr, float *add_out = nullptr,
                  hipEvent_t add_ready = nullptr, const SharedFuse *shf = nullptr,
-                 const RouteFuse *rf = nullptr) {
+                 const RouteFuse *rf = nullptr, const DenseRider *rd = nullptr) {
     /* with add_out: also add_out = bf16(y + add_src), fused into the last
      * launch where it can be; add_src is complete once add_ready has fired */
     auto wait_add = [&]() {
@@ -674,6 +682,7 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
             return 1;
         }
         a.hq = w.hc; a.hqs = (uint8_t *)w.hs; a.hq_tk = pair_tickets(st);
+        if (rd) { a.rdw = rd->w; a.rdws = rd->ws; a.rdout = rd->out; a.rdtiled = rd->tiled; }
         if (!launched(apus_launch_moe_pair13(&a, nj, st), "pair w1/w3")) return 1;
         ApusGemmArgs b{};
         b.wtiled = wtiled;
@@ -701,6 +710,15 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
     constexpr int SMALL = MOE_SMALL;
     if (!launched(apus_launch_act_quant(x, dim, nullptr, s, dim, w.xc, w.xs, st), "act_quant"))
         return 1;
+    if (rd) {
+        /* the dense linear on the quantised x (its own launch here) */
+        ApusGemmArgs d{};
+        d.wtiled = rd->tiled;
+        d.acodes = w.xc; d.ascale = w.xs;
+        d.ent0.w = rd->w; d.ent0.ws = rd->ws; d.ent0.out = rd->out; d.ent0.M = s;
+        d.O = 2 * inter; d.K = dim; d.ldo = 2 * inter; d.round_out = 1;
+        if (!launched(apus_launch_gemm(APUS_W_FP8, &d, 1, st), "dense rider")) return 1;
+    }
     if (!launched(apus_launch_moe_route(idx, nj, topk, E, t, w.gm, w.um, w.eo, w.pair, w.tok,
                                         w.e13s, w.e2s, w.e13l, w.e2l, SMALL, w.items13, w.items2,
                                         w.n_items, st), "moe_route"))
@@ -1493,6 +1511,29 @@ int apus_hip_moe_routed_dev(const ApusHipStore *st, int layer, const float *x, c
         return 1;
     }
     return routed_dev(st, layer, x, idx, wgt, s, topk, limit, y, workspace);
+}
+
+int apus_hip_moe_routed_dense_dev(const ApusHipStore *st, int layer, const float *x,
+                                  const int32_t *idx, const float *wgt, int s, int topk, float limit,
+                                  float *y, void *workspace, const uint8_t *dw, const uint8_t *dws,
+                                  int dense_tiled, float *dense_out) {
+    if (!st || layer < 0 || layer >= st->L || s <= 0 || topk <= 0 || !workspace || !dw || !dws ||
+        !dense_out || st->inter % 64) {
+        set_err("moe_routed_dense_dev: bad arguments");
+        return 1;
+    }
+    if (dense_tiled && !tiled_shape(2 * st->inter, st->dim)) {
+        set_err("moe_routed_dense_dev: a tiled dense weight needs 2*inter %% 128 == 0 and K 1024..8192");
+        return 1;
+    }
+    MoeWs mw = moe_carve(workspace, s, topk, st->E, st->dim, st->inter);
+    MoeSlab slab{st->layer_base[layer], st->expert_bytes, {}};
+    size_t off = 0;
+    for (int i = 0; i < 6; i++) { slab.off[i] = off; off += align256(st->sz[i]); }
+    DenseRider rd{dw, dws, dense_tiled ? 1 : 0, dense_out};
+    return moe_pipeline(st->E, st->dim, st->inter, limit, st->layer_tab[layer], x, idx, wgt, s, topk, y,
+                        mw, st->tiled, &slab, dev_stream(), nullptr, nullptr, nullptr, nullptr, nullptr,
+                        &rd);
 }
 
 size_t apus_hip_moe_noalloc_max(void) { return APUS_NOALLOC_SCRATCH_BYTES; }

@@ -1032,7 +1032,7 @@ template <int WF, int NS, int TILES>
 __device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const ApusStageRaw<APUS_A_F32> &raw,
                                                  const ApusGemmEnt &ent, bool tiled, bool ok,
                                                  int hrow, uint8_t *lcodes, uint8_t *lsc,
-                                                 float (*lgu)[TILES][64]) {
+                                                 float (*lgu)[TILES][64], float *plain = nullptr) {
     constexpr int K = NS * 512;
     /* 16-wave workgroups get at most 128 registers a lane: a shorter FP8 ring */
     constexpr int PD = (TILES == 8 && WF == APUS_W_FP8) ? 2 : 3;
@@ -1081,6 +1081,17 @@ __device__ __forceinline__ void apus_pair13_body(const ApusGemmArgs &args, const
      * pick the g == 0 lanes of the w1 and w3 waves */
     lgu[mat][tile][lane] = apus_bf16_rne(acc[0]);
     __syncthreads();
+    if (plain) {
+        /* a dense linear riding in the launch: rows [0, O) of its weight are
+         * "w1", rows [O, 2 O) "w3"; out = bf16(W x) as is */
+        if (threadIdx.x < 32 * TILES) {
+            const int mt = threadIdx.x / (16 * TILES), rem = threadIdx.x - mt * 16 * TILES;
+            const int t = rem >> 4, rr = rem & 15;
+            apus_gst<float>(plain + (size_t)mt * args.O + blockIdx.x * (16 * TILES) + t * 16 + rr,
+                            lgu[mt][t][rr]);
+        }
+        return;
+    }
     if constexpr (TILES == 8) {
         /* the workgroup holds a whole 128-column group of h: quantise it
          * here as the activation quantiser does (c/fp4.h:293-321: BF16,
@@ -1167,6 +1178,19 @@ __global__ __launch_bounds__(128 * TILES) void apus_moe_pair13_kernel(ApusGemmAr
     const int mat = (threadIdx.x >> 6) & 1;
     const int p = blockIdx.y;
     ApusStageRaw<APUS_A_F32> raw;
+    const int nsh = SH ? args.acc_s : 0;
+    if (args.rdout && p >= args.npairs + nsh) {
+        /* token t's dense FP8 linear [2 O, K] (rider rows after the pairs and
+         * the shared-expert rows): out row t of rdout [s, 2 O] */
+        const int t = p - args.npairs - nsh;
+        apus_stage_load<K, APUS_A_F32>(args, nullptr, t, 0, 1, 0, raw);
+        ApusGemmEnt ent;
+        ent.w = mat ? args.rdw + (size_t)args.O * K : args.rdw;
+        ent.ws = mat ? args.rdws + (size_t)(args.O / 128) * NQ : args.rdws;
+        apus_pair13_body<APUS_W_FP8, NS, TILES>(args, raw, ent, args.rdtiled, true, p, lcodes, lsc, lgu,
+                                                args.rdout + (size_t)t * 2 * args.O);
+        return;
+    }
     if (SH && p >= args.npairs) {
         /* token t's shared expert: FP8 w1 / w3 */
         const int t = p - args.npairs;
@@ -1344,7 +1368,8 @@ hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t
     if (a->rsp && (a->rE <= 0 || a->rE > 1024 || a->adiv > 16 || a->adiv > a->rE || !a->ridx ||
                    !a->rwgt || (!a->rt2e && !a->rsel) || (a->rt2e && !a->rids)))
         return hipErrorInvalidValue;
-    const int rows = npairs + (sh ? a->acc_s : 0);
+    if (a->rdout && (!a->rdw || !a->rdws || a->acc_s <= 0 || a->O % 128)) return hipErrorInvalidValue;
+    const int rows = npairs + (sh ? a->acc_s : 0) + (a->rdout ? a->acc_s : 0);
     /* 128-column workgroups (16 waves) quantise h themselves; 32-column ones
      * hand it over through counters. The wide ones win once they give at
      * least one workgroup per CU (4 tokens of top-6: 3.7 us less per

@@ -101,6 +101,13 @@ typedef struct {
      * apus_moe_pair2 reads its A operands straight from hq / hqs */
     uint8_t *hq, *hqs;
     unsigned *hq_tk;
+    /* apus_moe_pair13 with rdout set: launch rows after the pairs (and the
+     * shared-expert rows) compute, per token t, a dense FP8 linear of the same
+     * x: rdout[t, 0 : 2 O] = bf16(W x) with W = rdw [2 O, K] (tile scales
+     * rdws [2 O / 128, K / 128]; MFMA-tiled when rdtiled) */
+    const uint8_t *rdw, *rdws;
+    float *rdout;
+    int rdtiled, pad4;
     const float *rsel, *rsp;
     const int64_t *rt2e, *rids;
     float rscale;

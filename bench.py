@@ -456,18 +456,19 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
         dx = dev.upload(x)
         hd = dev.alloc(dim * 4)
         y = dev.alloc(dim * 4 * L)
-        wlin = dev.alloc(L_.apus_hip_linear_workspace(1, dim))
         wsp = dev.alloc(L_.apus_hip_moe_workspace(store, 1, topk))
         per = topk * 4
 
         def step(t):
+            # per layer: the FP8 projection of x and the routed dispatch of x;
+            # the projection rides in the routed w1/w3 launch (2 launches a layer)
             for l in range(L):
-                H._check(L_.apus_hip_linear_dev(1 | H.W_TILED, wdt.ptr + l * dbytes, wds.ptr + l * dsb,
-                                                dx.ptr, hd.ptr, 1, dim, dim, wlin.ptr), "fp8 linear")
                 off = (t * L + l) * per
-                H._check(L_.apus_hip_moe_routed_dev(store, l, dx.ptr, didx.ptr + off,
-                                                    dwgt.ptr + off, 1, topk, 10.0,
-                                                    y.ptr + l * dim * 4, wsp.ptr), "moe")
+                H._check(L_.apus_hip_moe_routed_dense_dev(store, l, dx.ptr, didx.ptr + off,
+                                                          dwgt.ptr + off, 1, topk, 10.0,
+                                                          y.ptr + l * dim * 4, wsp.ptr,
+                                                          wdt.ptr + l * dbytes, wds.ptr + l * dsb, 1,
+                                                          hd.ptr), "moe + fp8 projection")
 
         d0 = L_.apus_hip_dispatches()
         step(0)

@@ -302,6 +302,21 @@ int      apus_hip_moe_routed_dev(const ApusHipStore *st, int layer,
                                  const float *wgt, int s, int topk,
                                  float limit, float *y, void *workspace);
 
+/* apus_hip_moe_routed_dev plus a dense FP8 linear of the same x, e.g. a
+ * shared expert's fused gate/up projection: dense_out [s, 2*inter] =
+ * bf16(W x) (c/attn.h:408-430 semantics) for W [2*inter, dim] E4M3 with
+ * 128 x 128 E8M0 tile scales dws (MFMA-tiled when dense_tiled). With the
+ * one-token kernels (s * topk <= 32, topk 6 or 8, dim and inter 2048 or
+ * 4096) the linear runs inside the routed w1/w3 launch, so the pair costs
+ * two launches instead of three; otherwise it is its own launch on the
+ * quantised x. No counterpart in the reference (a co-scheduling of two of
+ * its calls). Device pointers, asynchronous. */
+int      apus_hip_moe_routed_dense_dev(const ApusHipStore *st, int layer, const float *x,
+                                       const int32_t *idx, const float *wgt, int s, int topk,
+                                       float limit, float *y, void *workspace,
+                                       const uint8_t *dw, const uint8_t *dws, int dense_tiled,
+                                       float *dense_out);
+
 /* apus_hip_moe_routed_dev without a caller workspace, for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). No counterpart in the reference. The

@@ -235,3 +235,41 @@ def test_moe_routed_dev_graph_replays(hip, oracle, store, rng):
         run(di2, dw2, dy2)
         got2 = dy2.to_array(np.float32, (1, dim))
         assert np.array_equal(got2.view(np.uint32), eager2.view(np.uint32)), rep
+
+
+@pytest.mark.parametrize("s", [1, 7])
+def test_routed_with_dense_rider(hip, oracle, store, rng, s):
+    """apus_hip_moe_routed_dense_dev: the routed output equals
+    apus_hip_moe_routed_dev bit for bit, and the co-scheduled dense FP8
+    linear [2*inter, dim] (inside the one-token w1/w3 launch at s = 1, its
+    own launch in the sorted pipeline at s = 7) is within the linear bar of
+    the oracle's float64 truth (one BF16 ulp + 1e-4 * esc)."""
+    from helpers import bf16, bf16_linear_ok, fp8_weights
+    E, dim, inter, topk = 16, 4096, 2048, 6
+    st = store(1, E, dim, inter)
+    L_ = hip.lib()
+    hip._check(L_.apus_hip_store_fill_random(st, 3), "fill")
+    x = bf16(acts(rng, s, dim))
+    idx, wgt = topk_routing(rng, s, E, topk)
+    w8, ws8 = fp8_weights(rng, 2 * inter, dim)
+    dw, dws = hip.DevBuf(w8.nbytes), hip.DevBuf.from_array(ws8)
+    raw = hip.DevBuf.from_array(w8)
+    hip._check(L_.apus_hip_pack_weights_dev(1, raw.ptr, None, dw.ptr, None, 2 * inter, dim), "pack")
+    dx, di, dwg = (hip.DevBuf.from_array(a) for a in (x, idx, wgt))
+    y0, y1 = hip.DevBuf(s * dim * 4), hip.DevBuf(s * dim * 4)
+    dout = hip.DevBuf(s * 2 * inter * 4)
+    wsp = hip.DevBuf(L_.apus_hip_moe_workspace(st, s, topk))
+    hip._check(L_.apus_hip_moe_routed_dev(st, 0, dx.ptr, di.ptr, dwg.ptr, s, topk, 10.0, y0.ptr,
+                                          wsp.ptr), "routed_dev")
+    d0 = L_.apus_hip_dispatches()
+    hip._check(L_.apus_hip_moe_routed_dense_dev(st, 0, dx.ptr, di.ptr, dwg.ptr, s, topk, 10.0, y1.ptr,
+                                                wsp.ptr, dw.ptr, dws.ptr, 1, dout.ptr), "routed_dense_dev")
+    launches = L_.apus_hip_dispatches() - d0
+    a, b = y0.to_array(np.float32, (s, dim)), y1.to_array(np.float32, (s, dim))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    got = dout.to_array(np.float32, (s, 2 * inter))
+    c, sc = oracle.act_quant(x)
+    truth, esc = oracle.fp8_truth(w8, ws8, c, sc)
+    assert bf16_linear_ok(got, truth, 1e-4 * esc).all()
+    if s == 1:
+        assert launches == 2, launches        # rider inside the w1/w3 launch
