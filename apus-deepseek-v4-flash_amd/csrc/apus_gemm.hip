@@ -1227,17 +1227,22 @@ __global__ __launch_bounds__(128 * TILES) void apus_moe_pair13_kernel(ApusGemmAr
     apus_pair13_body<APUS_W_FP4, NS, TILES>(args, raw, ent, args.wtiled, ok, p, lcodes, lsc, lgu);
 }
 
-template <int NS, int NP, bool SH>
-__global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) {
-    constexpr int K = NS * 512, NQ = NS * 4, KS = 4, NSW = NS / KS;
-    constexpr int STEPS = NP * NSW, PD = STEPS < 6 ? STEPS : (NSW == 1 ? 6 : 4);
+template <int NS, int NP, bool SH, int G>
+__global__ __launch_bounds__(256 * G) void apus_moe_pair2_kernel(ApusGemmArgs args) {
+    /* G groups of 4 waves: group i takes the pairs [i NP/G, (i+1) NP/G) (and
+     * the last group the shared w2); the 4 waves of a group take the K
+     * quarters */
+    constexpr int K = NS * 512, NQ = NS * 4, KS = 4, NSW = NS / KS, NPG = NP / G;
+    constexpr int STEPS = NPG * NSW, PD = STEPS < 6 ? STEPS : (NSW == 1 ? 6 : 4);
+    static_assert(NP % G == 0, "pairs per wave group");
     constexpr int NR = NP + (SH ? 1 : 0);            /* A rows per token */
     static_assert(NS % KS == 0 && NP <= 8, "pair2 shape");
     static_assert(!SH || NSW == 1, "the shared w2 takes one 512-slice per wave");
     __shared__ float lred[KS][NR][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
-    const int kpart = wave;
+    const int kpart = wave & 3, grp = __builtin_amdgcn_readfirstlane(wave >> 2), jb = grp * NPG;
+    const bool shg = SH && grp == G - 1;           /* this group runs the shared w2 */
     const int o = blockIdx.x * 16 + r;
     const int sbase = kpart * NSW;
     /* the shared w2 stream of this lane (FP8, one 512-slice per wave) */
@@ -1269,27 +1274,29 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
             asv[si] = arow ? apus_gld<unsigned>(args.hqs + (size_t)hr * NQ + (sbase + si) * 4)
                            : 0x7f7f7f7fu;
         }
-        ApusWLane wl[NP];
+        ApusWLane wl[NPG];
         bool okj[NP];
 #pragma unroll
         for (int j = 0; j < NP; ++j) {
             const int e = apus_gld<int>(args.pidx + p0 + j);
             okj[j] = (unsigned)e < (unsigned)args.pE;
-            ApusGemmEnt ent;
-            apus_expert_ptrs(args, 0, okj[j] ? e : 0, ent.w, ent.ws);
-            wl[j] = apus_wlane<APUS_W_FP4>(ent, args.wtiled, o, lane, K);
+            if (j >= jb && j < jb + NPG) {
+                ApusGemmEnt ent;
+                apus_expert_ptrs(args, 0, okj[j] ? e : 0, ent.w, ent.ws);
+                wl[j - jb] = apus_wlane<APUS_W_FP4>(ent, args.wtiled, o, lane, K);
+            }
         }
         ApusBFrag<APUS_W_FP4> ring[PD];
 #pragma unroll
         for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl[u / NSW], sbase + u % NSW);
         ApusBFrag<APUS_W_FP8> fsh;
-        if constexpr (SH) apus_load_b_full<APUS_W_FP8>(fsh, wsh, sbase);
-        apus_v4f acc[NP];
+        if (shg) apus_load_b_full<APUS_W_FP8>(fsh, wsh, sbase);
+        apus_v4f acc[NPG];
 #pragma unroll
-        for (int j = 0; j < NP; ++j) acc[j] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < NPG; ++j) acc[j] = apus_v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int stp = 0; stp < STEPS; ++stp) {
-            const int j = stp / NSW, si = stp % NSW;
+            const int jl = stp / NSW, j = jb + jl, si = stp % NSW;
             ApusBFrag<APUS_W_FP4> &cur = ring[stp % PD];
             const int z = r == j ? -1 : 0;
 #pragma unroll
@@ -1301,13 +1308,13 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
                 const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
                 const int sa = (int)((asv[si] >> (8 * st)) & 0xffu);
                 const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
-                acc[j] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[j], sa, sb);
+                acc[jl] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[jl], sa, sb);
             }
             if (stp + PD < STEPS)
                 apus_load_b_full<APUS_W_FP4>(cur, wl[(stp + PD) / NSW], sbase + (stp + PD) % NSW);
         }
         apus_v4f accs = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (SH) {
+        if (shg) {
             const int z = r == NP ? -1 : 0;
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
@@ -1329,8 +1336,8 @@ __global__ __launch_bounds__(256) void apus_moe_pair2_kernel(ApusGemmArgs args) 
          * results, and the compiler then sinks the MFMAs into the narrowed-EXEC
          * region, where a matrix instruction does not see the inactive lanes */
 #pragma unroll
-        for (int j = 0; j < NP; ++j) lred[kpart][j][lane] = acc[j][j & 3];
-        if constexpr (SH) lred[kpart][NP][lane] = accs[NP & 3];
+        for (int jl = 0; jl < NPG; ++jl) lred[kpart][jb + jl][lane] = acc[jl][(jb + jl) & 3];
+        if (shg) lred[kpart][NP][lane] = accs[NP & 3];
         __syncthreads();
         if (threadIdx.x < 16) {
             float y = 0.0f;
@@ -1404,8 +1411,11 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
     if (sh && (a->K != 2048 || a->O % 128 || !a->sh_out || !a->add_out ||
                a->npairs != a->acc_s * a->acc_topk))
         return hipErrorInvalidValue;
-    dim3 grid(a->O / 16), block(256);
-#define APUS_P2(NS, NP, SH) hipLaunchKernelGGL((apus_moe_pair2_kernel<NS, NP, SH>), grid, block, 0, st, *a)
+#ifndef APUS_PAIR2_GROUPS
+#define APUS_PAIR2_GROUPS 1
+#endif
+    dim3 grid(a->O / 16), block(256 * APUS_PAIR2_GROUPS);
+#define APUS_P2(NS, NP, SH) hipLaunchKernelGGL((apus_moe_pair2_kernel<NS, NP, SH, APUS_PAIR2_GROUPS>), grid, block, 0, st, *a)
     if (a->K == 4096) {
         if (a->acc_topk == 6) APUS_P2(8, 6, false);
         else                  APUS_P2(8, 8, false);

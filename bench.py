@@ -415,7 +415,8 @@ def bench_moe_sublayer(H, dev, store, layers, s, steps, dim=4096, inter=2048, E=
 
 # ------------------------------------------------------------------ CPU baseline
 
-def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=2048, topk=6):
+def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=2048, topk=6,
+                         unfused=False):
     """Config 4: L MoE layers resident in HBM (256 MXFP4 experts each, config-2
     shapes) plus one FP8 [4096, 4096] projection per layer, ~148 GB. A token
     step runs, per layer, the FP8 linear and the routed dispatch of the
@@ -459,11 +460,21 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
         wsp = dev.alloc(L_.apus_hip_moe_workspace(store, 1, topk))
         per = topk * 4
 
+        wlin = dev.alloc(L_.apus_hip_linear_workspace(1, dim))
+
         def step(t):
             # per layer: the FP8 projection of x and the routed dispatch of x;
-            # the projection rides in the routed w1/w3 launch (2 launches a layer)
+            # the projection rides in the routed w1/w3 launch (2 launches a
+            # layer), or, with unfused, is its own launch (3 a layer)
             for l in range(L):
                 off = (t * L + l) * per
+                if unfused:
+                    H._check(L_.apus_hip_linear_dev(1 | H.W_TILED, wdt.ptr + l * dbytes, wds.ptr + l * dsb,
+                                                    dx.ptr, hd.ptr, 1, dim, dim, wlin.ptr), "fp8 linear")
+                    H._check(L_.apus_hip_moe_routed_dev(store, l, dx.ptr, didx.ptr + off,
+                                                        dwgt.ptr + off, 1, topk, 10.0,
+                                                        y.ptr + l * dim * 4, wsp.ptr), "moe")
+                    continue
                 H._check(L_.apus_hip_moe_routed_dense_dev(store, l, dx.ptr, didx.ptr + off,
                                                           dwgt.ptr + off, 1, topk, 10.0,
                                                           y.ptr + l * dim * 4, wsp.ptr,
@@ -677,6 +688,8 @@ def main():
     ap.add_argument("--only", default="", help="comma list: gemv,fp8,attn,decode,prefill,full,load")
     ap.add_argument("--full-layers", type=int, default=43,
                     help="config 4: resident MoE layers (43 fill ~148 GB)")
+    ap.add_argument("--full-unfused", action="store_true",
+                    help="config 4: the FP8 projection as its own launch (the pre-fusion schedule)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
@@ -755,7 +768,7 @@ def main():
         H.lib().apus_hip_store_free(store)
     if not args.skip_extras and want("full"):
         log("[bench] config 4 full-footprint decode")
-        f = bench_full_footprint(H, dev, L=args.full_layers)
+        f = bench_full_footprint(H, dev, L=args.full_layers, unfused=args.full_unfused)
         extras.update({"config4_tok_s": round(f["tok_s"], 1),
                        "config4_ms_per_token": round(f["ms_per_token"], 3),
                        "config4_GBs": round(f["gbs"], 1),
