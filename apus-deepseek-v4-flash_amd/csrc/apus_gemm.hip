@@ -497,8 +497,14 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
         apus_lds_barrier();           /* the previous chunk's LDS reads are done */
         ApusBFrag<WF> ring[PD];
         if constexpr (ASRC == APUS_A_CODES) {
+            /* weight prefetch ring first: the staging below waits on its
+             * loads through branches (vmcnt 0), so issuing the ring after it
+             * would start the weight stream one or two memory round trips
+             * late (config-0 launch 11.25 -> 11.11 us with the ring first) */
+#pragma unroll
+            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, sbase + u);
             /* stage: row indices, then every code/scale load, then the LDS
-             * writes (no load waits on another load's result more than once) */
+             * writes */
             int ridx[R];
             if (ent.arows) {
 #pragma unroll
@@ -528,26 +534,23 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
                 int ar = ridx[0];
 #pragma unroll
                 for (int t = 1; t < R; ++t) ar = row == t ? ridx[t] : ar;
-                /* only the entry's rows are read; the test is uniform over
-                 * each wave (a row is K16 >= 128 consecutive threads) */
-                if (row < rows) v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);
-                else v[j] = uint4{0u, 0u, 0u, 0u};
+                /* unconditional: rows past the entry's read its last row
+                 * again (ridx is clamped) and are not stored; a load behind
+                 * a branch would make the compiler drain every load in
+                 * flight, one memory round trip per row */
+                v[j] = apus_ld16(args.acodes + (size_t)ar * K + cc * 16);
             }
             constexpr int SPT = (R * NQ + APUS_DEC_NT - 1) / APUS_DEC_NT;   /* scales per thread */
             float scv[SPT];
 #pragma unroll
             for (int k = 0; k < SPT; ++k) {
-                const int si = threadIdx.x + APUS_DEC_NT * k, srr = si / NQ;
+                /* index clamped instead of a guarded load (no branch) */
+                const int si = min(threadIdx.x + APUS_DEC_NT * k, R * NQ - 1), srr = si / NQ;
                 int sar = ridx[0];
 #pragma unroll
                 for (int t = 1; t < R; ++t) sar = srr == t ? ridx[t] : sar;
-                scv[k] = si < R * NQ ? apus_gld<float>(args.ascale + ((size_t)sar * NQ + (si - srr * NQ)))
-                                     : 1.0f;
+                scv[k] = apus_gld<float>(args.ascale + ((size_t)sar * NQ + (si - srr * NQ)));
             }
-            /* weight prefetch ring: issued after the staging loads (so waiting
-             * for those does not wait for these) and before the LDS hand-off */
-#pragma unroll
-            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, sbase + u);
 #pragma unroll
             for (int j = 0; j < STAGE; ++j) {
                 int row, cc;
@@ -1254,12 +1257,50 @@ __global__ __launch_bounds__(256 * G) void apus_moe_pair2_kernel(ApusGemmArgs ar
     }
     for (int t = 0; t < args.acc_s; ++t) {
         const int p0 = t * NP;
+        /* Load order: the token's expert ids (all in flight together), then
+         * the weight ring, then the h rows. Loads behind a branch make the
+         * compiler drain every load in flight, so nothing here is
+         * conditional, and the weight stream starts one memory round trip
+         * after the launch instead of after the h rows and one round trip
+         * per pair. */
+        int ev[NP];
+#pragma unroll
+        for (int j = 0; j < NP; ++j) ev[j] = apus_gld<int>(args.pidx + p0 + j);
+        bool okj[NP];
+#pragma unroll
+        for (int j = 0; j < NP; ++j) okj[j] = (unsigned)ev[j] < (unsigned)args.pE;
+        /* one uniform branch for all pairs (slab arithmetic or pointer
+         * tables), not one per pair */
+        ApusGemmEnt ents[NPG];
+        if (args.pbase) {
+#pragma unroll
+            for (int jl = 0; jl < NPG; ++jl) {
+                const uint8_t *b = args.pbase + (size_t)(okj[jb + jl] ? ev[jb + jl] : 0) * args.pstride;
+                ents[jl].w = b + args.pwoff[0];
+                ents[jl].ws = b + args.psoff[0];
+            }
+        } else {
+#pragma unroll
+            for (int jl = 0; jl < NPG; ++jl) {
+                const int e = okj[jb + jl] ? ev[jb + jl] : 0;
+                ents[jl].w = apus_gld<const uint8_t *>(args.pw[0] + e);
+                ents[jl].ws = apus_gld<const uint8_t *>(args.pws[0] + e);
+            }
+        }
+        ApusWLane wl[NPG];
+#pragma unroll
+        for (int jl = 0; jl < NPG; ++jl) wl[jl] = apus_wlane<APUS_W_FP4>(ents[jl], args.wtiled, o, lane, K);
+        ApusBFrag<APUS_W_FP4> ring[PD];
+#pragma unroll
+        for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl[u / NSW], sbase + u % NSW);
         /* A operands straight from the quantised h rows: lane (r, g) holds
          * row r's codes for its K sub-blocks (pair r, or the shared h as row
-         * NP); an MFMA for pair j masks every row but j */
+         * NP); an MFMA for pair j masks every row but j. Rows that feed no
+         * MFMA read row p0 and get a finite scale (their codes are masked). */
         const bool arow = r < NR;
         const int hr = r < NP ? p0 + r : args.npairs + t;
-        const uint8_t *ab = args.hq + (size_t)(arow ? hr : p0) * K + g * 16;
+        const int hrl = arow ? hr : p0;
+        const uint8_t *ab = args.hq + (size_t)hrl * K + g * 16;
         uint4 av[NSW][4][2];
         unsigned asv[NSW];
 #pragma unroll
@@ -1270,25 +1311,9 @@ __global__ __launch_bounds__(256 * G) void apus_moe_pair2_kernel(ApusGemmArgs ar
                 av[si][st][0] = apus_gld<uint4>(ab + q * 128);
                 av[si][st][1] = apus_gld<uint4>(ab + q * 128 + 64);
             }
-            /* rows that feed no MFMA get a finite scale (their codes are masked) */
-            asv[si] = arow ? apus_gld<unsigned>(args.hqs + (size_t)hr * NQ + (sbase + si) * 4)
-                           : 0x7f7f7f7fu;
+            const unsigned sv = apus_gld<unsigned>(args.hqs + (size_t)hrl * NQ + (sbase + si) * 4);
+            asv[si] = arow ? sv : 0x7f7f7f7fu;
         }
-        ApusWLane wl[NPG];
-        bool okj[NP];
-#pragma unroll
-        for (int j = 0; j < NP; ++j) {
-            const int e = apus_gld<int>(args.pidx + p0 + j);
-            okj[j] = (unsigned)e < (unsigned)args.pE;
-            if (j >= jb && j < jb + NPG) {
-                ApusGemmEnt ent;
-                apus_expert_ptrs(args, 0, okj[j] ? e : 0, ent.w, ent.ws);
-                wl[j - jb] = apus_wlane<APUS_W_FP4>(ent, args.wtiled, o, lane, K);
-            }
-        }
-        ApusBFrag<APUS_W_FP4> ring[PD];
-#pragma unroll
-        for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl[u / NSW], sbase + u % NSW);
         ApusBFrag<APUS_W_FP8> fsh;
         if (shg) apus_load_b_full<APUS_W_FP8>(fsh, wsh, sbase);
         apus_v4f acc[NPG];
