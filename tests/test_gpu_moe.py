@@ -7,9 +7,14 @@ The routed dispatch output y = sum_j wgt * bf16(w2(bf16(swiglu(bf16(w1 x),
 bf16(w3 x))))) contains three BF16 roundings per expert; a GPU fp32 sum that
 differs from the CPU's only in order can land on the other side of a BF16
 rounding boundary, which moves that element by one BF16 ulp (2^-8 relative).
-The bar is therefore max|d|/max|y| <= 2^-7 (two BF16 ulps at the top of the
+The bar here, on the host-pointer hook whose intermediates stay on the
+device, is therefore max|d|/max|y| <= 2^-7 (two BF16 ulps at the top of the
 range), and the batched dispatch must equal per-token dispatches bitwise
 (the reference's own batched == per-token gate, tests/m9b/test_m9b.c:1-20).
+The same kernels run the device entry point, where the per-element stage
+checks of moe_check.py hold every token to the rounding intervals
+(test_gpu_store.py, which also checks the hook equal to the device entry
+point bit for bit, and test_gpu_fullsize.py).
 """
 import numpy as np
 import pytest

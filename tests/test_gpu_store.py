@@ -3,9 +3,10 @@ dispatch (apus_hip_moe_routed_dev).
 
 * Device-generated synthetic weights equal the host twin of the counter
   generator (orc_fill_bytes) byte for byte, so the oracle can rebuild them.
-* apus_hip_moe_routed_dev over the store matches the oracle's routed
-  dispatch (bar 2^-7 as in test_gpu_moe.py) and equals the host-pointer hook
-  bit for bit (same kernels, same data).
+* apus_hip_moe_routed_dev over the store passes the per-element stage
+  checks of moe_check.py on every token (w1/w3 rounding intervals, SwiGLU
+  and act-quant codes, w2 and the (t, j) accumulation, pinned values exact)
+  and equals the host-pointer hook bit for bit (same kernels, same data).
 * store_put / store_get round-trip the six tensors of an expert.
 """
 import ctypes as C
@@ -14,6 +15,7 @@ import numpy as np
 import pytest
 
 from helpers import acts, max_rel, moe_experts, topk_routing
+from moe_check import check_token
 
 pytestmark = pytest.mark.gpu
 
@@ -73,6 +75,22 @@ def host_expert(oracle, seed, layer, e, E, dim, inter):
     return tuple(out)
 
 
+def stage_check(hip, oracle, st, experts_of, x, idx, wgt, y, wsp, inter, tokens=None, limit=10.0):
+    """Per-element checks (moe_check.check_token) of the dispatch that just
+    ran on workspace wsp: the h codes and E8M0 bytes of every pair are read
+    back with apus_hip_moe_routed_h."""
+    L_ = hip.lib()
+    s, topk = idx.shape
+    hc, he = hip.DevBuf(s * topk * inter), hip.DevBuf(s * topk * (inter // 128))
+    hip._check(L_.apus_hip_moe_routed_h(st, s, topk, wsp.ptr, hc.ptr, he.ptr), "routed_h")
+    hcodes = hc.to_array(np.uint8, (s, topk, inter))
+    he8 = he.to_array(np.uint8, (s, topk, inter // 128))
+    for t in (range(s) if tokens is None else tokens):
+        r = check_token(oracle, experts_of, x[t], idx[t], wgt[t], limit, hcodes[t], he8[t], y[t])
+        print(f"token {t}: h pinned {r['h_pinned']:.3f}, y pinned {r['y_pinned']:.3f}, "
+              f"y max_rel {r['y_max_rel']:.3g}", flush=True)
+
+
 def test_store_fill_matches_host_generator(hip, oracle, store):
     L, E, dim, inter = 2, 5, 512, 256
     st = store(L, E, dim, inter)
@@ -128,7 +146,8 @@ def test_moe_routed_dev_over_store(hip, oracle, store, rng, E, dim, inter, s, to
     hip._check(L_.apus_hip_moe_routed_dev(st, layer, dx.ptr, di.ptr, dw.ptr, s, topk, 10.0,
                                           dy.ptr, wsp.ptr), "moe_routed_dev")
     got = dy.to_array(np.float32, (s, dim))
-    assert max_rel(got, want) <= 2.0 ** -7
+    print(f"max_rel {max_rel(got, want):.3g}")
+    stage_check(hip, oracle, st, lambda e: experts[e], x, idx, wgt, got, wsp, inter)
     host = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=777 + E)
     assert np.array_equal(got.view(np.uint32), host.view(np.uint32))
 
@@ -150,7 +169,11 @@ def _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt, seed=9):
     wsp = hip.DevBuf(L_.apus_hip_moe_workspace(st, s, topk))
     hip._check(L_.apus_hip_moe_routed_dev(st, 0, dx.ptr, di.ptr, dw.ptr, s, topk, 10.0,
                                           dy.ptr, wsp.ptr), "moe_routed_dev")
-    return dy.to_array(np.float32, (s, dim)), want
+    got = dy.to_array(np.float32, (s, dim))
+    print(f"max_rel {max_rel(got, want):.3g}")
+    tokens = range(s) if s <= 4 else sorted(set(np.random.default_rng(s).choice(s, 4, replace=False)) | {0})
+    stage_check(hip, oracle, st, lambda e: host[e], x, idx, wgt, got, wsp, inter, tokens)
+    return got, want
 
 
 def test_moe_routed_dev_one_token_full_shape(hip, oracle, store, rng):
@@ -159,8 +182,7 @@ def test_moe_routed_dev_one_token_full_shape(hip, oracle, store, rng):
     E, dim, inter, topk = 256, 4096, 2048, 6
     x = acts(rng, 1, dim)
     idx, wgt = topk_routing(rng, 1, E, topk)
-    got, want = _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
-    assert max_rel(got, want) <= 2.0 ** -7
+    _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
 
 
 def test_moe_routed_dev_skewed_small_batch(hip, oracle, store, rng):
@@ -179,8 +201,7 @@ def test_moe_routed_dev_skewed_small_batch(hip, oracle, store, rng):
     wgt /= wgt.sum(1, keepdims=True)
     counts = np.bincount(idx.ravel(), minlength=E)
     assert counts[0] == 16 and counts[1] >= 12 and counts.mean() < 1
-    got, want = _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
-    assert max_rel(got, want) <= 2.0 ** -7
+    _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
 
 
 def test_moe_routed_dev_duplicate_ids(hip, oracle, store, rng):
@@ -190,8 +211,7 @@ def test_moe_routed_dev_duplicate_ids(hip, oracle, store, rng):
     x = acts(rng, 2, dim)
     idx = np.array([[3, 3, 7, 9, 3, 11], [5, 6, 7, 8, 9, 5]], np.int32)
     wgt = rng.random((2, topk)).astype(np.float32)
-    got, want = _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
-    assert max_rel(got, want) <= 2.0 ** -7
+    _routed_over_store(hip, oracle, store, E, dim, inter, x, idx, wgt)
 
 
 def test_moe_routed_dev_graph_replays(hip, oracle, store, rng):
@@ -215,12 +235,11 @@ def test_moe_routed_dev_graph_replays(hip, oracle, store, rng):
 
     run(di, dw, dy)
     eager = dy.to_array(np.float32, (1, dim)).copy()
-    run(di2, dw2, dy2)
-    eager2 = dy2.to_array(np.float32, (1, dim)).copy()
     used = sorted(set(int(e) for e in idx.ravel()))
     host = {e: host_expert(oracle, seed, 0, e, E, dim, inter) for e in used}
-    want = oracle.moe_routed([host.get(e, host[used[0]]) for e in range(E)], x, idx, wgt, 10.0)
-    assert max_rel(eager, want) <= 2.0 ** -7
+    stage_check(hip, oracle, st, lambda e: host[e], x, idx, wgt, eager, wsp, inter)
+    run(di2, dw2, dy2)
+    eager2 = dy2.to_array(np.float32, (1, dim)).copy()
     hip._check(L_.apus_hip_memset(dy.ptr, 0, dim * 4), "memset")
     hip._check(L_.apus_hip_synchronize(), "sync")
     hip._check(L_.apus_hip_graph_begin(), "graph_begin")
