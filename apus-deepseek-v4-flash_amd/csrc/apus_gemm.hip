@@ -288,6 +288,9 @@ __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args
  * the same per-element steps as the standalone kernels, so the codes are
  * identical.
  */
+#ifndef APUS_TILE_FP
+#define APUS_TILE_FP 1
+#endif
 #ifndef APUS_DEC_WAVES
 #define APUS_DEC_WAVES 4
 #endif
@@ -884,8 +887,13 @@ __global__ __launch_bounds__(64 * NW) void apus_gemm_tile_kernel(ApusGemmArgs ar
     constexpr int BM = 64, BN = 128, LDA = 128 + 16;
     constexpr int K = NQ * 128;
     constexpr size_t RB = WF == APUS_W_FP4 ? K / 2 : K;     /* weight row bytes */
-    __shared__ __align__(16) uint8_t la[2][BM * LDA];
-    __shared__ uint8_t lsa[2][BM];
+    /* FP: three LDS stages, and each step reads the next step's activation
+     * fragments into registers before its own MFMAs, so LDS latency hides
+     * behind the matrix cores instead of following the barrier */
+    constexpr bool FP = APUS_TILE_FP != 0;
+    constexpr int NB = FP ? 3 : 2;
+    __shared__ __align__(16) uint8_t la[NB][BM * LDA];
+    __shared__ uint8_t lsa[NB][BM];
     const ApusGemmEnt ent = args.ents ? apus_gld<ApusGemmEnt>(args.ents + blockIdx.z) : args.ent0;
     const int m0 = blockIdx.y * BM;
     if (m0 >= ent.M) return;
@@ -934,10 +942,10 @@ __global__ __launch_bounds__(64 * NW) void apus_gemm_tile_kernel(ApusGemmArgs ar
         sreg[slot] = apus_gld<float>(ssp + q);    /* unconditional: no branch around a load */
     };
     auto store_a = [&](int q, int slot) {
-        uint8_t *d = la[q & 1] + srow * LDA + spart * SB;
+        uint8_t *d = la[q % NB] + srow * LDA + spart * SB;
 #pragma unroll
         for (int i = 0; i < SB / 16; ++i) *reinterpret_cast<uint4 *>(d + 16 * i) = areg[slot][i];
-        if (spart == 0) lsa[q & 1][srow] = (uint8_t)apus_e8m0_of(sreg[slot]);
+        if (spart == 0) lsa[q % NB][srow] = (uint8_t)apus_e8m0_of(sreg[slot]);
     };
 
     ApusTileB<WF, TN> ring[PD];
@@ -947,6 +955,10 @@ __global__ __launch_bounds__(64 * NW) void apus_gemm_tile_kernel(ApusGemmArgs ar
 #pragma unroll
     for (int u = 0; u < PD; ++u) load_b(ring[u], u);
     store_a(0, 0);
+    if constexpr (FP) {
+        static_assert(!FP || DA >= 2, "two staged groups ahead");
+        if (NQ > 1) store_a(1, 1);
+    }
     apus_lds_barrier();
 
     apus_v4f acc[TM][TN];
@@ -955,12 +967,61 @@ __global__ __launch_bounds__(64 * NW) void apus_gemm_tile_kernel(ApusGemmArgs ar
 #pragma unroll
         for (int i = 0; i < TN; ++i) acc[t][i] = apus_v4f{0.f, 0.f, 0.f, 0.f};
 
+    /* activation fragments of step q: rows wm*32 + 16t + r */
+    struct Frag { apus_v8i a[TM]; int sa[TM]; };
+    auto read_frag = [&](Frag &f, int q) {
+        const uint8_t *ab = la[q % NB];
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            const int row = wm * 32 + t * 16 + r;
+            const uint4 a0 = *reinterpret_cast<const uint4 *>(ab + row * LDA + g * 16);
+            const uint4 a1 = *reinterpret_cast<const uint4 *>(ab + row * LDA + 64 + g * 16);
+            f.a[t] = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                              (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+            f.sa[t] = lsa[q % NB][row];
+        }
+    };
+    if constexpr (FP) {
+        Frag fc, fn;
+        read_frag(fc, 0);
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+            /* activation rows of step q + DA (slot of step q, staged two steps ago) */
+            if (q + DA < NQ) load_a(q + DA, q % DA);
+            if (q + 1 < NQ) read_frag(fn, q + 1);
+            ApusTileB<WF, TN> &cur = ring[q % PD];
+#pragma unroll
+            for (int t = 0; t < TM; ++t) {
+#pragma unroll
+                for (int i = 0; i < TN; ++i) {
+                    if constexpr (WF == APUS_W_FP4) {
+                        const apus_v4u w = cur.w[i][0];
+                        const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                        const int sb = (int)((cur.s[i] >> (8 * g)) & 0xffu);
+                        acc[t][i] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(fc.a[t], b, acc[t][i],
+                                                                                         fc.sa[t], sb);
+                    } else {
+                        const apus_v4u w0 = cur.w[i][0], w1 = cur.w[i][1];
+                        const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                                    (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                        const int sb = (int)((sb8[q >> 2] >> (8 * (q & 3))) & 0xffu);
+                        acc[t][i] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(fc.a[t], b, acc[t][i],
+                                                                                         fc.sa[t], sb);
+                    }
+                }
+            }
+            if (q + PD < NQ) load_b(cur, q + PD);
+            if (q + 2 < NQ) store_a(q + 2, (q + 2) % DA);
+            apus_lds_barrier();
+            fc = fn;
+        }
+    } else
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
         /* activation rows of step q + DA (slot of step q, written last step) */
         if (q + DA < NQ) load_a(q + DA, q % DA);
         ApusTileB<WF, TN> &cur = ring[q % PD];
-        const uint8_t *ab = la[q & 1];
+        const uint8_t *ab = la[q % NB];
 #pragma unroll
         for (int t = 0; t < TM; ++t) {
             const int row = wm * 32 + t * 16 + r;
@@ -968,7 +1029,7 @@ __global__ __launch_bounds__(64 * NW) void apus_gemm_tile_kernel(ApusGemmArgs ar
             const uint4 a1 = *reinterpret_cast<const uint4 *>(ab + row * LDA + 64 + g * 16);
             const apus_v8i a = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
                                         (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-            const int sa = lsa[q & 1][row];
+            const int sa = lsa[q % NB][row];
 #pragma unroll
             for (int i = 0; i < TN; ++i) {
                 if constexpr (WF == APUS_W_FP4) {
