@@ -3,8 +3,9 @@
 apus's hook table `apus_backend_hooks` (c/attn.h:203) lives in the
 reference build (oracle/_ref/libapus_ref.so, compiled from the apus sources
 in place). The test copies the backend's table (apus_hip_hooks(): its first
-three members are ApusBackendHooks, c/backend_metal.h:73-80) into it exactly
-as the enable code in INTEGRATION.md does, then calls the reference's own
+three members are ApusBackendHooks, c/backend_metal.h:73-80) into it as an
+engine's enable path would (c/apus.c:155-166 does the same for Metal), then
+calls the reference's own
 functions:
   apus_fp8_linear  (hook tried first, c/attn.h:408-414)
   apus_bf16_linear (f32_linear hook with R_IN | R_OUT, c/attn.h:621-626)
