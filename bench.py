@@ -7,7 +7,8 @@ grouped-GEMM TFLOP/s @512 tok"):
            E4M3 activations quantised per 128 as apus does. One step = one grouped
            launch of 12 GEMVs (the gate+up GEMVs of one token's 6 routed experts, as
            the decode MoE issues them), each GEMV on its own HBM-resident weight copy
-           (1.1 GB in rotation, so the 256 MB Infinity Cache cannot serve them).
+           (no copy read twice in a run, so the 256 MB Infinity Cache cannot serve
+           them).
            Exactly --steps launches are timed with HIP events on the backend
            stream; the stream is held on the device while the host queues the
            warm-up and the timed launches, so the interval is device time of the
@@ -131,14 +132,18 @@ def timed_eager(H, launch, steps):
 
 # ------------------------------------------------------------------ config 0
 
-def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12, extras=True,
+def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=None, group=12, extras=True,
                    singles=768):
     """Config 0. A step is one grouped launch of `group` M=1 expert GEMVs
-    (W [O, K] MXFP4), each on its own weight copy (256 copies, 1.1 GB in
-    rotation, so no cache level holds them): the decode MoE issues exactly
-    this launch per token and layer (gate+up of the token's 6 routed experts
-    = 12 GEMVs). `steps` launches, queued behind a device-side hold, are timed
-    with HIP events on the backend stream -> `value`.
+    (W [O, K] MXFP4), each on its own weight copy: the decode MoE issues
+    exactly this launch per token and layer (gate+up of the token's 6 routed
+    experts = 12 GEMVs). No copy is read twice in the warm-up and timed
+    launches (group x (steps + warmup + 1) copies, at least 256; 14.5 GB at
+    the default 256 steps), so no cache level can serve the weights: with
+    a 1.1 GB rotation reused every 21 launches the same kernel measured 4-7 %
+    faster, its weights partly held by the 256 MB Infinity Cache. `steps`
+    launches, queued behind a device-side hold, are timed with HIP events on
+    the backend stream -> `value`.
     Extras (single GEMVs, `singles` of them):
       serial  : one launch per GEMV, serialized on one stream;
       lanes   : one launch per GEMV, round-robin on 4 concurrent streams;
@@ -147,6 +152,8 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12, 
     `value` uses the MFMA-tiled layout the backend keeps resident."""
     import ctypes as C
     L = H.lib()
+    if copies is None:
+        copies = max(256, group * (steps + warmup + 1))
     wbytes, sbytes = O * K // 2, O * K // 32
     w = dev.alloc(wbytes * copies)
     ws = dev.alloc(sbytes * copies)
@@ -200,11 +207,14 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=256, group=12, 
         H._check(L.apus_hip_fp4_linear_dev(w.ptr + c * wbytes, ws.ptr + c * sbytes, dx.ptr,
                                            out.ptr + c * O * 4, 1, K, O, ws_lin.ptr), "linear")
 
-    grouped_tiled(0)          # first launch of the kernel (code object set-up), untimed
+    # first launches of the kernels (code object set-up), untimed, on the one
+    # spare window of copies that the timed and warm-up launches do not use
+    spare = steps + warmup
+    grouped_tiled(spare)
     if extras:
         for i in range(warmup):
-            gemv(i)
-            grouped(i)
+            gemv(spare * group + i % group)
+            grouped(spare)
     H.synchronize()
     launches = steps
     # the warm-up steps run right before the timed launches (same launch,
@@ -838,15 +848,16 @@ def main():
         "config": {"workload": "config 0: MXFP4 expert GEMV O=2048 K=4096 M=1; one step = one "
                                f"grouped launch of {g['group']} such GEMVs (gate+up of one token's 6 "
                                "routed experts, as the decode MoE issues them), each on its own "
-                               "HBM-resident weight copy (256 copies, 1.1 GB in rotation); weights "
-                               "in the MFMA-tiled layout the backend's caches and expert store keep",
+                               "HBM-resident weight copy (no copy read twice in the warm-up and "
+                               "timed launches); weights in the MFMA-tiled layout the backend's "
+                               "caches and expert store keep",
                    "group": g["group"], "gemvs_timed": g["gemvs_timed"],
                    "hbm_frac": round(g["tiled_gbs"] / HBM_PEAK_GBS, 4),
                    },
         # the dominant kernel is the grouped GEMM launch; the steps run back
-        # to back in one graph replay (the device holds the stream until the
-        # host has queued the replay), so per-launch time = kernel duration
-        # plus the graph's inter-kernel gap (compare rocprofv3's average)
+        # to back (the device holds the stream until the host has queued
+        # them), so per-launch time = kernel duration plus the inter-kernel
+        # gap (compare rocprofv3's average)
         "roofline": {"bound": "hbm",
                      "achieved": round(g["launch_bytes"] / (g["tiled_launch_us"] * 1e-6) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
