@@ -63,6 +63,13 @@ class Dev:
         self.bufs.append(b)
         return b
 
+    def free(self, *bufs):
+        """Release buffers early (the large weight rotations of one bench)."""
+        self.H.synchronize()
+        for b in bufs:
+            self.bufs.remove(b)
+            b.close()
+
 
 def queue_delay_us(launches):
     """Device-side hold before the timed work: long enough for the host to
@@ -228,6 +235,7 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=None, group=12,
            "tiled_launch_us": ms_tiled / launches * 1e3,
            "tiled_ms_per_step": ms_tiled / launches}
     if not extras:
+        dev.free(w, ws, tw, tws)
         return res
     ms_group = timed_graph(H, grouped, launches)
     steps = singles
@@ -260,13 +268,19 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=None, group=12,
         "linear_gbs": lin_bytes * steps / (ms_lin * 1e-3) / 1e9,
         "linear_us": ms_lin / steps * 1e3,
     })
+    dev.free(w, ws, tw, tws)
     return res
 
 
 # ------------------------------------------------------------------ config 1
 
-def bench_fp8(H, dev, steps, O=4096, K=4096, copies=40):
+def bench_fp8(H, dev, steps, O=4096, K=4096):
+    """Config 1: FP8 [4096, 4096] GEMV (M = 1) and GEMM (M = 512) on
+    MFMA-tiled weights; every timed and warm-up launch reads its own weight
+    copy (steps + 4 copies, 4.4 GB at 256 steps), so each launch streams its
+    16.8 MB from HBM."""
     L = H.lib()
+    copies = steps + 4
     wbytes, sbytes = O * K, (O // 128) * (K // 128)
     w = dev.alloc(wbytes * copies)
     ws = dev.alloc(sbytes * copies)
@@ -277,6 +291,7 @@ def bench_fp8(H, dev, steps, O=4096, K=4096, copies=40):
     for c in range(copies):
         H._check(L.apus_hip_pack_weights_dev(1, w.ptr + c * wbytes, None, tw.ptr + c * wbytes, None,
                                              O, K), "pack w8")
+    dev.free(w)
     w = tw
     res = {}
     for M in (1, 512):
@@ -294,12 +309,13 @@ def bench_fp8(H, dev, steps, O=4096, K=4096, copies=40):
 
         n = steps if M == 1 else max(10, steps // 10)
         for i in range(3):
-            gemm(i)
+            gemm(n + i)            # warm-up on copies the timed launches do not read
         ms = timed_graph(H, gemm, n)
         nbytes = wbytes + sbytes + M * K + M * (K // 128) * 4 + M * O * 4
         t = ms * 1e-3 / n
         res[f"M{M}"] = {"us": t * 1e6, "gbs": nbytes / t / 1e9,
                         "tflops": 2 * M * O * K / t / 1e12}
+    dev.free(w, ws)
     return res
 
 
@@ -310,12 +326,15 @@ def bench_fp8(H, dev, steps, O=4096, K=4096, copies=40):
 ATTN_FP8 = {"wq_a": (1024, 4096), "wq_b": (32768, 1024), "wkv": (512, 4096), "wo_b": (4096, 8192)}
 
 
-def bench_attn_fp8(H, dev, steps=64, M=1, copies=8, tiled=True):
+def bench_attn_fp8(H, dev, steps=64, M=1, tiled=True):
     """One-token FP8 linears at the attention shapes (fp32 x -> BF16 out, act
-    quant fused), MFMA-tiled weights, `copies` distinct weight copies in
-    rotation so each launch streams from HBM."""
+    quant fused), MFMA-tiled weights; every timed and warm-up launch reads
+    its own weight copy (steps + 4 copies), so each launch streams from HBM
+    (with 8 copies in rotation the small shapes, 32 MB and less, would sit
+    in the 256 MB Infinity Cache)."""
     L = H.lib()
     out = {}
+    copies = steps + 4
     for name, (O, K) in ATTN_FP8.items():
         wb, sb = O * K, (O // 128) * (K // 128)
         w = dev.alloc(wb * copies)
@@ -332,30 +351,35 @@ def bench_attn_fp8(H, dev, steps=64, M=1, copies=8, tiled=True):
                                            ws.ptr + c * sb, x.ptr, y.ptr, M, K, O, wl.ptr), "linear")
 
         for i in range(4):
-            step(i)
+            step(steps + i)
         H.synchronize()
         us = timed_graph(H, step, steps) * 1e3 / steps
         out[name] = {"us": us, "GBs": (wb + sb) / us / 1e3}
+        dev.free(w, ws)
     return out
 
 
 def bench_head(H, dev, steps=16, O=129280, K=4096):
     """LM-head GEMV (reference/config.json vocab 129280 x dim 4096, BF16
-    weights, 1.06 GB: far beyond the 256 MB Infinity Cache), one token,
-    FP32 accumulate, through apus_hip_wlinear_dev."""
+    weights, 1.06 GB), one token, FP32 accumulate, through
+    apus_hip_wlinear_dev; every timed launch reads its own copy of the head
+    (steps + 1 copies, 18 GB at 16 steps), so the Infinity Cache holds none
+    of it."""
     L = H.lib()
     wb = O * K * 2
-    w = dev.alloc(wb)
-    H._check(L.apus_hip_fill_random(w.ptr, wb, 5, 7, 1), "fill")   # finite BF16 patterns
+    copies = steps + 1
+    w = dev.alloc(wb * copies)
+    H._check(L.apus_hip_fill_random(w.ptr, wb * copies, 5, 7, 1), "fill")   # finite BF16 patterns
     x = dev.upload(np.random.default_rng(2).standard_normal((1, K)).astype(np.float32))
     y = dev.alloc(O * 4)
 
     def step(i):
-        H._check(L.apus_hip_wlinear_dev(w.ptr, x.ptr, y.ptr, 1, K, O, 4), "head")
+        H._check(L.apus_hip_wlinear_dev(w.ptr + (i % copies) * wb, x.ptr, y.ptr, 1, K, O, 4), "head")
 
-    step(0)
+    step(steps)
     H.synchronize()
     us = timed_graph(H, step, steps) * 1e3 / steps
+    dev.free(w)
     return {"us": us, "GBs": wb / us / 1e3}
 
 
