@@ -174,6 +174,7 @@ SIGNATURES = {
     "apus_hip_graph_replay": (C.c_int, [C.c_int]),
     "apus_hip_last_error": (C.c_char_p, []),
     "apus_hip_device_info": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int)]),
+    "apus_hip_layer1": (C.c_int, [C.c_int, C.POINTER(C.c_uint)]),
     "apus_hip_check_e4m3_hw": (C.c_int, [C.POINTER(C.c_uint), C.POINTER(C.c_uint)]),
     "apus_hip_host_bf16_round": (C.c_float, [C.c_float]),
     "apus_hip_host_e4m3_quant": (C.c_uint8, [C.c_float]),

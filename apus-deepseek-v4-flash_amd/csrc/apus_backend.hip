@@ -96,6 +96,11 @@ struct State {
     /* per-lane counters of the one-token MoE h hand-off (apus_moe_pair13):
      * zeroed once here, every launch leaves them zero */
     unsigned *pair_tk[8] = {};
+    /* grid barrier words of the one-launch one-token layer
+     * (apus_moe_layer1_kernel), which runs on lane 0 only: two of those
+     * launches running at once would each wait for CUs the other holds */
+    unsigned *layer_bar = nullptr;
+    bool layer1 = false, layer1_ok = false;
     std::unordered_map<const void *, DenseW> dense;
     std::unordered_map<uint64_t, ExpertW> experts;
     DevBuf slots[8];          /* grow-only device scratch of the host-pointer calls */
@@ -170,6 +175,19 @@ bool ensure_init() {
     g.lane[0] = g.stream;
     if (!ok(hipEventCreateWithFlags(&g.lane_ev[0], hipEventDisableTiming), "hipEventCreate")) return false;
     if (!alloc_pair_tickets(0)) return false;
+    {
+        void *p = nullptr;
+        const size_t nb = (size_t)apus_moe_layer1_bar_words() * sizeof(unsigned);
+        if (!ok(hipMalloc(&p, nb), "hipMalloc layer barrier") ||
+            !ok(hipMemset(p, 0, nb), "hipMemset layer barrier"))
+            return false;
+        g.layer_bar = (unsigned *)p;
+        /* the one-launch layer needs its 256 workgroups resident together;
+         * APUS_HIP_LAYER1=0 turns it off (two launches per layer) */
+        const char *v = getenv("APUS_HIP_LAYER1");
+        g.layer1_ok = prop.multiProcessorCount >= 256 && apus_moe_layer1_fits() >= 1;
+        g.layer1 = g.layer1_ok && !(v && atoi(v) == 0);
+    }
     if (!ok(hipStreamCreateWithFlags(&g.side, hipStreamNonBlocking), "hipStreamCreate") ||
         !ok(hipEventCreateWithFlags(&g.side_fork, hipEventDisableTiming), "hipEventCreate") ||
         !ok(hipEventCreateWithFlags(&g.side_done, hipEventDisableTiming), "hipEventCreate"))
@@ -683,7 +701,6 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
         }
         a.hq = w.hc; a.hqs = (uint8_t *)w.hs; a.hq_tk = pair_tickets(st);
         if (rd) { a.rdw = rd->w; a.rdws = rd->ws; a.rdout = rd->out; a.rdtiled = rd->tiled; }
-        if (!launched(apus_launch_moe_pair13(&a, nj, st), "pair w1/w3")) return 1;
         ApusGemmArgs b{};
         b.wtiled = wtiled;
         b.O = dim; b.K = inter; b.ldo = dim;
@@ -701,6 +718,13 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
             for (int i = 0; i < 3; i++) { b.shw[i] = shf->w[i]; b.shws[i] = shf->ws[i]; }
             b.sh_tiled = shf->tiled; b.sh_out = shf->sh_out; b.add_out = shf->out;
         }
+        if (g.layer1 && st == g.lane[0] && s == 1 && topk == 6 && dim == 4096 && inter == 2048 &&
+            !shf && !rf) {
+            /* one launch: w1/w3 (+ rider), a grid barrier, w2 */
+            if (add_out && !wait_add()) return 1;
+            return launched(apus_launch_moe_layer1(&a, &b, g.layer_bar, st), "one-token layer") ? 0 : 1;
+        }
+        if (!launched(apus_launch_moe_pair13(&a, nj, st), "pair w1/w3")) return 1;
         if (add_out && !wait_add()) return 1;
         return launched(apus_launch_moe_pair2(&b, st), "pair w2") ? 0 : 1;
     }
@@ -1622,6 +1646,28 @@ int apus_hip_fill_random(void *dst, size_t bytes, uint64_t seed, uint64_t stream
 int apus_hip_synchronize(void) {
     if (!ensure_init()) return 1;
     return finish() ? 0 : 1;
+}
+
+int apus_hip_layer1(int mode, unsigned *faults) {
+    if (!ensure_init()) return -1;
+    if (mode < -1 || mode > 1) { set_err("layer1: mode -1, 0 or 1"); return -1; }
+    if (mode >= 0 && capturing("apus_hip_layer1")) return -1;
+    if (mode == 0) g.layer1 = false;
+    if (mode == 1) g.layer1 = g.layer1_ok;
+    if (faults) {
+        if (capturing("apus_hip_layer1")) return -1;
+        if (!finish()) return -1;
+        if (!ok(hipMemcpy(faults, g.layer_bar + apus_moe_layer1_fault_word(), sizeof(unsigned),
+                          hipMemcpyDeviceToHost),
+                "hipMemcpy layer1 faults"))
+            return -1;
+        /* a workgroup that gave up waiting may have left the counter
+         * behind: start the next launch from zero */
+        if (*faults && !ok(hipMemset(g.layer_bar, 0, (size_t)apus_moe_layer1_bar_words() * sizeof(unsigned)),
+                           "hipMemset layer barrier"))
+            return -1;
+    }
+    return g.layer1 ? 1 : 0;
 }
 
 int apus_hip_timer_start(void) {

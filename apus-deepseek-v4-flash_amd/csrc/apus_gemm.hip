@@ -1516,6 +1516,424 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
     return hipGetLastError();
 }
 
+/*
+ * One-token MoE layer in ONE launch (apus_moe_layer1_kernel): the work of
+ * apus_moe_pair13 (w1/w3 of the 6 routed pairs, optionally a dense FP8
+ * [4096, 4096] linear of the same x riding along) and of apus_moe_pair2 (w2
+ * and y = sum_j wgt * bf16(eo_j)) for dim 4096, inter 2048, topk 6, with a
+ * barrier between the phases instead of a kernel boundary.
+ *
+ * 256 workgroups of 8 waves, one per CU (the launcher checks that 256 fit at
+ * once; a barrier over workgroups that are not all resident would wait for
+ * ever, so the wait is also bounded). Workgroup b:
+ *  - issues the loads of its w2 share first (behind its phase-1 ring): 16
+ *    columns of dim for all 6 pairs, 102 KB, held in registers (wave group
+ *    i takes pairs 3i..3i+2, its 4 waves the K quarters, as apus_moe_pair2
+ *    with G = 2), so those bytes stream while phase 1 runs;
+ *  - phase 1 (b < 192): two pair13 units (32 inter rows of one pair each,
+ *    one per 4-wave half: units 2b and 2b + 1, unit u = pair u / 64, column
+ *    block u % 64), each computed exactly as apus_moe_pair13 with TILES = 2
+ *    (same MFMA chain over K, same h hand-off through the per-group
+ *    counters and quantisation by the group's last unit, which then arrives
+ *    at the barrier); b >= 192 arrive at once;
+ *  - the rider, if any: after arriving, every workgroup streams its 16-row
+ *    tile b of the rider's weight (wave w: K slice w) and multiplies it, so
+ *    these 16.8 MB, which do not depend on h, fill the hand-off and barrier
+ *    latency; out = bf16(sum of the 8 slice chains in order), which may
+ *    differ from the two-launch path's single K chain by fp32 rounding;
+ *  - waits at the barrier (apus_l1_arrive / apus_l1_wait);
+ *  - phase 2: the w2 MFMAs on the registers loaded at the start, the K
+ *    quarters met in LDS, y written (and add_out = bf16(y + add_src)).
+ * y and the h codes are bit-identical to the two-launch path.
+ */
+/* Phase barrier words (device memory, zero when allocated): the arrival
+ * counter (left zero), 8 release words (one per group of workgroups b & 7)
+ * and a fault counter, each 1 KB from the next. */
+#define APUS_L1_COUNT 0
+#define APUS_L1_GEN(i) ((1 + (i)) * 256)
+#define APUS_L1_FAULT (9 * 256)
+#define APUS_L1_BAR_WORDS (10 * 256)
+struct ApusLayerBar {
+    unsigned *w;
+};
+
+
+/* Phase barrier of the one-launch layer. Arrivals: the unit that completes
+ * each of the 96 h groups (after its codes are stored) and every workgroup
+ * without pair units (b >= 192), 160 per launch; the 160th resets the
+ * counter and bumps the 8 release words (one per workgroup group b & 7).
+ * Every workgroup reads its release word at its start, before any of this
+ * launch's arrivals it could be waiting for can have happened (a workgroup
+ * with pair units before its own units finish, the others before they
+ * arrive), and waits for it to move. The release words spread the polling:
+ * one word polled by all 256 workgroups, which the arrivals also hit,
+ * measured 3.4 us slower per launch.
+ * The barrier orders nothing in memory itself (no release / acquire fences:
+ * at device scope those write back and invalidate a whole XCD's L2,
+ * measured at ~3 us per launch here): the data that crosses it (the h
+ * codes) is written with device-coherent stores that have completed
+ * (s_waitcnt) before the writer arrives, and read only after it, by loads
+ * that cannot hit stale cache lines (no workgroup reads those lines before
+ * the barrier in a launch, and a launch starts with invalidated caches). */
+#define APUS_L1_ARRIVALS 160u
+__device__ __forceinline__ void apus_l1_arrive(const ApusLayerBar &bar) {
+    unsigned *cnt = bar.w + APUS_L1_COUNT;
+    if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == APUS_L1_ARRIVALS - 1u) {
+        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (unsigned i = 0; i < 8; ++i)
+            __hip_atomic_fetch_add(bar.w + APUS_L1_GEN(i), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__device__ __forceinline__ void apus_l1_wait(const ApusLayerBar &bar, unsigned g0) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned *genp = bar.w + APUS_L1_GEN(blockIdx.x & 7u);
+        /* bounded: after about a second the fault counter is bumped and the
+         * workgroup goes on (the launch's outputs are then not to be
+         * trusted) */
+        unsigned spins = 0;
+        while (__hip_atomic_load(genp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0) {
+            __builtin_amdgcn_s_sleep(1);
+            if (++spins == (1u << 23)) {
+                __hip_atomic_fetch_add(bar.w + APUS_L1_FAULT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+/* phase-1 MFMA chain of one wave: row 0 of A is x (codes in LDS), the tile's
+ * 16 weight rows stream through `ring` (issued by the caller), as in
+ * apus_pair13_body */
+template <int WF, int NS, int PD>
+__device__ __forceinline__ apus_v4f apus_layer1_chain(ApusBFrag<WF> (&ring)[PD], const ApusWLane &wl,
+                                                      const uint8_t *lcodes, const uint8_t *lsc,
+                                                      int r, int g, int s0) {
+    const int z = r == 0 ? -1 : 0;
+    const uint8_t *arow = lcodes + g * 16;
+    apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+        ApusBFrag<WF> &cur = ring[s % PD];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int q = (s0 + s) * 4 + st;
+            const uint4 a0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
+            const uint4 a1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+            const apus_v8i a = apus_v8i{(int)a0.x & z, (int)a0.y & z, (int)a0.z & z, (int)a0.w & z,
+                                        (int)a1.x & z, (int)a1.y & z, (int)a1.z & z, (int)a1.w & z};
+            if constexpr (WF == APUS_W_FP4) {
+                const apus_v4u w = cur.w[st][0];
+                const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, (int)lsc[q], sb);
+            } else {
+                const apus_v4u w0 = cur.w[st][0], w1 = cur.w[st][1];
+                const apus_v8i b = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                            (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, (int)lsc[q],
+                                                                           (int)cur.s[st]);
+            }
+        }
+        if (s + PD < NS) apus_load_b_full<WF>(cur, wl, s0 + s + PD);
+    }
+    return acc;
+}
+
+/* shared memory of apus_moe_layer1_kernel */
+struct ApusLayer1Lds {
+    uint8_t codes[4096 + 32];
+    uint8_t sc[32];
+    float gu[2][2][2][64];                    /* [half][mat][tile][lane] */
+    float red[4][6][64];                      /* [K quarter][pair][lane] */
+    float rr[8][64];                          /* rider partial sums [wave][lane] */
+    int last[2];
+};
+
+
+/* The workgroup's whole program for one role (ROLE 0: two pair units; 2: no
+ * pair units), so that each role's registers are allocated on their own. */
+template <int ROLE>
+__device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const ApusGemmArgs &a2,
+                                                 const ApusLayerBar &bar, ApusLayer1Lds &L) {
+    constexpr int K1 = 4096, NS1 = 8, O1 = 2048;
+    constexpr int K2 = 2048, NQ2 = 16, NP = 6, NPG = 3, KS = 4, PD1 = 3;
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = wave >> 2, w4 = wave & 3;
+    const int r = lane & 15, g = lane >> 4;
+    const bool rd = a1.rdout != nullptr;
+
+    /* this workgroup's barrier release word, read before anything else
+     * (every lane reads the same word: no branch around the load) */
+    const unsigned g0 = __hip_atomic_load(bar.w + APUS_L1_GEN(blockIdx.x & 7u), __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    /* x row (one token): its loads go out first */
+    ApusStageRaw<APUS_A_F32> raw;
+    apus_stage_load<K1, APUS_A_F32>(a1, nullptr, 0, 0, 1, 0, raw);
+    /* the token's expert ids, all in flight together */
+    int ev[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) ev[j] = apus_gld<int>(a1.pidx + j);
+    bool okj[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) okj[j] = (unsigned)ev[j] < (unsigned)a1.pE;
+    /* the routing weights (inputs of the launch) */
+    float wj[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) wj[j] = apus_gld<float>(a2.acc_w + j);
+
+    /* phase-1 unit of this half (ROLE 0) */
+    const int mat = w4 & 1, tile = w4 >> 1;
+    const int u = 2 * b + half, p = u >> 6, cb = u & 63;
+    const int o1 = cb * 32 + tile * 16 + r;
+    int ep = ev[0];
+#pragma unroll
+    for (int j = 1; j < NP; ++j) ep = p == j ? ev[j] : ep;
+    const bool okp = (unsigned)ep < (unsigned)a1.pE;
+    /* Every weight pointer first (one uniform branch: slab arithmetic or
+     * pointer tables), then the loads: the phase-1 ring, then the w2 share
+     * (wave group `half` takes pairs 3 half .. 3 half + 2, wave w4 the K
+     * quarter w4, one 512-slice each). A load behind a branch, or a wait
+     * for a pointer issued after weight loads, would make the compiler
+     * drain the loads in flight. Weights are MFMA-tiled (the launcher
+     * checks). */
+    const int jb = half * NPG, o2 = b * 16 + r;
+    ApusGemmEnt ent1, ents2[NPG];
+    if (a1.pbase) {
+        if constexpr (ROLE == 0) {
+            const uint8_t *base = a1.pbase + (size_t)(okp ? ep : 0) * a1.pstride;
+            ent1.w = base + (mat ? a1.pwoff[1] : a1.pwoff[0]);
+            ent1.ws = base + (mat ? a1.psoff[1] : a1.psoff[0]);
+        }
+#pragma unroll
+        for (int jl = 0; jl < NPG; ++jl) {
+            const uint8_t *base = a2.pbase + (size_t)(okj[jb + jl] ? ev[jb + jl] : 0) * a2.pstride;
+            ents2[jl].w = base + a2.pwoff[0];
+            ents2[jl].ws = base + a2.psoff[0];
+        }
+    } else {
+        if constexpr (ROLE == 0) {
+            const int e = okp ? ep : 0;
+            ent1.w = apus_gld<const uint8_t *>((mat ? a1.pw[1] : a1.pw[0]) + e);
+            ent1.ws = apus_gld<const uint8_t *>((mat ? a1.pws[1] : a1.pws[0]) + e);
+        }
+#pragma unroll
+        for (int jl = 0; jl < NPG; ++jl) {
+            const int e = okj[jb + jl] ? ev[jb + jl] : 0;
+            ents2[jl].w = apus_gld<const uint8_t *>(a2.pw[0] + e);
+            ents2[jl].ws = apus_gld<const uint8_t *>(a2.pws[0] + e);
+        }
+    }
+    ApusBFrag<APUS_W_FP4> ring1[PD1];
+    ApusWLane wl1{};
+    if constexpr (ROLE == 0) {
+        wl1 = apus_wlane<APUS_W_FP4>(ent1, true, o1, lane, K1);
+#pragma unroll
+        for (int v = 0; v < PD1; ++v) apus_load_b_full<APUS_W_FP4>(ring1[v], wl1, v);
+    }
+    /* keep the w2 loads behind the whole phase-1 ring (loads return in
+     * order: a w2 load ahead of ring slice 1 would delay the chain) */
+    asm volatile("" ::: "memory");
+    ApusBFrag<APUS_W_FP4> ring2[NPG];
+#pragma unroll
+    for (int jl = 0; jl < NPG; ++jl)
+        apus_load_b_full<APUS_W_FP4>(ring2[jl], apus_wlane<APUS_W_FP4>(ents2[jl], true, o2, lane, K2), w4);
+    /* the rider's rows of this workgroup: 16-row tile b of its [4096, 4096]
+     * weight, wave w taking the 512-slice w of K (loaded after the
+     * workgroup's arrival, below) */
+    ApusWLane wlr{};
+    if (rd) {
+        ApusGemmEnt er;
+        er.w = a1.rdw; er.ws = a1.rdws;
+        wlr = apus_wlane<APUS_W_FP8>(er, true, o2, lane, K1);
+    }
+
+    apus_stage_quant<K1, APUS_A_F32>(a1, raw, L.codes, L.sc);
+    apus_lds_barrier();
+    /* ---- phase 1 ---- */
+    if constexpr (ROLE == 0) {
+        const apus_v4f acc = apus_layer1_chain<APUS_W_FP4, NS1, PD1>(ring1, wl1, L.codes, L.sc, r, g, 0);
+        /* every lane stores its element (see apus_pair13_body) */
+        L.gu[half][mat][tile][lane] = apus_bf16_rne(acc[0]);
+        __syncthreads();
+        const int ht = threadIdx.x & 255;            /* thread within the half */
+        float *hdst = a1.pout[0] + (size_t)p * O1;
+        if (ht < 32) {
+            const int t = ht >> 4, rr = ht & 15;
+            const float h = okp ? apus_swiglu_h(L.gu[half][0][t][rr], L.gu[half][1][t][rr], a1.limit) : 0.0f;
+            __hip_atomic_store(hdst + cb * 32 + t * 16 + rr, h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        /* the four units of a 128-column group take tickets; the last
+         * quantises the group (as apus_pair13_body) and arrives */
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        constexpr int G = O1 >> 7;
+        const int gq = cb >> 2;
+        unsigned *tk = a1.hq_tk + (size_t)p * G + gq;
+        if (ht == 0)
+            L.last[half] = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 3u;
+        __syncthreads();
+        if (L.last[half] && ht < 8) {
+            const float *src = hdst + gq * 128 + ht * 16;
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                v[i] = apus_bf16_rne(__hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            float m = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+            m = fmaxf(m, __shfl_xor(m, 1, 64));
+            m = fmaxf(m, __shfl_xor(m, 2, 64));
+            m = fmaxf(m, __shfl_xor(m, 4, 64));
+            const uint32_t e8 = apus_act_scale_exp(m);
+            const float inv = apus_inv_pow2_from_exp(e8);
+            uint32_t q4[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                q4[i] = apus_e4m3_pack4_hw(v[4 * i] * inv, v[4 * i + 1] * inv, v[4 * i + 2] * inv,
+                                           v[4 * i + 3] * inv);
+            /* device-coherent: the w2 phase on other XCDs reads them */
+            unsigned *hw = reinterpret_cast<unsigned *>(a1.hq + (size_t)p * O1 + gq * 128 + ht * 16);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                __hip_atomic_store(hw + i, q4[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (ht == 0) {
+                __hip_atomic_store(a1.hqs + (size_t)p * G + gq, (uint8_t)e8, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* complete before arriving */
+            if (ht == 0) apus_l1_arrive(bar);
+        }
+    } else {
+        /* workgroups without pair units arrive at once */
+        if (threadIdx.x == 0) apus_l1_arrive(bar);
+    }
+    /* The rider (a dense FP8 linear of x, independent of h) streams while
+     * the h hand-off and the barrier run: a workgroup loads its slices only
+     * after every wait that precedes its arrival (a wait counts every load
+     * issued before it; issuing them right after the phase-1 chain instead,
+     * with LDS-only barriers in the hand-off, and at the start in the
+     * workgroups without pair units, measured 5 % slower per layer); the
+     * MFMAs run before the wait. */
+    if (rd) {
+        ApusBFrag<APUS_W_FP8> fr;
+        apus_load_b_full<APUS_W_FP8>(fr, wlr, wave);
+        const int z = r == 0 ? -1 : 0;
+        const uint8_t *arow = L.codes + g * 16;
+        apus_v4f accr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const int q = wave * 4 + st;
+            const uint4 x0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
+            const uint4 x1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+            const apus_v8i a = apus_v8i{(int)x0.x & z, (int)x0.y & z, (int)x0.z & z, (int)x0.w & z,
+                                        (int)x1.x & z, (int)x1.y & z, (int)x1.z & z, (int)x1.w & z};
+            const apus_v4u w0 = fr.w[st][0], w1 = fr.w[st][1];
+            const apus_v8i bb = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                         (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+            accr = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, bb, accr, (int)L.sc[q], (int)fr.s[st]);
+        }
+        L.rr[wave][lane] = accr[0];                   /* lane (g 0, r): weight row 16 b + r */
+    }
+    apus_l1_wait(bar, g0);
+
+    /* ---- phase 2 (as apus_moe_pair2_kernel, G = 2, one token) ---- */
+    /* the h codes and scale bytes (see apus_l1_arrive for why plain
+     * loads see them) */
+    const bool arow = r < NP;
+    const uint8_t *ab = a2.hq + (size_t)(arow ? r : 0) * K2 + g * 16;
+    apus_v8i av[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        const int q = w4 * 4 + st;
+        const uint4 x0 = apus_gld<uint4>(ab + q * 128), x1 = apus_gld<uint4>(ab + q * 128 + 64);
+        av[st] = apus_v8i{(int)x0.x, (int)x0.y, (int)x0.z, (int)x0.w, (int)x1.x, (int)x1.y, (int)x1.z, (int)x1.w};
+    }
+    const unsigned sv = apus_gld<unsigned>(a2.hqs + (size_t)(arow ? r : 0) * NQ2 + w4 * 4);
+    const unsigned asv = arow ? sv : 0x7f7f7f7fu;
+    apus_v4f acc2[NPG];
+#pragma unroll
+    for (int jl = 0; jl < NPG; ++jl) {
+        const int j = jb + jl;
+        const int z = r == j ? -1 : 0;
+        acc2[jl] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const apus_v8i a = av[st] & apus_v8i{z, z, z, z, z, z, z, z};
+            const apus_v4u w = ring2[jl].w[st][0];
+            const apus_v8i bb = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+            const int sa = (int)((asv >> (8 * st)) & 0xffu);
+            const int sb = (int)((ring2[jl].s[st] >> (8 * g)) & 0xffu);
+            acc2[jl] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, bb, acc2[jl], sa, sb);
+        }
+    }
+#pragma unroll
+    for (int jl = 0; jl < NPG; ++jl) L.red[w4][jb + jl][lane] = acc2[jl][(jb + jl) & 3];
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        float y = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            const int src = (j >> 2) * 16 + threadIdx.x;
+            float eo = L.red[0][j][src];
+#pragma unroll
+            for (int kp = 1; kp < KS; ++kp) eo += L.red[kp][j][src];
+            eo = okj[j] ? apus_bf16_rne(eo) : 0.0f;
+            y = __fadd_rn(y, __fmul_rn(wj[j], eo));
+        }
+        const size_t oo = (size_t)b * 16 + threadIdx.x;
+        apus_gst<float>(a2.acc_y + oo, y);
+        if (a2.add_out)
+            apus_gst<float>(a2.add_out + oo, apus_bf16_rne(y + apus_gld<float>(a2.add_src + oo)));
+    } else if (rd && threadIdx.x < 32) {
+        /* the rider's row 16 b + i: bf16 of the 8 K-slice sums in order */
+        const int i = threadIdx.x - 16;
+        float v = L.rr[0][i];
+#pragma unroll
+        for (int w = 1; w < 8; ++w) v += L.rr[w][i];
+        apus_gst<float>(a1.rdout + (size_t)b * 16 + i, apus_bf16_rne(v));
+    }
+}
+
+__global__ __launch_bounds__(512) void apus_moe_layer1_kernel(ApusGemmArgs a1, ApusGemmArgs a2,
+                                                              ApusLayerBar bar) {
+    __shared__ __align__(16) ApusLayer1Lds L;
+    if (blockIdx.x < 192)
+        apus_layer1_role<0>(a1, a2, bar, L);
+    else
+        apus_layer1_role<2>(a1, a2, bar, L);
+}
+
+hipError_t apus_launch_moe_layer1(const ApusGemmArgs *a1, const ApusGemmArgs *a2, unsigned *bar,
+                                  hipStream_t st) {
+    if (a1->K != 4096 || a1->O != 2048 || a1->npairs != 6 || a1->adiv != 6 || a1->acc_s != 1 ||
+        !a1->wtiled || !a2->wtiled || (a1->rdout && !a1->rdtiled) || !a1->pbase != !a2->pbase ||
+        a1->shw[0] || a1->rsp || a1->zero || !a1->hq || !a1->hqs || !a1->hq_tk || !a1->pidx ||
+        a2->K != 2048 || a2->O != 4096 || a2->acc_topk != 6 || a2->acc_s != 1 || a2->shw[1] ||
+        a2->hq != a1->hq || a2->hqs != a1->hqs || a2->pidx != a1->pidx || !bar ||
+        (a1->rdout && (!a1->rdw || !a1->rdws)))
+        return hipErrorInvalidValue;
+    ApusLayerBar b{bar};
+    hipLaunchKernelGGL(apus_moe_layer1_kernel, dim3(256), dim3(512), 0, st, *a1, *a2, b);
+    return hipGetLastError();
+}
+
+int apus_moe_layer1_bar_words() { return APUS_L1_BAR_WORDS; }
+int apus_moe_layer1_fault_word() { return APUS_L1_FAULT; }
+
+int apus_moe_layer1_fits() {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, apus_moe_layer1_kernel, 512, 0) != hipSuccess)
+        return 0;
+    return n;
+}
+
 namespace {
 
 template <int WF, int R, int NS, int KS, int ASRC, bool FOLD = false>

@@ -149,6 +149,23 @@ static inline bool apus_group_k(int K) { return K == 2048 || K == 4096; }
 hipError_t apus_launch_moe_pair13(const ApusGemmArgs *a, int npairs, hipStream_t st);
 hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st);
 
+/* The same one-token dispatch (dim 4096, inter 2048, topk 6, one token, no
+ * shared expert or in-kernel routing; optionally the dense rider of a1) in
+ * ONE launch of 256 workgroups with a grid-wide barrier between the w1/w3
+ * and the w2 phases; a1 / a2 as for apus_launch_moe_pair13 / pair2. bar:
+ * apus_moe_layer1_bar_words() device words, zero before the first launch
+ * and left zero (but for the counter at apus_moe_layer1_fault_word() of
+ * workgroups that gave up waiting at the barrier). Needs all 256
+ * workgroups resident at once: callers check apus_moe_layer1_fits() and the
+ * CU count, and never run two of these launches concurrently. */
+hipError_t apus_launch_moe_layer1(const ApusGemmArgs *a1, const ApusGemmArgs *a2, unsigned *bar,
+                                  hipStream_t st);
+/* workgroups of apus_moe_layer1_kernel that fit on one CU; its barrier
+ * buffer size and fault-counter word */
+int apus_moe_layer1_fits();
+int apus_moe_layer1_bar_words();
+int apus_moe_layer1_fault_word();
+
 /* The few-row schedule for every entry (each entry's M is computed in
  * chunks of up to `rows` rows; rows 1 or 8), with the activation source,
  * pair entries and fused accumulation of ApusGemmArgs. Needs K 2048 or

@@ -520,8 +520,9 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
 
         def step(t):
             # per layer: the FP8 projection of x and the routed dispatch of x;
-            # the projection rides in the routed w1/w3 launch (2 launches a
-            # layer), or, with unfused, is its own launch (3 a layer)
+            # the projection rides in the routed launch (1 launch a layer with
+            # the one-launch layer, else 2: in the w1/w3 launch), or, with
+            # unfused, is its own launch (3 a layer)
             for l in range(L):
                 off = (t * L + l) * per
                 if unfused:
@@ -537,27 +538,43 @@ def bench_full_footprint(H, dev, L=43, tokens=8, reps=3, E=256, dim=4096, inter=
                                                           wdt.ptr + l * dbytes, wds.ptr + l * dsb, 1,
                                                           hd.ptr), "moe + fp8 projection")
 
-        d0 = L_.apus_hip_dispatches()
-        step(0)
-        launches = L_.apus_hip_dispatches() - d0
-        H.synchronize()
-        H._check(L_.apus_hip_graph_begin(), "graph_begin")
-        for t in range(tokens):
-            step(t)
-        H._check(L_.apus_hip_graph_end(), "graph_end")
-        H._check(L_.apus_hip_graph_replay(1), "warm replay")
-        H.synchronize()
-        H._check(L_.apus_hip_timer_start(), "timer")
-        H._check(L_.apus_hip_graph_replay(reps), "replay")
-        ms = L_.apus_hip_timer_stop()
-        n = tokens * reps
-        t_tok = ms * 1e-3 / n
+        def measure():
+            d0 = L_.apus_hip_dispatches()
+            step(0)
+            launches = L_.apus_hip_dispatches() - d0
+            H.synchronize()
+            H._check(L_.apus_hip_graph_begin(), "graph_begin")
+            for t in range(tokens):
+                step(t)
+            H._check(L_.apus_hip_graph_end(), "graph_end")
+            H._check(L_.apus_hip_graph_replay(1), "warm replay")
+            H.synchronize()
+            H._check(L_.apus_hip_timer_start(), "timer")
+            H._check(L_.apus_hip_graph_replay(reps), "replay")
+            ms = L_.apus_hip_timer_stop()
+            return ms * 1e-3 / (tokens * reps), launches
+
+        t_tok, launches = measure()
+        # the same steps with the two-launch layer (w1/w3, then w2), when the
+        # one-launch layer is what ran above
+        t_two = None
+        if not unfused and L_.apus_hip_layer1(-1, None) == 1:
+            L_.apus_hip_layer1(0, None)
+            try:
+                t_two, _ = measure()
+            finally:
+                L_.apus_hip_layer1(1, None)
+        faults = C.c_uint(0)
+        L_.apus_hip_layer1(-1, C.byref(faults))
+        if faults.value:
+            raise RuntimeError(f"config 4: {faults.value} workgroups gave up at the layer barrier")
         expert_bytes = 3 * (inter * dim // 2 + inter * dim // 32)
         tok_bytes = L * (topk * expert_bytes + dbytes + dsb)
         return {"tok_s": 1.0 / t_tok, "ms_per_token": t_tok * 1e3, "layers": L,
                 "resident_GB": (L_.apus_hip_store_bytes(store) + (dbytes + dsb) * L) / 1e9,
                 "bytes_per_token": tok_bytes, "gbs": tok_bytes / t_tok / 1e9,
-                "launches_per_token": launches, "fill_s": fill_s}
+                "launches_per_token": launches, "fill_s": fill_s,
+                "two_launch_tok_s": (1.0 / t_two) if t_two else None}
     finally:
         L_.apus_hip_store_free(store)
 
@@ -832,7 +849,9 @@ def main():
                        "config4_layers": f["layers"],
                        "config4_resident_GB": round(f["resident_GB"], 1),
                        "config4_bytes_per_token": f["bytes_per_token"],
-                       "config4_launches_per_token": f["launches_per_token"]})
+                       "config4_launches_per_token": f["launches_per_token"],
+                       "config4_two_launch_layer_tok_s": (round(f["two_launch_tok_s"], 1)
+                                                          if f["two_launch_tok_s"] else None)})
 
     if not args.skip_extras and want("load"):
         log("[bench] expert slab loader: 64 experts from a page-cached container")

@@ -462,6 +462,17 @@ int   apus_hip_graph_end(void);
 int   apus_hip_graph_replay(int times);
 /* Last error message of this thread ("" when none). */
 const char *apus_hip_last_error(void);
+/* The one-launch one-token MoE layer (dim 4096, inter 2048, top-6, one
+ * token, no fused shared expert or routing: w1/w3, a grid-wide barrier and
+ * w2 in one kernel of 256 resident workgroups, on lane 0; y bit-identical to
+ * the two-launch path). mode 1 turns it on (only where 256 workgroups fit
+ * at once), 0 off (two launches per layer), -1 leaves it; the environment
+ * variable APUS_HIP_LAYER1=0 turns it off at start-up. With faults: waits
+ * for lane 0 and stores the number of workgroups that gave up waiting at the
+ * barrier since the last such read (nonzero: the outputs of some launch are
+ * not to be trusted; the barrier words are then reset). Returns 1 when on, 0 when off, -1 on
+ * error. No counterpart in the reference (a launch-structure switch). */
+int   apus_hip_layer1(int mode, unsigned *faults);
 /* Device name and compute-unit count of the current device. */
 int   apus_hip_device_info(char *name, size_t cap, int *cus);
 

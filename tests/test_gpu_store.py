@@ -291,4 +291,5 @@ def test_routed_with_dense_rider(hip, oracle, store, rng, s):
     truth, esc = oracle.fp8_truth(w8, ws8, c, sc)
     assert bf16_linear_ok(got, truth, 1e-4 * esc).all()
     if s == 1:
-        assert launches == 2, launches        # rider inside the w1/w3 launch
+        # rider inside the w1/w3 launch; one launch in all with the one-launch layer
+        assert launches == (1 if L_.apus_hip_layer1(-1, None) == 1 else 2), launches
