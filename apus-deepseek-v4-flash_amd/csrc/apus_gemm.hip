@@ -704,7 +704,7 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
 #define APUS_PRE_THREADS (64 * APUS_PRE_WAVES)
 
 template <int WF, int NS, int TT, int PD, bool FOLD>
-__global__ __launch_bounds__(APUS_PRE_THREADS, 2) void apus_gemm_prefill_kernel(ApusGemmArgs args) {
+__global__ __launch_bounds__(APUS_PRE_THREADS, APUS_PRE_WAVES >= 16 ? 1 : 2) void apus_gemm_prefill_kernel(ApusGemmArgs args) {
     constexpr int K = NS * 512, NQ = NS * 4;
     /* FOLD: the K-quarter order (four chains from zero over the quarters of
      * K, added left to right) */
