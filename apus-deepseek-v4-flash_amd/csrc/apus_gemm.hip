@@ -853,6 +853,149 @@ __global__ __launch_bounds__(APUS_PRE_THREADS, APUS_PRE_WAVES >= 16 ? 1 : 2) voi
 }
 
 /*
+ * Prefill schedule with the activations resident in LDS (MXFP4, K = 2048,
+ * the K-quarter order: the routed w2 of many-row experts). A workgroup of
+ * 8 waves takes one work item (entry, 64-row chunk), stages the chunk's
+ * whole activation block once (64 rows x 2048 codes, 130 KB of LDS) and
+ * then streams NCB consecutive 128-row column blocks of the weight through
+ * one register ring that runs across the blocks without a barrier: the
+ * activations are read-only after the staging. Against
+ * apus_gemm_prefill_kernel, whose workgroups each restage the chunk for one
+ * column block (as many activation bytes through L2 as weight bytes) and
+ * meet at an LDS barrier every 512-slice, the L2 activation traffic drops
+ * NCB-fold. Each output is the same four K-quarter chains added in order,
+ * so the results are bit-identical to it.
+ */
+#ifndef APUS_PRE_RA_NCB
+#define APUS_PRE_RA_NCB 4
+#endif
+template <int NCB>
+__global__ __launch_bounds__(512, 2) void apus_gemm_prefill_ra_kernel(ApusGemmArgs args) {
+#ifndef APUS_PRE_RA_PD
+#define APUS_PRE_RA_PD 2
+#endif
+    constexpr int K = 2048, NS = 4, NQ = 16, TT = 4, ROWS = 64, PD = APUS_PRE_RA_PD, NW = 8;
+    constexpr int PITCH = K + 32;                 /* bytes per staged row (bank spread) */
+    constexpr int LOADS = ROWS * (K / 16) / (64 * NW);   /* 16-byte staging loads per thread */
+    extern __shared__ __align__(16) uint8_t ra_lds[];
+    uint8_t *la = ra_lds;                          /* [ROWS][PITCH] codes */
+    uint8_t *lsa = ra_lds + ROWS * PITCH;          /* [ROWS][NQ] E8M0 bytes */
+    const int2 it = apus_gld<int2>(args.items + blockIdx.y);
+    if (it.x < 0) return;
+    const ApusGemmEnt ent = apus_gld<ApusGemmEnt>(args.ents + it.x);
+    if (ent.M <= args.m_min || (args.m_max > 0 && ent.M > args.m_max)) return;
+    const int c0 = it.y;
+    const int rows = min(ROWS, ent.M - c0);
+    const int ntile = __builtin_amdgcn_readfirstlane((rows + 15) >> 4);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    auto wlane = [&](int cb) {
+        return apus_wlane<APUS_W_FP4>(ent, args.wtiled, ((blockIdx.x * NCB + cb) * NW + wave) * 16 + r, lane, K);
+    };
+    /* the weight ring first (column block 0, slices 0 and 1) */
+    ApusBFrag<APUS_W_FP4> ring[PD];
+    const ApusWLane wl0 = wlane(0);
+#pragma unroll
+    for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl0, u);
+    /* then the staging loads: thread t takes 16-byte piece (t + 512 j) % 128
+     * of row (t + 512 j) / 128; rows past the chunk repeat its last row */
+    uint4 v[LOADS];
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int i = threadIdx.x + j * 64 * NW;
+        const int rr = min(i >> 7, rows - 1);
+        const int ar = ent.arows ? apus_gld<int>(ent.arows + (c0 + rr)) : ent.a0 + c0 + rr;
+        v[j] = apus_ld16(args.acodes + (size_t)ar * K + (i & 127) * 16);
+    }
+    float sv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int i = threadIdx.x + j * 64 * NW;   /* (row, group) = (i / NQ, i % NQ) */
+        const int rr = min(i / NQ, rows - 1);
+        const int ar = ent.arows ? apus_gld<int>(ent.arows + (c0 + rr)) : ent.a0 + c0 + rr;
+        sv[j] = apus_gld<float>(args.ascale + (size_t)ar * NQ + (i % NQ));
+    }
+    /* the output rows of this lane's accumulator elements (looked up once:
+     * a lookup behind the store's branch would drain the ring) */
+    int orow[TT][4];
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int mm = c0 + min(t * 16 + 4 * g + q, rows - 1);
+            orow[t][q] = ent.orows ? apus_gld<int>(ent.orows + mm) : ent.o0 + mm;
+        }
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+        const int i = threadIdx.x + j * 64 * NW;
+        *reinterpret_cast<uint4 *>(la + (i >> 7) * PITCH + (i & 127) * 16) = v[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) lsa[threadIdx.x + j * 64 * NW] = (uint8_t)apus_e8m0_of(sv[j]);
+    apus_lds_barrier();
+
+    ApusWLane wln = wl0;                           /* stream of the ring's next refill */
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+        apus_v4f acc[TT], tot[TT];
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+            tot[t] = apus_v4f{-0.f, -0.f, -0.f, -0.f};
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int k = cb * NS + s;
+            ApusBFrag<APUS_W_FP4> &cur = ring[k % PD];
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                if (t >= ntile) break;
+                const uint8_t *ap = la + (t * 16 + r) * PITCH + g * 16;
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const int q = s * 4 + st;
+                    const uint4 a0 = *reinterpret_cast<const uint4 *>(ap + q * 128);
+                    const uint4 a1 = *reinterpret_cast<const uint4 *>(ap + q * 128 + 64);
+                    const apus_v8i a = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                                (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                    const int sa = lsa[(t * 16 + r) * NQ + q];
+                    const apus_v4u w = cur.w[st][0];
+                    const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                    const int sbv = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                    acc[t] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[t], sa, sbv);
+                }
+                /* keep the tile's MFMAs here (they touch no memory) */
+                asm volatile("" : "+v"(acc[t]) :: "memory");
+            }
+            /* refill: step k + PD, possibly in the next column block */
+            if (k + PD < NCB * NS) {
+                const int kn = k + PD;
+                if (kn % NS == 0) wln = wlane(kn / NS);
+                apus_load_b_full<APUS_W_FP4>(cur, wln, kn % NS);
+            }
+            /* the K-quarter order: one chain per 512-slice, added in order */
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                tot[t] += acc[t];
+                acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        const int o = ((blockIdx.x * NCB + cb) * NW + wave) * 16 + r;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if (t * 16 + 4 * g + q < rows) {
+                    float val = tot[t][q];
+                    if (args.round_out) val = apus_bf16_rne(val);
+                    apus_gst<float>(ent.out + ((size_t)orow[t][q] * args.ldo + o), val);
+                }
+            }
+        }
+    }
+}
+
+/*
  * Tile schedule (dense GEMMs with more than 8 rows, e.g. a 512-token FP8
  * projection). A workgroup computes 64 rows (tokens) x 128 columns (weight
  * rows) over the whole K, one accumulation chain per output in 128-group
@@ -1994,6 +2137,16 @@ void apus_launch_dec_k(const ApusGemmArgs &d, int n_ent, int ks, hipStream_t st)
  * best once there are enough of them (12 x 2048-row GEMVs: KS 1 10.8 us, KS 2
  * 13.2 us) and small launches need the split (one 4096-row FP8 GEMV: KS 4
  * 6.3 us, KS 1 8.8 us). APUS_HIP_DEC_KS (1, 2, 4) overrides. */
+/* the resident-activation prefill schedule for the routed w2
+ * (APUS_HIP_PRE_RA=0 turns it off) */
+bool apus_pre_ra_on() {
+    static const bool on = [] {
+        const char *e = getenv("APUS_HIP_PRE_RA");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
 int apus_dec_ks(size_t row_tiles) {
     static const int forced = [] {
         const char *e = getenv("APUS_HIP_DEC_KS");
@@ -2108,8 +2261,20 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
 #endif
             constexpr int TT4 = APUS_PREFILL_ROWS / 16;
             if (a->kchain == 4) {
-                if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);
-                else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);
+                if (a->K == 4096) {
+                    hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);
+                } else if (a->items && TT4 == 4 && a->O % (128 * APUS_PRE_RA_NCB) == 0 && apus_pre_ra_on()) {
+                    /* activations resident in LDS, NCB column blocks per workgroup */
+                    constexpr size_t lds = 64 * (2048 + 32) + 64 * 16;
+                    static const hipError_t attr = hipFuncSetAttribute(
+                        reinterpret_cast<const void *>(&apus_gemm_prefill_ra_kernel<APUS_PRE_RA_NCB>),
+                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                    if (attr != hipSuccess) return attr;
+                    dim3 gr(a->O / (128 * APUS_PRE_RA_NCB), n_ent);
+                    hipLaunchKernelGGL((apus_gemm_prefill_ra_kernel<APUS_PRE_RA_NCB>), gr, dim3(512), lds, st, p);
+                } else {
+                    hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);
+                }
             } else {
                 if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4, false>), gp, bp, 0, st, p);
                 else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4, false>), gp, bp, 0, st, p);
