@@ -853,32 +853,39 @@ __global__ __launch_bounds__(APUS_PRE_THREADS, APUS_PRE_WAVES >= 16 ? 1 : 2) voi
 }
 
 /*
- * Prefill schedule with the activations resident in LDS (MXFP4, K = 2048,
- * the K-quarter order: the routed w2 of many-row experts). A workgroup of
- * 8 waves takes one work item (entry, 64-row chunk), stages the chunk's
- * whole activation block once (64 rows x 2048 codes, 130 KB of LDS) and
- * then streams NCB consecutive 128-row column blocks of the weight through
- * one register ring that runs across the blocks without a barrier: the
- * activations are read-only after the staging. Against
- * apus_gemm_prefill_kernel, whose workgroups each restage the chunk for one
+ * Prefill schedule with the activations resident in LDS (MXFP4 routed
+ * experts over many-row work items: w1/w3 at K = 4096, w2 at K = 2048 in the
+ * K-quarter order). A workgroup of 8 waves takes one work item (entry,
+ * 64-row chunk), stages the chunk's activations for K [0, 2048) once (64
+ * rows x 2048 codes, 130 KB of LDS), streams NCB consecutive 128-row column
+ * blocks of the weight over that K range through one register ring that
+ * runs across the blocks without a barrier (the activations are read-only
+ * between stagings), and for K = 4096 then stages K [2048, 4096) and streams
+ * the same blocks again, their accumulators kept in registers. Against
+ * apus_gemm_prefill_kernel, whose workgroups restage the chunk for every
  * column block (as many activation bytes through L2 as weight bytes) and
  * meet at an LDS barrier every 512-slice, the L2 activation traffic drops
- * NCB-fold. Each output is the same four K-quarter chains added in order,
- * so the results are bit-identical to it.
+ * NCB-fold. Every output is the same chain (one over the 128-groups in
+ * order, or four K-quarter chains added in order with FOLD), so the results
+ * are bit-identical to it.
  */
 #ifndef APUS_PRE_RA_NCB
 #define APUS_PRE_RA_NCB 4
 #endif
-template <int NCB>
-__global__ __launch_bounds__(512, 2) void apus_gemm_prefill_ra_kernel(ApusGemmArgs args) {
 #ifndef APUS_PRE_RA_PD
 #define APUS_PRE_RA_PD 2
 #endif
-    constexpr int K = 2048, NS = 4, NQ = 16, TT = 4, ROWS = 64, PD = APUS_PRE_RA_PD, NW = 8;
-    constexpr int PITCH = K + 32;                 /* bytes per staged row (bank spread) */
-    constexpr int LOADS = ROWS * (K / 16) / (64 * NW);   /* 16-byte staging loads per thread */
+template <int NS, bool FOLD, int NCB>
+__global__ __launch_bounds__(512, 2) void apus_gemm_prefill_ra_kernel(ApusGemmArgs args) {
+    constexpr int K = NS * 512, NQ = NS * 4, TT = 4, ROWS = 64, PD = APUS_PRE_RA_PD, NW = 8;
+    constexpr int KP = 2048, NPH = K / KP, SPH = KP / 512;    /* staged K per phase, phases */
+    constexpr int PITCH = KP + 32;                /* bytes per staged row (bank spread) */
+    constexpr int LOADS = ROWS * (KP / 16) / (64 * NW);       /* 16-byte staging loads per thread */
+    constexpr int SCL = ROWS * NQ / (64 * NW);                /* scale loads per thread */
+    constexpr int STEPS = NPH * NCB * SPH;                    /* ring steps (512-slices) */
+    static_assert(K % KP == 0 && (!FOLD || NS == 4) && ROWS * NQ % (64 * NW) == 0, "ra shape");
     extern __shared__ __align__(16) uint8_t ra_lds[];
-    uint8_t *la = ra_lds;                          /* [ROWS][PITCH] codes */
+    uint8_t *la = ra_lds;                          /* [ROWS][PITCH] codes of the phase */
     uint8_t *lsa = ra_lds + ROWS * PITCH;          /* [ROWS][NQ] E8M0 bytes */
     const int2 it = apus_gld<int2>(args.items + blockIdx.y);
     if (it.x < 0) return;
@@ -892,28 +899,46 @@ __global__ __launch_bounds__(512, 2) void apus_gemm_prefill_ra_kernel(ApusGemmAr
     auto wlane = [&](int cb) {
         return apus_wlane<APUS_W_FP4>(ent, args.wtiled, ((blockIdx.x * NCB + cb) * NW + wave) * 16 + r, lane, K);
     };
-    /* the weight ring first (column block 0, slices 0 and 1) */
+    /* ring step k: phase k / (NCB SPH), block (k / SPH) % NCB, K slice
+     * phase * SPH + k % SPH */
+    auto slice_of = [](int k) { return (k / (NCB * SPH)) * SPH + k % SPH; };
+    /* the weight ring first (block 0, the first slices) */
     ApusBFrag<APUS_W_FP4> ring[PD];
-    const ApusWLane wl0 = wlane(0);
+    ApusWLane wln = wlane(0);                      /* stream of the ring's next refill */
 #pragma unroll
-    for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wl0, u);
-    /* then the staging loads: thread t takes 16-byte piece (t + 512 j) % 128
-     * of row (t + 512 j) / 128; rows past the chunk repeat its last row */
-    uint4 v[LOADS];
+    for (int u = 0; u < PD; ++u) apus_load_b_full<APUS_W_FP4>(ring[u], wln, slice_of(u));
+    /* activation row of each staging load and scale load (rows past the
+     * chunk repeat its last row); thread t takes 16-byte piece (t + 512 j) %
+     * 128 of row (t + 512 j) / 128 */
+    int arow[LOADS];
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
-        const int i = threadIdx.x + j * 64 * NW;
-        const int rr = min(i >> 7, rows - 1);
-        const int ar = ent.arows ? apus_gld<int>(ent.arows + (c0 + rr)) : ent.a0 + c0 + rr;
-        v[j] = apus_ld16(args.acodes + (size_t)ar * K + (i & 127) * 16);
+        const int rr = min((threadIdx.x + j * 64 * NW) >> 7, rows - 1);
+        arow[j] = ent.arows ? apus_gld<int>(ent.arows + (c0 + rr)) : ent.a0 + c0 + rr;
     }
-    float sv[2];
+    auto stage = [&](int ph) {
+        uint4 v[LOADS];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int i = threadIdx.x + j * 64 * NW;   /* (row, group) = (i / NQ, i % NQ) */
-        const int rr = min(i / NQ, rows - 1);
-        const int ar = ent.arows ? apus_gld<int>(ent.arows + (c0 + rr)) : ent.a0 + c0 + rr;
-        sv[j] = apus_gld<float>(args.ascale + (size_t)ar * NQ + (i % NQ));
+        for (int j = 0; j < LOADS; ++j)
+            v[j] = apus_ld16(args.acodes + (size_t)arow[j] * K + ph * KP + ((threadIdx.x + j * 64 * NW) & 127) * 16);
+#pragma unroll
+        for (int j = 0; j < LOADS; ++j) {
+            const int i = threadIdx.x + j * 64 * NW;
+            *reinterpret_cast<uint4 *>(la + (i >> 7) * PITCH + (i & 127) * 16) = v[j];
+        }
+    };
+    stage(0);
+    {
+        float sv[SCL];
+#pragma unroll
+        for (int j = 0; j < SCL; ++j) {
+            const int i = threadIdx.x + j * 64 * NW;   /* (row, group) = (i / NQ, i % NQ) */
+            const int rr = min(i / NQ, rows - 1);
+            const int ar = ent.arows ? apus_gld<int>(ent.arows + (c0 + rr)) : ent.a0 + c0 + rr;
+            sv[j] = apus_gld<float>(args.ascale + (size_t)ar * NQ + (i % NQ));
+        }
+#pragma unroll
+        for (int j = 0; j < SCL; ++j) lsa[threadIdx.x + j * 64 * NW] = (uint8_t)apus_e8m0_of(sv[j]);
     }
     /* the output rows of this lane's accumulator elements (looked up once:
      * a lookup behind the store's branch would drain the ring) */
@@ -925,74 +950,102 @@ __global__ __launch_bounds__(512, 2) void apus_gemm_prefill_ra_kernel(ApusGemmAr
             const int mm = c0 + min(t * 16 + 4 * g + q, rows - 1);
             orow[t][q] = ent.orows ? apus_gld<int>(ent.orows + mm) : ent.o0 + mm;
         }
-#pragma unroll
-    for (int j = 0; j < LOADS; ++j) {
-        const int i = threadIdx.x + j * 64 * NW;
-        *reinterpret_cast<uint4 *>(la + (i >> 7) * PITCH + (i & 127) * 16) = v[j];
-    }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) lsa[threadIdx.x + j * 64 * NW] = (uint8_t)apus_e8m0_of(sv[j]);
     apus_lds_barrier();
 
-    ApusWLane wln = wl0;                           /* stream of the ring's next refill */
-#pragma unroll
-    for (int cb = 0; cb < NCB; ++cb) {
-        apus_v4f acc[TT], tot[TT];
-#pragma unroll
-        for (int t = 0; t < TT; ++t) {
-            acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
-            tot[t] = apus_v4f{-0.f, -0.f, -0.f, -0.f};
-        }
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int k = cb * NS + s;
-            ApusBFrag<APUS_W_FP4> &cur = ring[k % PD];
-#pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                if (t >= ntile) break;
-                const uint8_t *ap = la + (t * 16 + r) * PITCH + g * 16;
-#pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    const int q = s * 4 + st;
-                    const uint4 a0 = *reinterpret_cast<const uint4 *>(ap + q * 128);
-                    const uint4 a1 = *reinterpret_cast<const uint4 *>(ap + q * 128 + 64);
-                    const apus_v8i a = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
-                                                (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-                    const int sa = lsa[(t * 16 + r) * NQ + q];
-                    const apus_v4u w = cur.w[st][0];
-                    const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
-                    const int sbv = (int)((cur.s[st] >> (8 * g)) & 0xffu);
-                    acc[t] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[t], sa, sbv);
-                }
-                /* keep the tile's MFMAs here (they touch no memory) */
-                asm volatile("" : "+v"(acc[t]) :: "memory");
-            }
-            /* refill: step k + PD, possibly in the next column block */
-            if (k + PD < NCB * NS) {
-                const int kn = k + PD;
-                if (kn % NS == 0) wln = wlane(kn / NS);
-                apus_load_b_full<APUS_W_FP4>(cur, wln, kn % NS);
-            }
-            /* the K-quarter order: one chain per 512-slice, added in order */
-#pragma unroll
-            for (int t = 0; t < TT; ++t) {
-                tot[t] += acc[t];
-                acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
-            }
-        }
+    /* accumulators of the column blocks (kept across the phases; with one
+     * phase a block's are stored right after it, so only one block's are
+     * live at a time) */
+    apus_v4f acc[NCB][TT], tot[FOLD ? NCB : 1][TT];
+    auto store_block = [&](int cb) {
         const int o = ((blockIdx.x * NCB + cb) * NW + wave) * 16 + r;
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 if (t * 16 + 4 * g + q < rows) {
-                    float val = tot[t][q];
+                    float val = FOLD ? tot[FOLD ? cb : 0][t][q] : acc[cb][t][q];
                     if (args.round_out) val = apus_bf16_rne(val);
                     apus_gst<float>(ent.out + ((size_t)orow[t][q] * args.ldo + o), val);
                 }
             }
         }
+    };
+#pragma unroll
+    for (int ph = 0; ph < NPH; ++ph) {
+        if (ph > 0) {
+            apus_lds_barrier();                    /* every wave is done with the phase before */
+            stage(ph);
+            apus_lds_barrier();
+        }
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            if (ph == 0) {
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    acc[cb][t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (FOLD) tot[cb][t] = apus_v4f{-0.f, -0.f, -0.f, -0.f};
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < SPH; ++s) {
+                const int k = (ph * NCB + cb) * SPH + s;
+                ApusBFrag<APUS_W_FP4> &cur = ring[k % PD];
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    if (t >= ntile) break;
+                    const uint8_t *ap = la + (t * 16 + r) * PITCH + g * 16;
+#pragma unroll
+                    for (int st = 0; st < 4; ++st) {
+                        const int ql = s * 4 + st, q = ph * SPH * 4 + ql;
+                        const uint4 a0 = *reinterpret_cast<const uint4 *>(ap + ql * 128);
+                        const uint4 a1 = *reinterpret_cast<const uint4 *>(ap + ql * 128 + 64);
+                        const apus_v8i a = apus_v8i{(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w,
+                                                    (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
+                        const int sa = lsa[(t * 16 + r) * NQ + q];
+                        const apus_v4u w = cur.w[st][0];
+                        const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                        const int sbv = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                        acc[cb][t] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc[cb][t], sa, sbv);
+                    }
+                    /* keep the tile's MFMAs here (they touch no memory) */
+                    asm volatile("" : "+v"(acc[cb][t]) :: "memory");
+                }
+                /* refill: step k + PD, possibly in the next block or phase */
+                if (k + PD < STEPS) {
+                    const int kn = k + PD;
+                    if (kn % SPH == 0) wln = wlane((kn / SPH) % NCB);
+                    apus_load_b_full<APUS_W_FP4>(cur, wln, slice_of(kn));
+                }
+                if constexpr (FOLD) {
+                    /* the K-quarter order: one chain per 512-slice, added in order */
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) {
+                        tot[cb][t] += acc[cb][t];
+                        acc[cb][t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+                    }
+                }
+            }
+            if (NPH == 1) store_block(cb);
+        }
     }
+    if (NPH > 1) {
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) store_block(cb);
+    }
+}
+
+/* launch the resident-activation schedule (returns false where it does not
+ * apply) */
+template <int NS, bool FOLD>
+bool apus_launch_pre_ra(const ApusGemmArgs &p, int n_ent, hipStream_t st) {
+    constexpr size_t lds = 64 * (2048 + 32) + 64 * (NS * 4);
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&apus_gemm_prefill_ra_kernel<NS, FOLD, APUS_PRE_RA_NCB>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return false;
+    dim3 gr(p.O / (128 * APUS_PRE_RA_NCB), n_ent);
+    hipLaunchKernelGGL((apus_gemm_prefill_ra_kernel<NS, FOLD, APUS_PRE_RA_NCB>), gr, dim3(512), lds, st, p);
+    return true;
 }
 
 /*
@@ -2147,6 +2200,16 @@ bool apus_pre_ra_on() {
     return on;
 }
 
+/* the same for the one-chain launches (the routed w1/w3;
+ * APUS_HIP_PRE_RA13=0 turns it off) */
+bool apus_pre_ra_w13() {
+    static const bool on = [] {
+        const char *e = getenv("APUS_HIP_PRE_RA13");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
 int apus_dec_ks(size_t row_tiles) {
     static const int forced = [] {
         const char *e = getenv("APUS_HIP_DEC_KS");
@@ -2260,21 +2323,18 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
 #define APUS_PRE_PD4 2
 #endif
             constexpr int TT4 = APUS_PREFILL_ROWS / 16;
+            /* activations resident in LDS, NCB column blocks per workgroup
+             * (work-list launches whose column blocks divide evenly) */
+            const bool ra = a->items && TT4 == 4 && a->O % (128 * APUS_PRE_RA_NCB) == 0 && apus_pre_ra_on();
             if (a->kchain == 4) {
                 if (a->K == 4096) {
                     hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);
-                } else if (a->items && TT4 == 4 && a->O % (128 * APUS_PRE_RA_NCB) == 0 && apus_pre_ra_on()) {
-                    /* activations resident in LDS, NCB column blocks per workgroup */
-                    constexpr size_t lds = 64 * (2048 + 32) + 64 * 16;
-                    static const hipError_t attr = hipFuncSetAttribute(
-                        reinterpret_cast<const void *>(&apus_gemm_prefill_ra_kernel<APUS_PRE_RA_NCB>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-                    if (attr != hipSuccess) return attr;
-                    dim3 gr(a->O / (128 * APUS_PRE_RA_NCB), n_ent);
-                    hipLaunchKernelGGL((apus_gemm_prefill_ra_kernel<APUS_PRE_RA_NCB>), gr, dim3(512), lds, st, p);
-                } else {
+                } else if (!(ra && apus_launch_pre_ra<4, true>(p, n_ent, st))) {
                     hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);
                 }
+            } else if (ra && apus_pre_ra_w13()) {
+                if (a->K == 4096) { if (!apus_launch_pre_ra<8, false>(p, n_ent, st)) return hipErrorInvalidValue; }
+                else              { if (!apus_launch_pre_ra<4, false>(p, n_ent, st)) return hipErrorInvalidValue; }
             } else {
                 if (a->K == 4096) hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4, false>), gp, bp, 0, st, p);
                 else              hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 4, TT4, APUS_PRE_PD4, false>), gp, bp, 0, st, p);
