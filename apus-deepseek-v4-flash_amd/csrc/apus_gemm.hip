@@ -295,6 +295,9 @@ __global__ __launch_bounds__(256) void apus_gemm_stream_kernel(ApusGemmArgs args
 #define APUS_DEC_WAVES 4
 #endif
 #define APUS_DEC_NT (64 * APUS_DEC_WAVES)
+#ifndef APUS_DEC_SC_UPFRONT
+#define APUS_DEC_SC_UPFRONT 1
+#endif
 
 /* The weight stream of one lane of a 16-row tile: the address of its
  * 16 bytes of 128-group 0 and the distance between consecutive groups (qs)
@@ -330,8 +333,9 @@ __device__ __forceinline__ ApusWLane apus_wlane(const ApusGemmEnt &ent, bool til
     return l;
 }
 
-/* the four groups of 512-slice s of a lane's weight stream */
-template <int WF>
+/* the four groups of 512-slice s of a lane's weight stream (and, unless
+ * SC is false, the slice's scales) */
+template <int WF, bool SC = true>
 __device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const ApusWLane &l, int s) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -339,7 +343,9 @@ __device__ __forceinline__ void apus_load_b_full(ApusBFrag<WF> &f, const ApusWLa
         f.w[st][0] = apus_ld16_stream(p);
         if constexpr (WF == APUS_W_FP8) f.w[st][1] = apus_ld16_stream(p + (l.qs >> 1));
     }
-    if constexpr (WF == APUS_W_FP4) {
+    if constexpr (!SC) {
+        return;
+    } else if constexpr (WF == APUS_W_FP4) {
         f.s = apus_gld<apus_v4u>(l.s + (size_t)s * l.ss);
     } else {
         const unsigned b4 = apus_gld<unsigned>(l.s + s * 4);
@@ -495,6 +501,16 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
     const ApusWLane wl = apus_wlane<WF>(ent, args.wtiled, o, lane, K);
 
     const int sbase = kpart * NSW;
+    /* FP4: the group-scale bytes of every slice of this wave's stream, one
+     * burst ahead of the weight ring (loaded with each slice instead, as
+     * separate small loads into the scale array, the config-0 launch ran
+     * ~0.3 us slower) */
+    constexpr bool SCU = WF == APUS_W_FP4 && APUS_DEC_SC_UPFRONT;
+    apus_v4u scs[SCU ? NSW : 1];
+    if constexpr (SCU) {
+#pragma unroll
+        for (int si = 0; si < NSW; ++si) scs[si] = apus_gld<apus_v4u>(wl.s + (size_t)(sbase + si) * wl.ss);
+    }
     for (int c0 = 0; active && c0 < ent.M; c0 += R) {
         const int rows = min(R, ent.M - c0);
         apus_lds_barrier();           /* the previous chunk's LDS reads are done */
@@ -505,7 +521,7 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
              * would start the weight stream one or two memory round trips
              * late (config-0 launch 11.25 -> 11.11 us with the ring first) */
 #pragma unroll
-            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, sbase + u);
+            for (int u = 0; u < PD; ++u) apus_load_b_full<WF, !SCU>(ring[u], wl, sbase + u);
             /* stage: row indices, then every code/scale load, then the LDS
              * writes */
             int ridx[R];
@@ -580,7 +596,7 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
             if (pre && c0 == 0) r0 = raw0;
             else apus_stage_load<K, ASRC>(args, ent.arows, ent.a0, c0, rows, 0, r0);
 #pragma unroll
-            for (int u = 0; u < PD; ++u) apus_load_b_full<WF>(ring[u], wl, sbase + u);
+            for (int u = 0; u < PD; ++u) apus_load_b_full<WF, !SCU>(ring[u], wl, sbase + u);
             apus_stage_quant<K, ASRC>(args, r0, lcodes, lsc);
             constexpr int PASSES = (R * NQ + APUS_DEC_NT / 8 - 1) / (APUS_DEC_NT / 8);
 #pragma unroll
@@ -614,7 +630,7 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
                 if constexpr (WF == APUS_W_FP4) {
                     const apus_v4u w = cur.w[st][0];
                     const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
-                    const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                    const int sb = (int)(((SCU ? scs[SCU ? si : 0][st] : cur.s[st]) >> (8 * g)) & 0xffu);
                     acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, sa, sb);
                 } else {
                     const apus_v4u w0 = cur.w[st][0], w1 = cur.w[st][1];
@@ -623,7 +639,7 @@ __global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmA
                     acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, sa, (int)cur.s[st]);
                 }
             }
-            if (si + PD < NSW) apus_load_b_full<WF>(cur, wl, s + PD);
+            if (si + PD < NSW) apus_load_b_full<WF, !SCU>(cur, wl, s + PD);
             if constexpr (FOLD) {
                 if ((si + 1) % QS == 0) {
                     tot += acc;
