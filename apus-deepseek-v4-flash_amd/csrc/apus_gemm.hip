@@ -1820,10 +1820,11 @@ __device__ __forceinline__ void apus_l1_wait(const ApusLayerBar &bar, unsigned g
 /* phase-1 MFMA chain of one wave: row 0 of A is x (codes in LDS), the tile's
  * 16 weight rows stream through `ring` (issued by the caller), as in
  * apus_pair13_body */
-template <int WF, int NS, int PD>
+template <int WF, int NS, int PD, bool SC = true>
 __device__ __forceinline__ apus_v4f apus_layer1_chain(ApusBFrag<WF> (&ring)[PD], const ApusWLane &wl,
                                                       const uint8_t *lcodes, const uint8_t *lsc,
-                                                      int r, int g, int s0) {
+                                                      int r, int g, int s0,
+                                                      const apus_v4u *scs = nullptr) {
     const int z = r == 0 ? -1 : 0;
     const uint8_t *arow = lcodes + g * 16;
     apus_v4f acc = {0.f, 0.f, 0.f, 0.f};
@@ -1840,7 +1841,7 @@ __device__ __forceinline__ apus_v4f apus_layer1_chain(ApusBFrag<WF> (&ring)[PD],
             if constexpr (WF == APUS_W_FP4) {
                 const apus_v4u w = cur.w[st][0];
                 const apus_v8i b = apus_v8i{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
-                const int sb = (int)((cur.s[st] >> (8 * g)) & 0xffu);
+                const int sb = (int)(((SC ? cur.s[st] : scs[s][st]) >> (8 * g)) & 0xffu);
                 acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, (int)lsc[q], sb);
             } else {
                 const apus_v4u w0 = cur.w[st][0], w1 = cur.w[st][1];
@@ -1850,7 +1851,7 @@ __device__ __forceinline__ apus_v4f apus_layer1_chain(ApusBFrag<WF> (&ring)[PD],
                                                                            (int)cur.s[st]);
             }
         }
-        if (s + PD < NS) apus_load_b_full<WF>(cur, wl, s0 + s + PD);
+        if (s + PD < NS) apus_load_b_full<WF, SC>(cur, wl, s0 + s + PD);
     }
     return acc;
 }
@@ -1943,10 +1944,15 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
     }
     ApusBFrag<APUS_W_FP4> ring1[PD1];
     ApusWLane wl1{};
+    /* the group scales of the whole phase-1 stream in one burst ahead of
+     * its ring (as the few-row schedule) */
+    apus_v4u scs1[ROLE == 0 ? NS1 : 1];
     if constexpr (ROLE == 0) {
         wl1 = apus_wlane<APUS_W_FP4>(ent1, true, o1, lane, K1);
 #pragma unroll
-        for (int v = 0; v < PD1; ++v) apus_load_b_full<APUS_W_FP4>(ring1[v], wl1, v);
+        for (int v = 0; v < NS1; ++v) scs1[v] = apus_gld<apus_v4u>(wl1.s + (size_t)v * wl1.ss);
+#pragma unroll
+        for (int v = 0; v < PD1; ++v) apus_load_b_full<APUS_W_FP4, false>(ring1[v], wl1, v);
     }
     /* keep the w2 loads behind the whole phase-1 ring (loads return in
      * order: a w2 load ahead of ring slice 1 would delay the chain) */
@@ -1969,7 +1975,7 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
     apus_lds_barrier();
     /* ---- phase 1 ---- */
     if constexpr (ROLE == 0) {
-        const apus_v4f acc = apus_layer1_chain<APUS_W_FP4, NS1, PD1>(ring1, wl1, L.codes, L.sc, r, g, 0);
+        const apus_v4f acc = apus_layer1_chain<APUS_W_FP4, NS1, PD1, false>(ring1, wl1, L.codes, L.sc, r, g, 0, scs1);
         /* every lane stores its element (see apus_pair13_body) */
         L.gu[half][mat][tile][lane] = apus_bf16_rne(acc[0]);
         __syncthreads();
