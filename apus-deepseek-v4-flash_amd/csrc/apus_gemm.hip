@@ -1746,8 +1746,8 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
  *    one per 4-wave half: units 2b and 2b + 1, unit u = pair u / 64, column
  *    block u % 64), each computed exactly as apus_moe_pair13 with TILES = 2
  *    (same MFMA chain over K, same h hand-off through the per-group
- *    counters and quantisation by the group's last unit, which then arrives
- *    at the barrier); b >= 192 arrive at once;
+ *    counters and quantisation by the group's last unit), then the
+ *    workgroup arrives at the barrier; b >= 192 arrive at once;
  *  - the rider, if any: after arriving, every workgroup streams its 16-row
  *    tile b of the rider's weight (wave w: K slice w) and multiplies it, so
  *    these 16.8 MB, which do not depend on h, fill the hand-off and barrier
@@ -1758,44 +1758,52 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
  *    quarters met in LDS, y written (and add_out = bf16(y + add_src)).
  * y and the h codes are bit-identical to the two-launch path.
  */
-/* Phase barrier words (device memory, zero when allocated): the arrival
- * counter (left zero), 8 release words (one per group of workgroups b & 7)
- * and a fault counter, each 1 KB from the next. */
+/* Phase barrier words (device memory, zero when allocated): the top arrival
+ * counter (left zero), 8 release words (one per group of workgroups b & 7),
+ * a fault counter and 8 group arrival counters (left zero), each 1 KB from
+ * the next. */
 #define APUS_L1_COUNT 0
 #define APUS_L1_GEN(i) ((1 + (i)) * 256)
 #define APUS_L1_FAULT (9 * 256)
-#define APUS_L1_BAR_WORDS (10 * 256)
+#define APUS_L1_GROUP(i) ((10 + (i)) * 256)
+#define APUS_L1_BAR_WORDS (18 * 256)
 struct ApusLayerBar {
     unsigned *w;
 };
 
 
-/* Phase barrier of the one-launch layer. Arrivals: the unit that completes
- * each of the 96 h groups (after its codes are stored) and every workgroup
- * without pair units (b >= 192), 160 per launch; the 160th resets the
- * counter and bumps the 8 release words (one per workgroup group b & 7).
- * Every workgroup reads its release word at its start, before any of this
- * launch's arrivals it could be waiting for can have happened (a workgroup
- * with pair units before its own units finish, the others before they
- * arrive), and waits for it to move. The release words spread the polling:
+/* Phase barrier of the one-launch layer. Every workgroup arrives once, after
+ * its phase-1 duties (its units' h stores and, for the unit that completes
+ * an h group, the group's codes, all complete): first at the counter of its
+ * group b & 7 (32 arrivals), and the last of a group at the top counter (8
+ * arrivals); the 8th top arrival resets it and bumps the 8 release words (one
+ * per group). Same-address atomics serialise: one counter taking every
+ * arrival (the 96 group-completing units and the 64 workgroups without
+ * units) was measured against this two-level count in a microbenchmark of
+ * 256 simultaneous arrivals: release seen after 3.8 against 1.8 us.
+ * Every workgroup reads its release word at its start, before its own
+ * arrival, which the release needs. The release words spread the polling:
  * one word polled by all 256 workgroups, which the arrivals also hit,
  * measured 3.4 us slower per launch.
  * The barrier orders nothing in memory itself (no release / acquire fences:
  * at device scope those write back and invalidate a whole XCD's L2,
  * measured at ~3 us per launch here): the data that crosses it (the h
  * codes) is written with device-coherent stores that have completed
- * (s_waitcnt) before the writer arrives, and read only after it, by loads
- * that cannot hit stale cache lines (no workgroup reads those lines before
- * the barrier in a launch, and a launch starts with invalidated caches). */
-#define APUS_L1_ARRIVALS 160u
+ * (s_waitcnt) before the writer's workgroup arrives, and read only after it,
+ * by loads that cannot hit stale cache lines (no workgroup reads those lines
+ * before the barrier in a launch, and a launch starts with invalidated
+ * caches). */
+#define APUS_L1_WGS 256u
 __device__ __forceinline__ void apus_l1_arrive(const ApusLayerBar &bar) {
+    unsigned *gc = bar.w + APUS_L1_GROUP(blockIdx.x & 7u);
+    if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != APUS_L1_WGS / 8u - 1u) return;
+    __hip_atomic_store(gc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     unsigned *cnt = bar.w + APUS_L1_COUNT;
-    if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == APUS_L1_ARRIVALS - 1u) {
-        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 7u) return;
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
-        for (unsigned i = 0; i < 8; ++i)
-            __hip_atomic_fetch_add(bar.w + APUS_L1_GEN(i), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    for (unsigned i = 0; i < 8; ++i)
+        __hip_atomic_fetch_add(bar.w + APUS_L1_GEN(i), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ void apus_l1_wait(const ApusLayerBar &bar, unsigned g0) {
@@ -2026,8 +2034,11 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
                 __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* complete before arriving */
-            if (ht == 0) apus_l1_arrive(bar);
         }
+        /* both halves' hand-off duties are done (the completers' stores have
+         * completed above): the workgroup arrives once */
+        apus_lds_barrier();
+        if (threadIdx.x == 0) apus_l1_arrive(bar);
     } else {
         /* workgroups without pair units arrive at once */
         if (threadIdx.x == 0) apus_l1_arrive(bar);
@@ -2138,7 +2149,7 @@ hipError_t apus_launch_moe_layer1(const ApusGemmArgs *a1, const ApusGemmArgs *a2
         (a1->rdout && (!a1->rdw || !a1->rdws)))
         return hipErrorInvalidValue;
     ApusLayerBar b{bar};
-    hipLaunchKernelGGL(apus_moe_layer1_kernel, dim3(256), dim3(512), 0, st, *a1, *a2, b);
+    hipLaunchKernelGGL(apus_moe_layer1_kernel, dim3(APUS_L1_WGS), dim3(512), 0, st, *a1, *a2, b);
     return hipGetLastError();
 }
 
