@@ -202,7 +202,7 @@ bool ensure_init() {
 void *scratch_slot(int i, size_t n) {
     DevBuf &b = g.slots[i];
     if (b.n >= n && b.p) return b.p;
-    if (b.p) { hipStreamSynchronize(g.stream); hipFree(b.p); b.p = nullptr; b.n = 0; }
+    if (b.p) { (void)hipStreamSynchronize(g.stream); (void)hipFree(b.p); b.p = nullptr; b.n = 0; }
     size_t want = n < 4096 ? 4096 : n;
     if (!ok(hipMalloc(&b.p, want), "hipMalloc scratch")) return nullptr;
     b.n = want;
@@ -434,10 +434,10 @@ const DenseW *dense_weight(int wfmt, const uint8_t *w, const uint8_t *ws, size_t
     if (!weights_ok(wfmt, w, ws, wbytes, sbytes, "weight upload")) return nullptr;
     DenseW d{ws, nullptr, nullptr, wbytes, sbytes, fp, wfmt, O, K, false};
     if (!ok(hipMalloc(&d.w, wbytes), "hipMalloc weight")) return nullptr;
-    if (!ok(hipMalloc(&d.ws, sbytes), "hipMalloc scales")) { hipFree(d.w); return nullptr; }
+    if (!ok(hipMalloc(&d.ws, sbytes), "hipMalloc scales")) { (void)hipFree(d.w); return nullptr; }
     d.tiled = wfmt <= APUS_W_FP8 && tiled_shape(O, K);
     if (!upload_weights(wfmt, d.w, d.ws, w, ws, wbytes, sbytes, O, K, d.tiled)) {
-        hipFree(d.w); hipFree(d.ws);
+        (void)hipFree(d.w); (void)hipFree(d.ws);
         return nullptr;
     }
     g.bytes_uploaded += wbytes + sbytes;
@@ -845,12 +845,12 @@ int apus_hip_enable(char *err, size_t errcap) {
 void apus_hip_disable(void) {
     std::lock_guard<std::mutex> lk(g_mu);
     if (!g.inited) return;
-    hipStreamSynchronize(g.stream);
-    for (auto &kv : g.dense) { hipFree(kv.second.w); hipFree(kv.second.ws); }
+    (void)hipStreamSynchronize(g.stream);
+    for (auto &kv : g.dense) { (void)hipFree(kv.second.w); (void)hipFree(kv.second.ws); }
     g.dense.clear();
-    for (auto &kv : g.experts) hipFree(kv.second.p[0]);
+    for (auto &kv : g.experts) (void)hipFree(kv.second.p[0]);
     g.experts.clear();
-    for (auto &b : g.slots) { if (b.p) hipFree(b.p); b.p = nullptr; b.n = 0; }
+    for (auto &b : g.slots) { if (b.p) (void)hipFree(b.p); b.p = nullptr; b.n = 0; }
     if (g.pin) (void)hipHostFree(g.pin);
     g.pin = nullptr;
     g.pin_dev = nullptr;
@@ -1067,7 +1067,7 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
                 if (!upload_weights(APUS_W_FP4, ew.p[2 * m], ew.p[2 * m + 1], src[2 * m],
                                     src[2 * m + 1], sz[2 * m], sz[2 * m + 1], mo[m], mk[m],
                                     ew.tiled)) {
-                    hipFree(base);
+                    (void)hipFree(base);
                     return 1;
                 }
             }
@@ -1221,19 +1221,25 @@ ApusHipStore *apus_hip_store_create(int n_layers, int E, int dim, int inter, cha
                           (size_t)inter * dim / 2, (size_t)inter * dim / 32};
     st->expert_bytes = 0;
     for (int i = 0; i < 6; i++) { st->sz[i] = sz[i]; st->expert_bytes += align256(sz[i]); }
+    /* a failed layer frees every layer so far, its own included */
+    auto fail = [&](uint8_t *base, uint8_t **tab) -> ApusHipStore * {
+        if (err && errcap) snprintf(err, errcap, "%s", g_err);
+        if (base) (void)hipFree(base);
+        if (tab) (void)hipFree(tab);
+        for (size_t i = 0; i < st->layer_base.size(); i++) {
+            (void)hipFree(st->layer_base[i]);
+            (void)hipFree(st->layer_tab[i]);
+        }
+        delete st;
+        return nullptr;
+    };
     for (int l = 0; l < n_layers; l++) {
         uint8_t *base = nullptr;
         uint8_t **tab = nullptr;
         if (hipMalloc(&base, st->expert_bytes * E) != hipSuccess ||
             hipMalloc(&tab, 6 * (size_t)E * sizeof(void *)) != hipSuccess) {
             set_err("store_create: HBM exhausted at layer %d", l);
-            if (err && errcap) snprintf(err, errcap, "%s", g_err);
-            if (base) hipFree(base);
-            for (size_t i = 0; i < st->layer_base.size(); i++) {
-                hipFree(st->layer_base[i]); hipFree(st->layer_tab[i]);
-            }
-            delete st;
-            return nullptr;
+            return fail(base, tab);
         }
         std::vector<uint8_t *> h(6 * (size_t)E);
         for (int e = 0; e < E; e++) {
@@ -1243,7 +1249,9 @@ ApusHipStore *apus_hip_store_create(int n_layers, int E, int dim, int inter, cha
                 off += align256(sz[i]);
             }
         }
-        hipMemcpy(tab, h.data(), h.size() * sizeof(void *), hipMemcpyHostToDevice);
+        if (!ok(hipMemcpy(tab, h.data(), h.size() * sizeof(void *), hipMemcpyHostToDevice),
+                "store_create: slab table upload"))
+            return fail(base, tab);
         st->layer_base.push_back(base);
         st->layer_tab.push_back(tab);
     }
@@ -1254,10 +1262,10 @@ ApusHipStore *apus_hip_store_create(int n_layers, int E, int dim, int inter, cha
 void apus_hip_store_free(ApusHipStore *st) {
     if (!st) return;
     std::lock_guard<std::mutex> lk(g_mu);
-    hipStreamSynchronize(g.stream);
+    (void)hipStreamSynchronize(g.stream);
     for (size_t i = 0; i < st->layer_base.size(); i++) {
-        hipFree(st->layer_base[i]);
-        hipFree(st->layer_tab[i]);
+        (void)hipFree(st->layer_base[i]);
+        (void)hipFree(st->layer_tab[i]);
     }
     g.bytes_resident -= st->expert_bytes * st->E * st->L;
     delete st;
