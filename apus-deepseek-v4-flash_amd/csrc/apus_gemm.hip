@@ -2182,7 +2182,13 @@ void apus_launch_dec(const ApusGemmArgs &d, int n_ent, hipStream_t st) {
 #ifndef APUS_DEC_PD_FP4
 #define APUS_DEC_PD_FP4 3
 #endif
-    constexpr int NSW = NS / KS, PDD = WF == APUS_W_FP4 ? APUS_DEC_PD_FP4 : 2;
+/* the K-quarter-order launches (the routed w2, K = 2048: four slices per
+ * wave) run a ring of two: 160 -> fewer VGPRs, 141.5 -> 137.5 us per launch
+ * over configs 2 and 3 (rocprof, same box) */
+#ifndef APUS_DEC_PD_FOLD
+#define APUS_DEC_PD_FOLD 2
+#endif
+    constexpr int NSW = NS / KS, PDD = WF == APUS_W_FP4 ? (FOLD ? APUS_DEC_PD_FOLD : APUS_DEC_PD_FP4) : 2;
     constexpr int PD = PDD < NSW ? PDD : NSW;
     constexpr int K = NS * 512, NQ = NS * 4;
     const size_t lds = (((size_t)R * (K + 32) + (size_t)R * NQ + 15) & ~(size_t)15) +
