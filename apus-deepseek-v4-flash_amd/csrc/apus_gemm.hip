@@ -1893,7 +1893,10 @@ template <int ROLE>
 __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const ApusGemmArgs &a2,
                                                  const ApusLayerBar &bar, ApusLayer1Lds &L) {
     constexpr int K1 = 4096, NS1 = 8, O1 = 2048;
-    constexpr int K2 = 2048, NQ2 = 16, NP = 6, NPG = 3, KS = 4, PD1 = 3;
+#ifndef APUS_L1_PD
+#define APUS_L1_PD 3
+#endif
+    constexpr int K2 = 2048, NQ2 = 16, NP = 6, NPG = 3, KS = 4, PD1 = APUS_L1_PD;
     const int b = blockIdx.x;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
