@@ -11,7 +11,9 @@ fp32 rounding, not bit for bit. The bars:
   tokens are left out of every comparison below); hash routing: equal always;
 * weights: relative 1e-5;
 * routed, shared and final outputs: max |d| / max |ref| <= 2^-6 and
-  mean |d| / mean |ref| <= 2^-9. Each expert is a chain of BF16-rounded
+  mean |d| / mean |ref| <= 2^-9; at the model's shape the routed output of
+  every token is also held per element, stage by stage, to the rounding
+  intervals of moe_check.py, given the device's own expert ids and weights. Each expert is a chain of BF16-rounded
   linears with an E4M3 re-quantisation of h between them: a one-ulp BF16
   difference in g or u (fp32 sums in another order rounding the other way)
   can move an h element to the neighbouring E4M3 code, a 2^-3 relative step
@@ -51,7 +53,7 @@ def _case(rng, E, dim, inter, s, topk, hash_, gate_scale=1.0):
     return cfg, shared, acts(rng, s, dim)
 
 
-def _run_device(hip, st, cfg, shared, x, shared_tiled=False):
+def _run_device(hip, st, cfg, shared, x, shared_tiled=False, ws_out=None):
     L = hip.lib()
     s, dim = x.shape
     E, topk, inter = cfg["E"], cfg["topk"], cfg["inter"]
@@ -85,6 +87,8 @@ def _run_device(hip, st, cfg, shared, x, shared_tiled=False):
     hip._check(L.apus_hip_moe_forward_dev(st, 0, C.byref(ml), dx, dids, s, topk, outs["out"].ptr,
                                           C.byref(im), wsp.ptr), "moe_forward_dev")
     hip._check(L.apus_hip_synchronize(), "sync")
+    if ws_out is not None:
+        ws_out.append(wsp)      # the routed dispatch's workspace is its first part
     f = lambda n, sh, dt=np.float32: outs[n].to_array(dt, sh)  # noqa: E731
     return (f("out", (s, dim)), f("routed", (s, dim)), f("shared", (s, dim)), f("sp", (s, E)),
             f("idx", (s, topk), np.int32), f("wgt", (s, topk)))
@@ -202,8 +206,17 @@ def test_moe_forward_dev_model_shape(hip, oracle, store1, rng, hash_, shared_til
     host = {e: host_expert(oracle, seed, 0, e, E, dim, inter) for e in used}
     experts = [host.get(e, first) for e in range(E)]
     want = oracle.moe_forward(cfg, experts, shared, x)
-    got = _run_device(hip, st, cfg, shared, x, shared_tiled)
+    ws = []
+    got = _run_device(hip, st, cfg, shared, x, shared_tiled, ws)
     _compare(got, want, cfg)
+    # the routed output of every token, near-ties included, per element and
+    # stage by stage against the device's own choice of experts and weights
+    # (the bounds of moe_check.py instead of the 2^-6 output bar)
+    from test_gpu_store import stage_check
+    for e in set(int(v) for v in got[4].ravel()) - set(host):
+        host[e] = host_expert(oracle, seed, 0, e, E, dim, inter)
+    stage_check(hip, oracle, st, lambda e: host[e], x, got[4], got[5], got[1], ws[0], inter,
+                limit=cfg["limit"])
 
 
 def test_moe_forward_dev_graph_replays(hip, oracle, store1, rng):
