@@ -1750,23 +1750,23 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
  * 256 workgroups of 8 waves, one per CU (the launcher checks that 256 fit at
  * once; a barrier over workgroups that are not all resident would wait for
  * ever, so the wait is also bounded). Workgroup b:
- *  - issues the loads of its w2 share first (behind its phase-1 ring): 16
- *    columns of dim for all 6 pairs, 102 KB, held in registers (wave group
- *    i takes pairs 3i..3i+2, its 4 waves the K quarters, as apus_moe_pair2
- *    with G = 2), so those bytes stream while phase 1 runs;
  *  - phase 1 (b < 192): two pair13 units (32 inter rows of one pair each,
  *    one per 4-wave half: units 2b and 2b + 1, unit u = pair u / 64, column
  *    block u % 64), each computed exactly as apus_moe_pair13 with TILES = 2
  *    (same MFMA chain over K, same h hand-off through the per-group
  *    counters and quantisation by the group's last unit), then the
  *    workgroup arrives at the barrier; b >= 192 arrive at once;
- *  - the rider, if any: after arriving, every workgroup streams its 16-row
- *    tile b of the rider's weight (wave w: K slice w) and multiplies it, so
- *    these 16.8 MB, which do not depend on h, fill the hand-off and barrier
- *    latency; out = bf16(sum of the 8 slice chains in order), which may
- *    differ from the two-launch path's single K chain by fp32 rounding;
+ *  - after arriving, issues the loads of its rider slice, if any, then of
+ *    its w2 share: 16 columns of dim for all 6 pairs, 102 KB, held in
+ *    registers (wave group i takes pairs 3i..3i+2, its 4 waves the K
+ *    quarters, as apus_moe_pair2 with G = 2); these bytes stream during the
+ *    hand-off and barrier latency, not in front of the phase-1 refills;
+ *  - the rider, if any: every workgroup multiplies its 16-row tile b of the
+ *    rider's weight (wave w: K slice w), 16.8 MB that do not depend on h;
+ *    out = bf16(sum of the 8 slice chains in order), which may differ from
+ *    the two-launch path's single K chain by fp32 rounding;
  *  - waits at the barrier (apus_l1_arrive / apus_l1_wait);
- *  - phase 2: the w2 MFMAs on the registers loaded at the start, the K
+ *  - phase 2: the w2 MFMAs on the registers loaded at the arrival, the K
  *    quarters met in LDS, y written (and add_out = bf16(y + add_src)).
  * y and the h codes are bit-identical to the two-launch path.
  */
@@ -1932,9 +1932,8 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
     for (int j = 1; j < NP; ++j) ep = p == j ? ev[j] : ep;
     const bool okp = (unsigned)ep < (unsigned)a1.pE;
     /* Every weight pointer first (one uniform branch: slab arithmetic or
-     * pointer tables), then the loads: the phase-1 ring, then the w2 share
-     * (wave group `half` takes pairs 3 half .. 3 half + 2, wave w4 the K
-     * quarter w4, one 512-slice each). A load behind a branch, or a wait
+     * pointer tables), then the phase-1 ring (the w2 share follows the
+     * arrival). A load behind a branch, or a wait
      * for a pointer issued after weight loads, would make the compiler
      * drain the loads in flight. Weights are MFMA-tiled (the launcher
      * checks). */
@@ -1977,13 +1976,7 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
 #pragma unroll
         for (int v = 0; v < PD1; ++v) apus_load_b_full<APUS_W_FP4, false>(ring1[v], wl1, v);
     }
-    /* keep the w2 loads behind the whole phase-1 ring (loads return in
-     * order: a w2 load ahead of ring slice 1 would delay the chain) */
-    asm volatile("" ::: "memory");
     ApusBFrag<APUS_W_FP4> ring2[NPG];
-#pragma unroll
-    for (int jl = 0; jl < NPG; ++jl)
-        apus_load_b_full<APUS_W_FP4>(ring2[jl], apus_wlane<APUS_W_FP4>(ents2[jl], true, o2, lane, K2), w4);
     /* the rider's rows of this workgroup: 16-row tile b of its [4096, 4096]
      * weight, wave w taking the 512-slice w of K (loaded after the
      * workgroup's arrival, below) */
@@ -2065,9 +2058,17 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
      * with LDS-only barriers in the hand-off, and at the start in the
      * workgroups without pair units, measured 5 % slower per layer); the
      * MFMAs run before the wait. */
+    ApusBFrag<APUS_W_FP8> fr;
+    if (rd) apus_load_b_full<APUS_W_FP8>(fr, wlr, wave);
+    /* the w2 share (wave group `half` takes pairs 3 half .. 3 half + 2, wave
+     * w4 the K quarter w4, one 512-slice each), issued after the arrival:
+     * issued with the phase-1 ring, its bytes sat in front of the chain's
+     * refills (loads complete in order) while the hand-off and barrier
+     * window carried only the rider */
+#pragma unroll
+    for (int jl = 0; jl < NPG; ++jl)
+        apus_load_b_full<APUS_W_FP4>(ring2[jl], apus_wlane<APUS_W_FP4>(ents2[jl], true, o2, lane, K2), w4);
     if (rd) {
-        ApusBFrag<APUS_W_FP8> fr;
-        apus_load_b_full<APUS_W_FP8>(fr, wlr, wave);
         const int z = r == 0 ? -1 : 0;
         const uint8_t *arow = L.codes + g * 16;
         apus_v4f accr = {0.f, 0.f, 0.f, 0.f};
