@@ -47,104 +47,149 @@ hipError_t apus_launch_act_quant(const float *x, int ldx, const int32_t *arows,
 
 /* ---------------------------------------------------- SwiGLU + act quant */
 
+/* One 128-column group per 32 lanes (two per wave), 4 columns per lane:
+ * 16-byte loads of g and u, one 4-byte store of codes. */
 __global__ __launch_bounds__(256) void apus_swiglu_quant_kernel(
     const float *__restrict__ gm, const float *__restrict__ um, int M, int N,
     float limit, uint8_t *__restrict__ codes, float *__restrict__ scales) {
     const int nab = N >> 7;
-    const int gid = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (gid >= M * nab) return;
-    const int m = gid / nab, b = gid - m * nab;
-    const size_t off = (size_t)m * N + b * 128 + lane * 2;
-    const float2 gv = *reinterpret_cast<const float2 *>(gm + off);
-    const float2 uv = *reinterpret_cast<const float2 *>(um + off);
-    const float h[2] = {apus_swiglu_h(gv.x, uv.x, limit), apus_swiglu_h(gv.y, uv.y, limit)};
+    const int gid = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int l32 = threadIdx.x & 31;
+    /* both halves of a wave take part in the shuffles: a group past the end
+     * computes on a clamped group and stores nothing */
+    const bool live = gid < M * nab;
+    const int gq = live ? gid : M * nab - 1;
+    const int m = gq / nab, b = gq - m * nab;
+    const size_t off = (size_t)m * N + b * 128 + l32 * 4;
+    const float4 gv = *reinterpret_cast<const float4 *>(gm + off);
+    const float4 uv = *reinterpret_cast<const float4 *>(um + off);
+    const float h[4] = {apus_swiglu_h(gv.x, uv.x, limit), apus_swiglu_h(gv.y, uv.y, limit),
+                        apus_swiglu_h(gv.z, uv.z, limit), apus_swiglu_h(gv.w, uv.w, limit)};
     /* h is bf16-valued, so the act quant's own BF16 round is the identity */
-    const float amax = apus_wave_max(fmaxf(fabsf(h[0]), fabsf(h[1])));
+    float amax = fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3])));
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
     const uint32_t e = apus_act_scale_exp(amax);
     const float inv = apus_inv_pow2_from_exp(e);
-    *reinterpret_cast<uint16_t *>(codes + off) = (uint16_t)apus_e4m3_pack2_hw(h[0] * inv, h[1] * inv);
-    if (lane == 0) scales[(size_t)m * nab + b] = apus_pow2_from_exp(e);
+    if (!live) return;
+    *reinterpret_cast<uint32_t *>(codes + off) =
+        apus_e4m3_pack4_hw(h[0] * inv, h[1] * inv, h[2] * inv, h[3] * inv);
+    if (l32 == 0) scales[(size_t)m * nab + b] = apus_pow2_from_exp(e);
 }
 
 hipError_t apus_launch_swiglu_quant(const float *g, const float *u, int M,
                                     int N, float limit, uint8_t *codes,
                                     float *scales, hipStream_t st) {
     if (M <= 0) return hipSuccess;
+    if (N <= 0 || N % 128) return hipErrorInvalidValue;
     const int groups = M * (N >> 7);
-    hipLaunchKernelGGL(apus_swiglu_quant_kernel, dim3((groups + 3) / 4), dim3(256), 0, st,
+    hipLaunchKernelGGL(apus_swiglu_quant_kernel, dim3((groups + 7) / 8), dim3(256), 0, st,
                        g, u, M, N, limit, codes, scales);
     return hipGetLastError();
 }
 
 /* ------------------------------------------------------------ MoE route */
 
-/* Exclusive prefix sum of one int per thread over the workgroup (at most 16
- * waves); sw is 17 ints of LDS; total receives the sum of all v. */
-__device__ __forceinline__ int apus_block_scan_excl(int v, int *sw, int &total) {
+/* Exclusive prefix sums of three ints per thread over the workgroup (at most
+ * 16 waves) with one set of barriers; sw is 3 x 17 ints of LDS; total
+ * receives the sums of all v. */
+__device__ __forceinline__ int3 apus_block_scan3_excl(int3 v, int *sw, int3 &total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int nw = (blockDim.x + 63) >> 6;
-    int x = v;
+    int3 x = v;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
-        const int y = __shfl_up(x, d, 64);
-        if (lane >= d) x += y;
+        const int a = __shfl_up(x.x, d, 64), b = __shfl_up(x.y, d, 64), c = __shfl_up(x.z, d, 64);
+        if (lane >= d) { x.x += a; x.y += b; x.z += c; }
     }
-    if (lane == 63) sw[wave] = x;
+    if (lane == 63) { sw[wave] = x.x; sw[17 + wave] = x.y; sw[34 + wave] = x.z; }
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (threadIdx.x < 3) {
+        int *q = sw + 17 * threadIdx.x;
         int run = 0;
-        for (int w = 0; w < nw; ++w) { const int t = sw[w]; sw[w] = run; run += t; }
-        sw[16] = run;
+        for (int w = 0; w < nw; ++w) { const int t = q[w]; q[w] = run; run += t; }
+        q[16] = run;
     }
     __syncthreads();
-    const int r = x - v + sw[wave];
-    total = sw[16];
-    __syncthreads();
+    const int3 r = {x.x - v.x + sw[wave], x.y - v.y + sw[17 + wave], x.z - v.z + sw[34 + wave]};
+    total = int3{sw[16], sw[33], sw[50]};
     return r;
 }
 
 /* Single workgroup, one thread per expert (E <= 1024): histogram of expert
- * ids, exclusive scans, placement, entry tables. Experts with 1..small_max
- * pairs are listed (in expert order) at the front of the small tables, the
- * others with pairs at the front of the large tables; the remaining slots
- * get M = 0. Placement order inside an expert is whatever the LDS atomics
- * give: each output row of the grouped GEMMs depends only on its own
- * activation row, and results are written back by pair id, so the order is
- * not observable in the results. */
+ * ids, exclusive scans, placement, entry tables. A pair among the first
+ * APUS_ROUTE_REG per thread keeps its id in a register and its place inside
+ * its expert is the value its histogram atomic returned (the ids are read
+ * once); pairs past that window (nj > APUS_ROUTE_REG x 1024) are counted
+ * after them and placed by a second atomic. Experts with 1..small_max pairs
+ * are listed (in expert order) at the front of the small tables, the others
+ * with pairs at the front of the large tables; the remaining slots get M = 0.
+ * The order inside an expert is whatever the LDS atomics give: each output
+ * row of the grouped GEMMs depends only on its own activation row, and
+ * results are written back by pair id, so the order is not observable in
+ * the results. */
+#define APUS_ROUTE_REG 4
 __global__ __launch_bounds__(1024) void apus_moe_route_kernel(
     const int32_t *__restrict__ idx, int nj, int topk, int E,
     ApusExpertTable tab, float *g, float *u, float *eo,
     int32_t *pair_sorted, int32_t *tok_sorted, ApusGemmEnt *e13s, ApusGemmEnt *e2s,
     ApusGemmEnt *e13l, ApusGemmEnt *e2l, int small_max, int2 *items13, int2 *items2,
     int n_items) {
-    __shared__ int cnt[1024], cur[1024], sw[17];
-    const int e = threadIdx.x;
+    __shared__ int cnt[1024], base[1024], cur[1024], sw[51];
+    const int e = threadIdx.x, nt = blockDim.x;
+    const bool more = nj > APUS_ROUTE_REG * nt;
+    /* this thread's ids and its expert's weight pointers, all in flight together */
+    int qid[APUS_ROUTE_REG];
+#pragma unroll
+    for (int r = 0; r < APUS_ROUTE_REG; ++r) {
+        const int q = e + r * nt;
+        qid[r] = q < nj ? idx[q] : -1;
+    }
+    const int ee = e < E ? e : 0;
+    const uint8_t *pw1 = tab.w1[ee], *pw1s = tab.w1s[ee], *pw3 = tab.w3[ee], *pw3s = tab.w3s[ee],
+                  *pw2 = tab.w2[ee], *pw2s = tab.w2s[ee];
     cnt[e] = 0;
     __syncthreads();
-    for (int q = e; q < nj; q += blockDim.x) {
-        const int id = idx[q];
-        if ((unsigned)id < (unsigned)E) atomicAdd(&cnt[id], 1);
+    int qrank[APUS_ROUTE_REG];
+#pragma unroll
+    for (int r = 0; r < APUS_ROUTE_REG; ++r)
+        qrank[r] = (unsigned)qid[r] < (unsigned)E ? atomicAdd(&cnt[qid[r]], 1) : 0;
+    if (more) {
+        __syncthreads();
+        cur[e] = cnt[e];                                 /* pairs of e in the window */
+        __syncthreads();
+        for (int q = e + APUS_ROUTE_REG * nt; q < nj; q += nt) {
+            const int id = idx[q];
+            if ((unsigned)id < (unsigned)E) atomicAdd(&cnt[id], 1);
+        }
     }
     __syncthreads();
     const int c = e < E ? cnt[e] : 0;
-    int total;
-    const int o0 = apus_block_scan_excl(c, sw, total);
-    cur[e] = o0;
     const int small = c > 0 && c <= small_max, large = c > small_max;
-    int packed_total;
-    const int packed = apus_block_scan_excl(small | (large << 16), sw, packed_total);
-    const int ns = packed_total & 0xffff, nl = packed_total >> 16;
     /* work list of the many-row entries: one item per APUS_PREFILL_ROWS rows */
     const int nchunk = large ? (c + APUS_PREFILL_ROWS - 1) / APUS_PREFILL_ROWS : 0;
-    int total_chunks;
-    const int cbase = apus_block_scan_excl(nchunk, sw, total_chunks);
-    for (int q = e; q < nj; q += blockDim.x) {
-        const int id = idx[q];
-        if ((unsigned)id >= (unsigned)E) continue;      /* ids outside [0, E) are dropped */
-        const int pos = atomicAdd(&cur[id], 1);
+    int3 tot;
+    const int3 sc = apus_block_scan3_excl(int3{c, small | (large << 16), nchunk}, sw, tot);
+    const int o0 = sc.x, packed = sc.y, cbase = sc.z;
+    const int ns = tot.y & 0xffff, nl = tot.y >> 16, total_chunks = tot.z;
+    base[e] = o0;
+    if (more) cur[e] += o0;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < APUS_ROUTE_REG; ++r) {
+        if ((unsigned)qid[r] >= (unsigned)E) continue;  /* ids outside [0, E) are dropped */
+        const int q = e + r * nt, pos = base[qid[r]] + qrank[r];
         pair_sorted[pos] = q;
         tok_sorted[pos] = q / topk;
+    }
+    if (more) {
+        for (int q = e + APUS_ROUTE_REG * nt; q < nj; q += nt) {
+            const int id = idx[q];
+            if ((unsigned)id >= (unsigned)E) continue;
+            const int pos = atomicAdd(&cur[id], 1);
+            pair_sorted[pos] = q;
+            tok_sorted[pos] = q / topk;
+        }
     }
     if (items2) {
         for (int i = total_chunks + threadIdx.x; i < n_items; i += blockDim.x) {
@@ -157,14 +202,14 @@ __global__ __launch_bounds__(1024) void apus_moe_route_kernel(
     ApusGemmEnt a;
     a.arows = tok_sorted + o0; a.orows = nullptr; a.a0 = 0; a.o0 = o0; a.M = c; a.pad = 0;
     ApusGemmEnt b;
-    b.w = tab.w2[e]; b.ws = tab.w2s[e]; b.out = eo;
+    b.w = pw2; b.ws = pw2s; b.out = eo;
     b.arows = nullptr; b.orows = pair_sorted + o0; b.a0 = o0; b.o0 = 0; b.M = c; b.pad = 0;
     if (small | large) {
         const int slot = small ? (packed & 0xffff) : (packed >> 16);
         ApusGemmEnt *t13 = small ? e13s : e13l;
-        a.w = tab.w1[e]; a.ws = tab.w1s[e]; a.out = g;
+        a.w = pw1; a.ws = pw1s; a.out = g;
         t13[2 * slot] = a;
-        a.w = tab.w3[e]; a.ws = tab.w3s[e]; a.out = u;
+        a.w = pw3; a.ws = pw3s; a.out = u;
         t13[2 * slot + 1] = a;
         (small ? e2s : e2l)[slot] = b;
     }
@@ -180,7 +225,6 @@ __global__ __launch_bounds__(1024) void apus_moe_route_kernel(
             items13[2 * (cbase + k) + 1] = int2{2 * slot + 1, c0};
         }
     }
-    (void)total;
 }
 
 hipError_t apus_launch_moe_route(const int32_t *idx, int nj, int topk, int E,
@@ -330,10 +374,44 @@ __global__ __launch_bounds__(256) void apus_moe_accum_kernel(
     (void)s;
 }
 
+/* The same sums, 4 columns per thread (16-byte loads and stores; dim % 4 == 0). */
+__global__ __launch_bounds__(256) void apus_moe_accum4_kernel(
+    const float *__restrict__ eo, const float *__restrict__ wgt, int topk, int dim,
+    float *__restrict__ y, const float *__restrict__ add_src, float *__restrict__ add_out) {
+    const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
+    const int t = blockIdx.y;
+    if (i >= dim) return;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < topk; ++j) {
+        const float w = wgt[t * topk + j];
+        const float4 v = *reinterpret_cast<const float4 *>(eo + (size_t)(t * topk + j) * dim + i);
+        acc[0] = __fadd_rn(acc[0], __fmul_rn(w, v.x));
+        acc[1] = __fadd_rn(acc[1], __fmul_rn(w, v.y));
+        acc[2] = __fadd_rn(acc[2], __fmul_rn(w, v.z));
+        acc[3] = __fadd_rn(acc[3], __fmul_rn(w, v.w));
+    }
+    const size_t o = (size_t)t * dim + i;
+    *reinterpret_cast<float4 *>(y + o) = float4{acc[0], acc[1], acc[2], acc[3]};
+    if (add_out) {
+        const float4 a = *reinterpret_cast<const float4 *>(add_src + o);
+        *reinterpret_cast<float4 *>(add_out + o) =
+            float4{apus_bf16_rne(acc[0] + a.x), apus_bf16_rne(acc[1] + a.y),
+                   apus_bf16_rne(acc[2] + a.z), apus_bf16_rne(acc[3] + a.w)};
+    }
+}
+
 hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,
                                  int topk, int dim, float *y, const float *add_src,
                                  float *add_out, hipStream_t st) {
     if (s <= 0) return hipSuccess;
+    const bool al = ((reinterpret_cast<uintptr_t>(eo) | reinterpret_cast<uintptr_t>(y) |
+                      reinterpret_cast<uintptr_t>(add_src) | reinterpret_cast<uintptr_t>(add_out)) &
+                     15) == 0;
+    if (dim % 4 == 0 && al) {
+        hipLaunchKernelGGL(apus_moe_accum4_kernel, dim3((dim / 4 + 255) / 256, s), dim3(256), 0, st,
+                           eo, wgt, topk, dim, y, add_src, add_out);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(apus_moe_accum_kernel, dim3((dim + 255) / 256, s), dim3(256), 0, st,
                        eo, wgt, s, topk, dim, y, add_src, add_out);
     return hipGetLastError();

@@ -194,3 +194,25 @@ def test_moe_routed_same_layer_id_other_shape(hip, oracle, rng):
         want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
         got = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=4242)
         assert max_rel(got, want) <= 2.0 ** -7, (dim, inter)
+
+
+def test_moe_routed_many_pairs(hip, oracle, rng):
+    """More pairs than the route kernel keeps in registers (4 per thread of
+    1024): the pairs past that window are placed by a second pass. Every
+    expert takes the many-row schedule in both runs, and each output row
+    depends only on its own token, so the 800-token dispatch must equal two
+    400-token dispatches (register window only) bit for bit."""
+    E, dim, inter, s, topk = 16, 256, 256, 800, 6
+    experts = moe_experts(rng, E, dim, inter)
+    x = acts(rng, s, dim)
+    idx, wgt = topk_routing(rng, s, E, topk)
+    assert s * topk > 4096
+    counts = [np.bincount(idx[h:h + 400].ravel(), minlength=E) for h in (0, 400)]
+    assert min(c.min() for c in counts) > 8
+    full = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=4242)
+    for h in (0, 400):
+        part = hip.moe_routed(experts, x[h:h + 400], idx[h:h + 400], wgt[h:h + 400], 10.0,
+                              layer_id=4242)
+        assert np.array_equal(part.view(np.uint32), full[h:h + 400].view(np.uint32)), h
+    want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
+    assert max_rel(full, want) <= 2.0 ** -7
