@@ -1,11 +1,12 @@
 /*
  * apus_kernels.hip — gfx950 kernels of the HIP backend.
  *
- *  - act quant: BF16 round + per-128 E4M3 quantisation, one wave per
- *    128-element group (c/attn.h:393-403, c/fp4.h:293-321), bit-exact.
+ *  - act quant: BF16 round + per-128 E4M3 quantisation, 32 lanes (or one
+ *    wave where x is not 16-byte aligned) per 128-element group
+ *    (c/attn.h:393-403, c/fp4.h:293-321), bit-exact.
  *  (the block-scaled GEMMs live in apus_gemm.hip)
  *  - SwiGLU + act quant of h (c/moe.h:113-126 followed by the act quant of
- *    the w2 input, c/moe.h:309-314), one wave per 128 group.
+ *    the w2 input, c/moe.h:309-314), 32 lanes per 128 group.
  *  - routed-pair counting sort and GEMM entry tables (c/moe.h:465-474).
  *  - (t, j)-ordered weighted accumulation (c/moe.h:148-158).
  *  - counter-based weight fill for HBM-resident synthetic experts.
@@ -35,11 +36,44 @@ __global__ __launch_bounds__(256) void apus_act_quant_kernel(
     if (lane == 0) scales[(size_t)m * nab + b] = apus_pow2_from_exp(e);
 }
 
+/* The same, 32 lanes per group, 4 elements per lane (x rows 16-byte aligned). */
+__global__ __launch_bounds__(256) void apus_act_quant4_kernel(
+    const float *__restrict__ x, int ldx, const int32_t *__restrict__ arows,
+    int M, int K, uint8_t *__restrict__ codes, float *__restrict__ scales) {
+    const int nab = K >> 7;
+    const int gid = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int l32 = threadIdx.x & 31;
+    /* both halves of a wave take part in the shuffles: a group past the end
+     * computes on a clamped group and stores nothing */
+    const bool live = gid < M * nab;
+    const int gq = live ? gid : M * nab - 1;
+    const int m = gq / nab, b = gq - m * nab;
+    const int src = arows ? arows[m] : m;
+    const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)src * ldx + b * 128 + l32 * 4);
+    const float h[4] = {apus_bf16_rne(v.x), apus_bf16_rne(v.y), apus_bf16_rne(v.z),
+                        apus_bf16_rne(v.w)};
+    float amax = fmaxf(fmaxf(fabsf(h[0]), fabsf(h[1])), fmaxf(fabsf(h[2]), fabsf(h[3])));
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const uint32_t e = apus_act_scale_exp(amax);
+    const float inv = apus_inv_pow2_from_exp(e);
+    if (!live) return;
+    *reinterpret_cast<uint32_t *>(codes + (size_t)m * K + b * 128 + l32 * 4) =
+        apus_e4m3_pack4_hw(h[0] * inv, h[1] * inv, h[2] * inv, h[3] * inv);
+    if (l32 == 0) scales[(size_t)m * nab + b] = apus_pow2_from_exp(e);
+}
+
 hipError_t apus_launch_act_quant(const float *x, int ldx, const int32_t *arows,
                                  int M, int K, uint8_t *codes, float *scales,
                                  hipStream_t st) {
     if (M <= 0) return hipSuccess;
     const int groups = M * (K >> 7);
+    if ((reinterpret_cast<uintptr_t>(x) & 15) == 0 && ldx % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(codes) & 3) == 0) {
+        hipLaunchKernelGGL(apus_act_quant4_kernel, dim3((groups + 7) / 8), dim3(256), 0, st,
+                           x, ldx, arows, M, K, codes, scales);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(apus_act_quant_kernel, dim3((groups + 3) / 4), dim3(256), 0, st,
                        x, ldx, arows, M, K, codes, scales);
     return hipGetLastError();
@@ -81,7 +115,10 @@ hipError_t apus_launch_swiglu_quant(const float *g, const float *u, int M,
                                     int N, float limit, uint8_t *codes,
                                     float *scales, hipStream_t st) {
     if (M <= 0) return hipSuccess;
-    if (N <= 0 || N % 128) return hipErrorInvalidValue;
+    if (N <= 0 || N % 128 ||
+        ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u)) & 15) ||
+        (reinterpret_cast<uintptr_t>(codes) & 3))
+        return hipErrorInvalidValue;
     const int groups = M * (N >> 7);
     hipLaunchKernelGGL(apus_swiglu_quant_kernel, dim3((groups + 7) / 8), dim3(256), 0, st,
                        g, u, M, N, limit, codes, scales);
@@ -424,23 +461,25 @@ hipError_t apus_launch_moe_accum(const float *eo, const float *wgt, int s,
  * FP32 or BF16 weights, FP32 accumulation. A wave owns 4 output rows and
  * sweeps K in 512-element steps, each lane taking 8 consecutive elements
  * per row (one 16-byte BF16 load or two FP32 loads), against up to 8 rows
- * of x; lane partials meet in a fixed xor-shuffle tree. The CPU sums each
+ * of x (one row in the M = 1 instance); lane partials meet in a fixed xor-shuffle tree. The CPU sums each
  * row sequentially, so results agree within FP32 summation error, not
- * bitwise. Launch row y covers x rows [8y, 8y + 8). */
+ * bitwise. Launch row y covers x rows [MB y, MB y + MB). */
+#ifndef APUS_WG_NR
 #define APUS_WG_NR 4
-template <bool WB>
+#endif
+template <bool WB, int MB>
 __global__ __launch_bounds__(256) void apus_wgemv_kernel(const void *__restrict__ w,
                                                          const float *__restrict__ x,
                                                          float *__restrict__ out, int M, int K,
                                                          int O, int flags) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int o0 = (blockIdx.x * 4 + wave) * APUS_WG_NR;
-    const int m0 = blockIdx.y * 8;
-    const int mb = min(8, M - m0);
+    const int m0 = blockIdx.y * MB;
+    const int mb = min(MB, M - m0);
     const bool rin = flags & 1;
-    float acc[8][APUS_WG_NR];
+    float acc[MB][APUS_WG_NR];
 #pragma unroll
-    for (int m = 0; m < 8; ++m)
+    for (int m = 0; m < MB; ++m)
 #pragma unroll
         for (int r = 0; r < APUS_WG_NR; ++r) acc[m][r] = 0.0f;
     for (int k = lane * 8; k < K; k += 512) {
@@ -464,7 +503,7 @@ __global__ __launch_bounds__(256) void apus_wgemv_kernel(const void *__restrict_
             }
         }
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
+        for (int m = 0; m < MB; ++m) {
             if (m < mb) {
                 const float *p = x + (size_t)(m0 + m) * K + k;
                 const float4 a = apus_gld<float4>(p), b = apus_gld<float4>(p + 4);
@@ -481,7 +520,7 @@ __global__ __launch_bounds__(256) void apus_wgemv_kernel(const void *__restrict_
         }
     }
 #pragma unroll
-    for (int m = 0; m < 8; ++m) {
+    for (int m = 0; m < MB; ++m) {
         if (m < mb) {
 #pragma unroll
             for (int r = 0; r < APUS_WG_NR; ++r) {
@@ -499,9 +538,16 @@ hipError_t apus_launch_wgemv(const void *w, const float *x, float *out, int M, i
                              int flags, hipStream_t st) {
     if (M <= 0 || O <= 0) return hipSuccess;
     if (K <= 0 || K % 8) return hipErrorInvalidValue;
-    dim3 grid((O + 4 * APUS_WG_NR - 1) / (4 * APUS_WG_NR), (M + 7) / 8), block(256);
-    if (flags & 4) hipLaunchKernelGGL(apus_wgemv_kernel<true>, grid, block, 0, st, w, x, out, M, K, O, flags);
-    else           hipLaunchKernelGGL(apus_wgemv_kernel<false>, grid, block, 0, st, w, x, out, M, K, O, flags);
+    const unsigned gx = (O + 4 * APUS_WG_NR - 1) / (4 * APUS_WG_NR);
+    const dim3 block(256);
+    if (M == 1) {       /* decode (the LM head): accumulators for one x row */
+        if (flags & 4) hipLaunchKernelGGL((apus_wgemv_kernel<true, 1>), dim3(gx), block, 0, st, w, x, out, M, K, O, flags);
+        else           hipLaunchKernelGGL((apus_wgemv_kernel<false, 1>), dim3(gx), block, 0, st, w, x, out, M, K, O, flags);
+        return hipGetLastError();
+    }
+    const dim3 grid(gx, (M + 7) / 8);
+    if (flags & 4) hipLaunchKernelGGL((apus_wgemv_kernel<true, 8>), grid, block, 0, st, w, x, out, M, K, O, flags);
+    else           hipLaunchKernelGGL((apus_wgemv_kernel<false, 8>), grid, block, 0, st, w, x, out, M, K, O, flags);
     return hipGetLastError();
 }
 

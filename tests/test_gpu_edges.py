@@ -192,3 +192,24 @@ def test_memset_refused_under_capture(hip):
     assert rc != 0 and "capture" in msg
     hip._check(L.apus_hip_memset(buf.ptr, 7, 4096), "memset after capture")
     assert (buf.to_array(np.uint8, (4096,)) == 7).all()
+
+
+def test_act_quant_dev_unaligned(hip, oracle):
+    """x rows that are not 16-byte aligned take the one-wave-per-group
+    kernel; codes and scales equal the oracle's and the aligned call's."""
+    M, K = 3, 512
+    rng = np.random.default_rng(7)
+    x = acts(rng, M, K)
+    x[1, :128] *= 1e-3
+    rc, rs = oracle.act_quant(bf16(x).copy())
+    buf = hip.DevBuf((M * K + 4) * 4)
+    pad = np.zeros(M * K + 4, np.float32)
+    pad[1:1 + M * K] = x.ravel()
+    hip._check(hip.lib().apus_hip_h2d(buf.ptr, pad.ctypes.data, pad.nbytes), "h2d")
+    for off in (0, 4):                    # bytes: aligned copy at 16, unaligned at 4
+        src = hip.DevBuf.from_array(x) if off == 0 else None
+        dc, ds = hip.DevBuf(M * K), hip.DevBuf(M * (K // 128) * 4)
+        ptr = src.ptr if src else buf.ptr + off
+        hip._check(hip.lib().apus_hip_act_quant_dev(ptr, M, K, dc.ptr, ds.ptr), "act_quant_dev")
+        assert np.array_equal(dc.to_array(np.uint8, (M, K)), rc), off
+        assert np.array_equal(ds.to_array(np.float32, (M, K // 128)), rs), off
