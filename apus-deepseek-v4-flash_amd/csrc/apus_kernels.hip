@@ -338,10 +338,80 @@ __global__ __launch_bounds__(256) void apus_router_kernel(
     }
 }
 
+/* The same scores for more than 8 tokens: one workgroup per (8 experts, 8
+ * tokens), so each gate row and each x row is read by s/8 and E/8 workgroups
+ * instead of every x row by all E. Thread i takes the same K elements in the
+ * same order as above (float4s i, i + 256, ...) for its 64 (expert, token)
+ * dots; the xor-shuffle tree is computed as a reduce-scatter (at each step a
+ * lane adds its partner's half of the values it keeps, so after six steps
+ * lane l holds dot l, every addition the one the tree makes), then the four
+ * wave sums in wave order: every score equals the one-expert kernel's bit for
+ * bit. dim % 1024 == 0, dim <= 8192, E % 8 == 0. */
+__global__ __launch_bounds__(256) void apus_router8_kernel(
+    const float *__restrict__ gate_w, const float *__restrict__ bias,
+    const float *__restrict__ x, int s, int dim, int E, float *__restrict__ sp,
+    float *__restrict__ biased) {
+    constexpr int EG = 8, TT = APUS_ROUTER_TT;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int e0 = blockIdx.x * EG, t0 = blockIdx.y * TT;
+    float v[EG * TT];                                     /* index i * TT + t */
+#pragma unroll
+    for (int q = 0; q < EG * TT; ++q) v[q] = 0.0f;
+    for (int k = tid * 4; k < dim; k += 1024) {
+        float4 g[EG], a[TT];
+#pragma unroll
+        for (int i = 0; i < EG; ++i) g[i] = apus_gld<float4>(gate_w + (size_t)(e0 + i) * dim + k);
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+            a[t] = apus_gld<float4>(x + (size_t)min(t0 + t, s - 1) * dim + k);
+#pragma unroll
+        for (int i = 0; i < EG; ++i)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) {
+                float &c = v[i * TT + t];
+                c = c + a[t].x * g[i].x;
+                c = c + a[t].y * g[i].y;
+                c = c + a[t].z * g[i].z;
+                c = c + a[t].w * g[i].w;
+            }
+    }
+    /* reduce-scatter over the wave: step `off` keeps the upper half of the
+     * remaining values in lanes with that bit set, the lower half elsewhere */
+#pragma unroll
+    for (int off = 32, n = 64; off >= 1; off >>= 1, n >>= 1) {
+        const bool up = lane & off;
+#pragma unroll
+        for (int j = 0; j < n / 2; ++j) {
+            const float send = up ? v[j] : v[j + n / 2];
+            const float keep = up ? v[j + n / 2] : v[j];
+            v[j] = keep + __shfl_xor(send, off, 64);
+        }
+    }
+    __shared__ float part[4][EG * TT];
+    part[wv][lane] = v[0];                                /* dot `lane` */
+    __syncthreads();
+    if (tid < EG * TT) {
+        const int i = tid / TT, t = tid % TT;
+        if (t0 + t < s) {
+            const float d = ((part[0][tid] + part[1][tid]) + part[2][tid]) + part[3][tid];
+            const float u = d > 20.0f ? d : log1pf(expf(d));
+            const float r = sqrtf(u);
+            const size_t o = (size_t)(t0 + t) * E + e0 + i;
+            sp[o] = r;
+            if (biased) biased[o] = r + bias[e0 + i];
+        }
+    }
+}
+
 hipError_t apus_launch_router(const float *gate_w, const float *bias, const float *x, int s,
                               int dim, int E, float *sp, float *biased, hipStream_t st) {
     if (s <= 0) return hipSuccess;
     if (dim % 256 || dim > 8192 || E <= 0) return hipErrorInvalidValue;
+    if (s > APUS_ROUTER_TT && dim % 1024 == 0 && E % 8 == 0) {
+        hipLaunchKernelGGL(apus_router8_kernel, dim3(E / 8, (s + APUS_ROUTER_TT - 1) / APUS_ROUTER_TT),
+                           dim3(256), 0, st, gate_w, bias, x, s, dim, E, sp, biased);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(apus_router_kernel, dim3(E, (s + APUS_ROUTER_TT - 1) / APUS_ROUTER_TT),
                        dim3(256), 0, st, gate_w, bias, x, s, dim, E, sp, biased);
     return hipGetLastError();

@@ -165,6 +165,24 @@ def test_moe_forward_dev_small(hip, oracle, store1, rng, s, topk, hash_, gate_sc
     _compare(got, want, cfg)
 
 
+@pytest.mark.parametrize("gate_scale", [1.0, 40.0])
+def test_router_many_tokens_bitwise(hip, oracle, store1, rng, gate_scale):
+    """More than 8 tokens take the router kernel over (8 experts, 8 tokens)
+    tiles; its scores equal, bit for bit, those of the one-expert kernel that
+    calls of at most 8 tokens use (same K order, same shuffle tree), and the
+    sublayer holds the oracle's bars."""
+    E, dim, inter, s, topk = 16, 1024, 128, 20, 4
+    experts = moe_experts(rng, E, dim, inter)
+    cfg, shared, x = _case(rng, E, dim, inter, s, topk, 0, gate_scale)
+    st = store1(E, dim, inter)
+    _put_experts(hip, st, experts, dim, inter)
+    got = _run_device(hip, st, cfg, shared, x)
+    _compare(got, oracle.moe_forward(cfg, experts, shared, x), cfg)
+    for a, b in ((0, 8), (8, 16), (16, 20)):
+        part = _run_device(hip, st, cfg, shared, x[a:b])
+        assert np.array_equal(part[3].view(np.uint32), got[3][a:b].view(np.uint32)), (a, b)
+
+
 def test_moe_forward_dev_exact_ties_pick_lowest_index(hip, oracle, store1, rng):
     """All gate rows equal and no bias: every score ties, so the choice is
     experts 0..topk-1 in order, with equal weights route_scale / topk."""
