@@ -175,6 +175,7 @@ SIGNATURES = {
     "apus_hip_last_error": (C.c_char_p, []),
     "apus_hip_device_info": (C.c_int, [C.c_char_p, C.c_size_t, C.POINTER(C.c_int)]),
     "apus_hip_layer1": (C.c_int, [C.c_int, C.POINTER(C.c_uint)]),
+    "apus_hip_layer1_spin_limit": (C.c_int, [C.c_uint]),
     "apus_hip_check_e4m3_hw": (C.c_int, [C.POINTER(C.c_uint), C.POINTER(C.c_uint)]),
     "apus_hip_host_bf16_round": (C.c_float, [C.c_float]),
     "apus_hip_host_e4m3_quant": (C.c_uint8, [C.c_float]),
@@ -330,9 +331,14 @@ def fp4_gemm_grouped(entries, acodes, ascales, O):
     return outs
 
 
-def moe_routed(experts, x, idx, wgt, limit, layer_id=0):
+def moe_routed(experts, x, idx, wgt, limit, layer_id=0, resolve=None, hint=None):
     """experts: list of E tuples (w1, w1s, w2, w2s, w3, w3s) of numpy arrays
-    (w1/w3 [inter, dim/2], w2 [dim, inter/2]). x [s, dim]; idx/wgt [s, topk]."""
+    (w1/w3 [inter, dim/2], w2 [dim, inter/2]). x [s, dim]; idx/wgt [s, topk].
+
+    resolve(layer, eid) -> a tuple like experts[eid] or None (failure), and
+    hint(layer, eid), when given, are installed as ApusMoeW.hook_resolve /
+    hook_hint (c/moe.h:45-56) and the w1/w2/w3 arrays are left NULL; the
+    arrays a resolve returns must stay alive until the call returns."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     idx = np.ascontiguousarray(idx, dtype=np.int32)
     wgt = np.ascontiguousarray(wgt, dtype=np.float32)
@@ -340,18 +346,36 @@ def moe_routed(experts, x, idx, wgt, limit, layer_id=0):
     topk = idx.shape[1]
     E = len(experts)
     inter = experts[0][0].shape[0]
-    a1 = (ApusFp4W * E)()
-    a2 = (ApusFp4W * E)()
-    a3 = (ApusFp4W * E)()
-    for e, (w1, w1s, w2, w2s, w3, w3s) in enumerate(experts):
-        a1[e] = ApusFp4W(_p(w1, u8p), _p(w1s, u8p), inter, dim)
-        a2[e] = ApusFp4W(_p(w2, u8p), _p(w2s, u8p), dim, inter)
-        a3[e] = ApusFp4W(_p(w3, u8p), _p(w3s, u8p), inter, dim)
     mw = ApusMoeW()
     mw.E, mw.topk, mw.inter, mw.dim = E, topk, inter, dim
     mw.limit = limit
-    mw.w1, mw.w2, mw.w3 = a1, a2, a3
     mw.layer_id = layer_id
+    keep = []
+    if resolve is None:
+        a1 = (ApusFp4W * E)()
+        a2 = (ApusFp4W * E)()
+        a3 = (ApusFp4W * E)()
+        for e, (w1, w1s, w2, w2s, w3, w3s) in enumerate(experts):
+            a1[e] = ApusFp4W(_p(w1, u8p), _p(w1s, u8p), inter, dim)
+            a2[e] = ApusFp4W(_p(w2, u8p), _p(w2s, u8p), dim, inter)
+            a3[e] = ApusFp4W(_p(w3, u8p), _p(w3s, u8p), inter, dim)
+        mw.w1, mw.w2, mw.w3 = a1, a2, a3
+    else:
+        def _resolve(ctx, layer, eid, p1, p2, p3):
+            t = resolve(layer, eid)
+            if t is None:
+                return 1
+            keep.append(t)
+            w1, w1s, w2, w2s, w3, w3s = t
+            p1[0] = ApusFp4W(_p(w1, u8p), _p(w1s, u8p), inter, dim)
+            p2[0] = ApusFp4W(_p(w2, u8p), _p(w2s, u8p), dim, inter)
+            p3[0] = ApusFp4W(_p(w3, u8p), _p(w3s, u8p), inter, dim)
+            return 0
+        mw.hook_resolve = RESOLVE_FN(_resolve)
+        keep.append(mw.hook_resolve)
+        if hint is not None:
+            mw.hook_hint = HINT_FN(lambda ctx, layer, eid: hint(layer, eid))
+            keep.append(mw.hook_hint)
     y = np.empty((s, dim), np.float32)
     _check(lib().apus_hip_moe_routed(C.byref(mw), _p(x, f32p), _p(idx, i32p), _p(wgt, f32p), s,
                                      _p(y, f32p)), "moe_routed")

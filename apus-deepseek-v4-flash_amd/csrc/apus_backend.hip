@@ -22,6 +22,7 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <condition_variable>
 #include <deque>
@@ -76,6 +77,7 @@ struct ExpertW {       /* one cached routed expert, six tensors */
     size_t bytes;
     int dim, inter;    /* a (layer, id) reused with another shape is re-uploaded */
     bool tiled;
+    uint64_t fp;       /* fingerprint of the six host tensors' bytes (not their addresses) */
 };
 
 struct State {
@@ -101,6 +103,13 @@ struct State {
      * launches running at once would each wait for CUs the other holds */
     unsigned *layer_bar = nullptr;
     bool layer1 = false, layer1_ok = false;
+    /* set to 1 by a layer workgroup whose barrier wait gave up (pinned host
+     * memory, written by the kernel through l1_flag_dev); finish() reports
+     * it as an error */
+    volatile unsigned *l1_flag = nullptr;
+    unsigned *l1_flag_dev = nullptr;
+    unsigned l1_spin = 1u << 23;
+    unsigned l1_faults = 0;       /* workgroups that gave up, seen by finish() since the last read */
     std::unordered_map<const void *, DenseW> dense;
     std::unordered_map<uint64_t, ExpertW> experts;
     DevBuf slots[8];          /* grow-only device scratch of the host-pointer calls */
@@ -182,6 +191,13 @@ bool ensure_init() {
             !ok(hipMemset(p, 0, nb), "hipMemset layer barrier"))
             return false;
         g.layer_bar = (unsigned *)p;
+        void *hf = nullptr, *hd = nullptr;
+        if (!ok(hipHostMalloc(&hf, 256, hipHostMallocMapped | hipHostMallocCoherent), "hipHostMalloc layer flag") ||
+            !ok(hipHostGetDevicePointer(&hd, hf, 0), "hipHostGetDevicePointer layer flag"))
+            return false;
+        *(volatile unsigned *)hf = 0;
+        g.l1_flag = (volatile unsigned *)hf;
+        g.l1_flag_dev = (unsigned *)hd;
         /* the one-launch layer needs its 256 workgroups resident together;
          * APUS_HIP_LAYER1=0 turns it off (two launches per layer) */
         const char *v = getenv("APUS_HIP_LAYER1");
@@ -293,10 +309,32 @@ void pin_reset() {
     g.pin_used = 0;
 }
 
+/* After lane 0 has drained: if a one-launch layer's barrier wait gave up
+ * since the last check, fold its fault count into g.l1_faults, reset the
+ * barrier words and report an error (the launch wrote NaN into the y
+ * columns of every workgroup that gave up). */
+bool l1_fault_check() {
+    if (!g.l1_flag || !*g.l1_flag) return true;
+    *g.l1_flag = 0;
+    unsigned n = 0;
+    const size_t nb = (size_t)apus_moe_layer1_bar_words() * sizeof(unsigned);
+    if (!ok(hipMemcpy(&n, g.layer_bar + apus_moe_layer1_fault_word(), sizeof(unsigned),
+                      hipMemcpyDeviceToHost), "hipMemcpy layer1 faults") ||
+        !ok(hipMemset(g.layer_bar, 0, nb), "hipMemset layer barrier") ||
+        !ok(hipDeviceSynchronize(), "hipDeviceSynchronize"))
+        return false;
+    g.l1_faults += n;
+    set_err("one-launch layer: %u workgroup(s) gave up waiting at the grid barrier (another kernel or "
+            "process held CUs); their y columns are NaN: rerun with apus_hip_layer1(0)", n);
+    return false;
+}
+
 /* wait for the stream, then hand staged downloads to their callers' buffers
- * and release the staging buffer */
+ * and release the staging buffer; false (with the error set) if the stream
+ * failed or a one-launch layer gave up at its barrier */
 bool finish() {
-    const bool r = ok(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    bool r = ok(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    if (r) r = l1_fault_check();
     if (r) {
         for (size_t i = 0; i < g.pin_out.size(); ++i)
             memcpy(g.pin_out[i].first, g.pin + g.pin_out_off[i], g.pin_out[i].second);
@@ -722,7 +760,7 @@ int moe_pipeline(int E, int dim, int inter, float limit, uint8_t *const *tab,
             !shf && !rf) {
             /* one launch: w1/w3 (+ rider), a grid barrier, w2 */
             if (add_out && !wait_add()) return 1;
-            return launched(apus_launch_moe_layer1(&a, &b, g.layer_bar, st), "one-token layer") ? 0 : 1;
+            return launched(apus_launch_moe_layer1(&a, &b, g.layer_bar, g.l1_flag_dev, g.l1_spin, st), "one-token layer") ? 0 : 1;
         }
         if (!launched(apus_launch_moe_pair13(&a, nj, st), "pair w1/w3")) return 1;
         if (add_out && !wait_add()) return 1;
@@ -1018,17 +1056,53 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
     for (int q = 0; q < nj; q++)
         if (idx[q] < 0 || idx[q] >= E) { set_err("moe_routed: expert id out of range"); return 1; }
     if (!x_finite(x, (size_t)s * dim, "moe_routed")) return 1;
-    /* resident expert slabs keyed by (layer, eid) */
-    std::vector<uint8_t *> tab(6 * (size_t)E, nullptr);
+    /* resident expert slabs keyed by (layer, eid). As in c/moe.h:419-431,
+     * a resolve hook gets one hint per unique routed expert (first-seen
+     * order) before any weight is resolved; then every unique expert is
+     * resolved (c/moe.h:439-441) before anything is uploaded or launched, so
+     * a failing resolve returns nonzero with nothing issued. A resolved slab
+     * may sit at another address on every call (the store's tiers move it);
+     * the cached copy is kept while the bytes' fingerprint matches. */
     const size_t sz[6] = {(size_t)inter * dim / 2, (size_t)inter * dim / 32,
                           (size_t)dim * inter / 2, (size_t)dim * inter / 32,
                           (size_t)inter * dim / 2, (size_t)inter * dim / 32};
-    for (int q = 0; q < nj; q++) {
-        const int e = idx[q];
-        if (tab[e]) continue;
+    std::vector<int> uniq;
+    std::vector<char> seen((size_t)E, 0);
+    for (int q = 0; q < nj; q++)
+        if (!seen[idx[q]]) { seen[idx[q]] = 1; uniq.push_back(idx[q]); }
+    if (w->hook_resolve && w->hook_hint)
+        for (int e : uniq) w->hook_hint(w->hook_hint_ctx ? w->hook_hint_ctx : w->hook_ctx, w->layer_id, e);
+    std::vector<std::array<const void *, 6>> srcs(uniq.size());
+    for (size_t u = 0; u < uniq.size(); u++) {
+        const int e = uniq[u];
+        ApusFp4W r1, r2, r3;
+        if (w->hook_resolve) {
+            if (w->hook_resolve(w->hook_ctx, w->layer_id, e, &r1, &r2, &r3)) {
+                set_err("moe_routed: expert resolve failed (layer %d, expert %d)", w->layer_id, e);
+                return 1;
+            }
+        } else {
+            r1 = w->w1[e]; r2 = w->w2[e]; r3 = w->w3[e];
+        }
+        srcs[u] = {r1.packed, r1.scales, r2.packed, r2.scales, r3.packed, r3.scales};
+        for (int i = 0; i < 6; i++)
+            if (!srcs[u][i]) {
+                set_err("moe_routed: expert %d of layer %d has a null tensor", e, w->layer_id);
+                return 1;
+            }
+        for (int i = 1; i < 6; i += 2)
+            if (!e8m0_ok((const uint8_t *)srcs[u][i], sz[i], "moe_routed expert")) return 1;
+    }
+    std::vector<uint8_t *> tab(6 * (size_t)E, nullptr);
+    for (size_t u = 0; u < uniq.size(); u++) {
+        const int e = uniq[u];
+        const auto &src = srcs[u];
+        uint64_t fp = 0;
+        for (int i = 0; i < 6; i++) fp = (fp ^ fingerprint((const uint8_t *)src[i], sz[i])) * 0x100000001b3ull;
         const uint64_t key = ((uint64_t)(uint32_t)w->layer_id << 32) | (uint32_t)e;
         auto it = g.experts.find(key);
-        if (it != g.experts.end() && (it->second.dim != dim || it->second.inter != inter)) {
+        if (it != g.experts.end() &&
+            (it->second.dim != dim || it->second.inter != inter || it->second.fp != fp)) {
             (void)hipStreamSynchronize(g.stream);
             (void)hipFree(it->second.p[0]);
             g.bytes_resident -= it->second.bytes;
@@ -1036,18 +1110,6 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
             it = g.experts.end();
         }
         if (it == g.experts.end()) {
-            ApusFp4W r1, r2, r3;
-            if (w->hook_resolve) {
-                if (w->hook_resolve(w->hook_ctx, w->layer_id, e, &r1, &r2, &r3)) {
-                    set_err("moe_routed: expert resolve failed");
-                    return 1;
-                }
-            } else {
-                r1 = w->w1[e]; r2 = w->w2[e]; r3 = w->w3[e];
-            }
-            const void *src[6] = {r1.packed, r1.scales, r2.packed, r2.scales, r3.packed, r3.scales};
-            for (int i = 1; i < 6; i += 2)
-                if (!e8m0_ok((const uint8_t *)src[i], sz[i], "moe_routed expert")) return 1;
             ExpertW ew{};
             size_t tot = 0;
             for (int i = 0; i < 6; i++) tot += align256(sz[i]);
@@ -1063,6 +1125,7 @@ int apus_hip_moe_routed(const ApusMoeW *w, const float *x, const int32_t *idx, c
             ew.dim = dim;
             ew.inter = inter;
             ew.tiled = moe_tiled(dim, inter);
+            ew.fp = fp;
             for (int m = 0; m < 3; m++) {
                 if (!upload_weights(APUS_W_FP4, ew.p[2 * m], ew.p[2 * m + 1], src[2 * m],
                                     src[2 * m + 1], sz[2 * m], sz[2 * m + 1], mo[m], mk[m],
@@ -1583,6 +1646,13 @@ int apus_hip_moe_routed_dev_noalloc(const ApusHipStore *st, int layer, const flo
         set_err("moe_routed_dev_noalloc: bad arguments");
         return 1;
     }
+    if (g.cur_lane != 0) {
+        /* the one static workspace is shared by every call on the device:
+         * calls on two lanes could overlap and race on it */
+        set_err("moe_routed_dev_noalloc: runs on lane 0 only (lane %d selected); its static workspace "
+                "would be shared with concurrent calls", g.cur_lane);
+        return 1;
+    }
     const size_t need = moe_carve(nullptr, s, topk, st->E, st->dim, st->inter).total;
     if (need > APUS_NOALLOC_SCRATCH_BYTES) {
         set_err("moe_routed_dev_noalloc: %d tokens x top-%d need %zu bytes of workspace, the "
@@ -1664,18 +1734,19 @@ int apus_hip_layer1(int mode, unsigned *faults) {
     if (mode == 1) g.layer1 = g.layer1_ok;
     if (faults) {
         if (capturing("apus_hip_layer1")) return -1;
-        if (!finish()) return -1;
-        if (!ok(hipMemcpy(faults, g.layer_bar + apus_moe_layer1_fault_word(), sizeof(unsigned),
-                          hipMemcpyDeviceToHost),
-                "hipMemcpy layer1 faults"))
-            return -1;
-        /* a workgroup that gave up waiting may have left the counter
-         * behind: start the next launch from zero */
-        if (*faults && !ok(hipMemset(g.layer_bar, 0, (size_t)apus_moe_layer1_bar_words() * sizeof(unsigned)),
-                           "hipMemset layer barrier"))
-            return -1;
+        if (!ok(hipStreamSynchronize(g.stream), "hipStreamSynchronize")) return -1;
+        (void)l1_fault_check();   /* its error is reported through *faults here */
+        *faults = g.l1_faults;
+        g.l1_faults = 0;
     }
     return g.layer1 ? 1 : 0;
+}
+
+int apus_hip_layer1_spin_limit(unsigned spins) {
+    if (!ensure_init()) return 1;
+    if (capturing("apus_hip_layer1_spin_limit")) return 1;
+    g.l1_spin = spins;
+    return 0;
 }
 
 int apus_hip_timer_start(void) {

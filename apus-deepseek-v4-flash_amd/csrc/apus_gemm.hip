@@ -1781,6 +1781,8 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
 #define APUS_L1_BAR_WORDS (18 * 256)
 struct ApusLayerBar {
     unsigned *w;
+    unsigned *hflag;     /* host-visible word set to 1 when a wait gives up (or null) */
+    unsigned spin_lim;   /* polls of the release word before a wait gives up */
 };
 
 
@@ -1818,23 +1820,28 @@ __device__ __forceinline__ void apus_l1_arrive(const ApusLayerBar &bar) {
         __hip_atomic_fetch_add(bar.w + APUS_L1_GEN(i), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void apus_l1_wait(const ApusLayerBar &bar, unsigned g0) {
+/* Returns true in every thread when this workgroup gave up waiting: the
+ * release was not seen within bar.spin_lim polls (about a second at the
+ * default 2^23; 0 gives up at once). The fault counter is bumped and the
+ * host-visible flag set, and the caller poisons its outputs with NaN. */
+__device__ __forceinline__ bool apus_l1_wait(const ApusLayerBar &bar, unsigned g0, int &tmo) {
     __syncthreads();
     if (threadIdx.x == 0) {
         const unsigned *genp = bar.w + APUS_L1_GEN(blockIdx.x & 7u);
-        /* bounded: after about a second the fault counter is bumped and the
-         * workgroup goes on (the launch's outputs are then not to be
-         * trusted) */
         unsigned spins = 0;
+        bool gave_up = false;
         while (__hip_atomic_load(genp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0) {
+            if (spins++ >= bar.spin_lim) { gave_up = true; break; }
             __builtin_amdgcn_s_sleep(1);
-            if (++spins == (1u << 23)) {
-                __hip_atomic_fetch_add(bar.w + APUS_L1_FAULT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
         }
+        if (gave_up) {
+            __hip_atomic_fetch_add(bar.w + APUS_L1_FAULT, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (bar.hflag) __hip_atomic_store(bar.hflag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        tmo = gave_up;
     }
     __syncthreads();
+    return tmo != 0;
 }
 
 /* phase-1 MFMA chain of one wave: row 0 of A is x (codes in LDS), the tile's
@@ -1884,6 +1891,7 @@ struct ApusLayer1Lds {
     float red[4][6][64];                      /* [K quarter][pair][lane] */
     float rr[8][64];                          /* rider partial sums [wave][lane] */
     int last[2];
+    int tmo;                                  /* the barrier wait gave up */
 };
 
 
@@ -2086,7 +2094,9 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
         }
         L.rr[wave][lane] = accr[0];                   /* lane (g 0, r): weight row 16 b + r */
     }
-    apus_l1_wait(bar, g0);
+    /* a workgroup that gave up waiting may read h codes not yet written:
+     * its y (and add_out) columns are written as NaN */
+    const bool tmo = apus_l1_wait(bar, g0, L.tmo);
 
     /* ---- phase 2 (as apus_moe_pair2_kernel, G = 2, one token) ---- */
     /* the h codes and scale bytes (see apus_l1_arrive for why plain
@@ -2132,6 +2142,7 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
             eo = okj[j] ? apus_bf16_rne(eo) : 0.0f;
             y = __fadd_rn(y, __fmul_rn(wj[j], eo));
         }
+        if (tmo) y = __builtin_nanf("");
         const size_t oo = (size_t)b * 16 + threadIdx.x;
         apus_gst<float>(a2.acc_y + oo, y);
         if (a2.add_out)
@@ -2156,7 +2167,7 @@ __global__ __launch_bounds__(512) void apus_moe_layer1_kernel(ApusGemmArgs a1, A
 }
 
 hipError_t apus_launch_moe_layer1(const ApusGemmArgs *a1, const ApusGemmArgs *a2, unsigned *bar,
-                                  hipStream_t st) {
+                                  unsigned *hflag, unsigned spin_lim, hipStream_t st) {
     if (a1->K != 4096 || a1->O != 2048 || a1->npairs != 6 || a1->adiv != 6 || a1->acc_s != 1 ||
         !a1->wtiled || !a2->wtiled || (a1->rdout && !a1->rdtiled) || !a1->pbase != !a2->pbase ||
         a1->shw[0] || a1->rsp || a1->zero || !a1->hq || !a1->hqs || !a1->hq_tk || !a1->pidx ||
@@ -2164,7 +2175,7 @@ hipError_t apus_launch_moe_layer1(const ApusGemmArgs *a1, const ApusGemmArgs *a2
         a2->hq != a1->hq || a2->hqs != a1->hqs || a2->pidx != a1->pidx || !bar ||
         (a1->rdout && (!a1->rdw || !a1->rdws)))
         return hipErrorInvalidValue;
-    ApusLayerBar b{bar};
+    ApusLayerBar b{bar, hflag, spin_lim};
     hipLaunchKernelGGL(apus_moe_layer1_kernel, dim3(APUS_L1_WGS), dim3(512), 0, st, *a1, *a2, b);
     return hipGetLastError();
 }

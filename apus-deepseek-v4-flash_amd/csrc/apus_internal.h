@@ -157,9 +157,12 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st);
  * and left zero (but for the counter at apus_moe_layer1_fault_word() of
  * workgroups that gave up waiting at the barrier). Needs all 256
  * workgroups resident at once: callers check apus_moe_layer1_fits() and the
- * CU count, and never run two of these launches concurrently. */
+ * CU count, and never run two of these launches concurrently. A workgroup
+ * whose barrier wait gives up after spin_lim polls writes NaN to its y (and
+ * add_out) columns and sets *hflag = 1 (device-visible host memory, or
+ * null). */
 hipError_t apus_launch_moe_layer1(const ApusGemmArgs *a1, const ApusGemmArgs *a2, unsigned *bar,
-                                  hipStream_t st);
+                                  unsigned *hflag, unsigned spin_lim, hipStream_t st);
 /* workgroups of apus_moe_layer1_kernel that fit on one CU; its barrier
  * buffer size and fault-counter word */
 int apus_moe_layer1_fits();

@@ -657,9 +657,21 @@ def bench_hostptr(H, O=2048, K=4096, calls=400):
     return {"us": us, "GBs": nbytes / us / 1e3}
 
 
+def cpu_threads():
+    """Threads for apus's CPU pool: the host's usable CPUs (nproc: the
+    process's affinity set), capped by OMP_NUM_THREADS where the host sets
+    it (the GPU box's CPU share) and at 32 like the pool itself
+    (c/pool.h:51,97-103)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, min(n, 32))
+
+
 def cpu_baseline(O=2048, K=4096, budget_s=12.0):
     """apus's own apus_fp4_gemm_mt (AVX2 rows + pthread pool) on config 0."""
-    threads = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
     os.environ.setdefault("APUS_THREADS", str(threads))
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import pyoracle
@@ -694,8 +706,10 @@ def cpu_baseline(O=2048, K=4096, budget_s=12.0):
     if kind == "reference":
         assert R.L.ref_x86_avx2_hits() > 0, "reference AVX2 rows were not taken"
     return {"value": nbytes / best / 1e9, "unit": "GB/s", "cores": int(used), "kind": kind,
+            "host_cpus": os.cpu_count(),
             "sample": f"config 0 GEMV O={O} K={K} M=1 (apus_fp4_gemm_mt), best of 3 x {reps} "
-                      f"reps, {best * 1e3:.3f} ms/GEMV"}
+                      f"reps, {best * 1e3:.3f} ms/GEMV; {int(used)} pool threads of "
+                      f"{os.cpu_count()} host CPUs"}
 
 
 def cpu_extras(budget_s=4.0):
@@ -746,6 +760,95 @@ def cpu_extras(budget_s=4.0):
     out["cpu_config3_expert_w1_M64_us"] = round(t * 1e6, 1)
     out["cpu_config3_expert_w1_M64_TFLOPs"] = round(2.0 * M4 * O4 * K4 / t / 1e12, 4)
     out["cpu_threads"] = int(R.L.ref_pool_threads())
+    out["cpu_host_cpus"] = os.cpu_count()
+    return out
+
+
+def cpu_moe(budget_s=20.0):
+    """apus's own CPU path on the MoE configs, same host threads:
+    * configs 2 and 3: the real apus_moe_forward (c/moe.h:369-595) with the
+      expert ids forced through hash routing, on the config-2 routing (64
+      tokens, top-6 of 256 by N(0,1) gating) and the config-3 routing (512
+      tokens, Zipf(1.1)); experts at dim 4096 / inter 2048, expert id e
+      reading slab e % 64 of a pool of 64 distinct random experts (856 MB,
+      far above any CPU cache, so every expert is streamed from DRAM as a
+      distinct one would be; a full 3.4 GB set only costs generation time).
+      The timed call is the whole sublayer: router scores
+      (gate [256, 4096]), the routed experts (its batched path for s > 1)
+      and the FP8 shared expert (all-zero weights, full cost), so the
+      routed part alone is somewhat faster;
+    * config 4: one token through 43 layers, each the FP8 [4096, 4096]
+      projection and the token's 6 routed experts as apus_moe_forward's
+      one-token path runs them (ref_decode_layer), the 258 expert slabs drawn
+      in turn from the pool (each re-read only after 10 layers, 550 MB
+      later) and 43 distinct projections: the bytes one token touches in the
+      150 GB model.
+    """
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+    if not pyoracle.have_ref():
+        return {}
+    R = pyoracle.Reference()
+    E, dim, inter, topk = 256, 4096, 2048, 6
+    rng = np.random.default_rng(11)
+    t0 = time.perf_counter()
+    pool = []
+    for _ in range(64):
+        pool.append((rng.integers(0, 256, (inter, dim // 2), dtype=np.uint8),
+                        rng.integers(118, 131, (inter, dim // 32), dtype=np.uint8),
+                        rng.integers(0, 256, (dim, inter // 2), dtype=np.uint8),
+                        rng.integers(118, 131, (dim, inter // 32), dtype=np.uint8),
+                        rng.integers(0, 256, (inter, dim // 2), dtype=np.uint8),
+                        rng.integers(118, 131, (inter, dim // 32), dtype=np.uint8)))
+    experts = [pool[e % len(pool)] for e in range(E)]
+    gate = (rng.standard_normal((E, dim)) / np.sqrt(dim)).astype(np.float32)
+    log(f"[bench] CPU MoE: experts generated in {time.perf_counter() - t0:.1f} s")
+    out = {}
+    ebytes = sum(a.nbytes for a in experts[0])
+    # the GPU legs' routings (the same generator, drawn in the same order)
+    rr = np.random.default_rng(3)
+    routes = {"config2": gate_routing(rr, 64, E, topk)[0], "config3": zipf_routing(rr, 512, E, topk, 1.1)[0]}
+    for cfg, s in (("config2", 64), ("config3", 512)):
+        idx = routes[cfg]
+        x = rng.standard_normal((s, dim)).astype(np.float32)
+        t0 = time.perf_counter()
+        R.moe_routed(experts, gate, x, idx, 2.5, 10.0)
+        one = time.perf_counter() - t0
+        reps = max(1, min(3, int(budget_s / 3 / one)))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            R.moe_routed(experts, gate, x, idx, 2.5, 10.0)
+        dt = (time.perf_counter() - t0) / reps
+        uniq = len(np.unique(idx))
+        out[f"cpu_{cfg}_sublayer_us"] = round(dt * 1e6, 1)
+        out[f"cpu_{cfg}_tok_s"] = round(s / dt, 2)
+        out[f"cpu_{cfg}_expert_GBs"] = round(uniq * ebytes / dt / 1e9, 2)
+        if cfg == "config3":
+            out["cpu_config3_routed_TFLOPs"] = round(2.0 * 3 * s * topk * dim * inter / dt / 1e12, 5)
+        log(f"[bench] CPU {cfg}: {dt * 1e3:.1f} ms per sublayer ({reps} timed)")
+    L = 43
+    pw = [rng.integers(0, 0x7E, (dim, dim), dtype=np.uint8) for _ in range(L)]
+    pws = [rng.integers(117, 124, (dim // 128, dim // 128), dtype=np.uint8) for _ in range(L)]
+    x = rng.standard_normal(dim).astype(np.float32)
+    wgt = np.full(topk, 1.0 / topk, np.float32)
+
+    def token():
+        for l in range(L):
+            exs = [experts[(l * topk + j) % E] for j in range(topk)]
+            pyoracle.ref_decode_layer(R, exs, wgt, pw[l], pws[l], x, 10.0)
+    token()
+    t0 = time.perf_counter()
+    n = 0
+    while n < 3 and (n == 0 or time.perf_counter() - t0 < budget_s / 3):
+        token()
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    per_tok = L * (topk * ebytes + dim * dim + (dim // 128) ** 2)
+    out["cpu_config4_tok_s"] = round(1.0 / dt, 3)
+    out["cpu_config4_ms_per_token"] = round(dt * 1e3, 1)
+    out["cpu_config4_GBs"] = round(per_tok / dt / 1e9, 2)
+    out["cpu_config4_layers"] = L
+    log(f"[bench] CPU config 4: {dt * 1e3:.1f} ms per token ({n} timed)")
     return out
 
 
@@ -872,6 +975,7 @@ def main():
     if cpu is not None and not args.skip_extras:
         log("[bench] CPU reference on configs 1 and 3 (samples)")
         extras.update(cpu_extras())
+        extras.update(cpu_moe())
     if g is None:
         print(json.dumps({"metric": METRIC, "extras": extras, "cpu_baseline": cpu}))
         return

@@ -326,8 +326,9 @@ int      apus_hip_moe_routed_dense_dev(const ApusHipStore *st, int layer, const 
  * with an error naming the bytes needed); the call itself allocates nothing
  * (apus_hip_enable must have run first). Every call on a GPU shares that
  * GPU's array and it keeps the last call's contents (nothing in it needs
- * to start at zero): calls that overlap on one GPU (other lanes, other
- * threads) race. Results are bit-identical to apus_hip_moe_routed_dev. */
+ * to start at zero): calls that overlap on one GPU (other threads, other
+ * processes) race; with a concurrency lane other than lane 0 selected the
+ * call is refused. Results are bit-identical to apus_hip_moe_routed_dev. */
 size_t   apus_hip_moe_noalloc_max(void);
 int      apus_hip_moe_routed_dev_noalloc(const ApusHipStore *st, int layer,
                                          const float *x, const int32_t *idx,
@@ -467,12 +468,22 @@ const char *apus_hip_last_error(void);
  * w2 in one kernel of 256 resident workgroups, on lane 0; y bit-identical to
  * the two-launch path). mode 1 turns it on (only where 256 workgroups fit
  * at once), 0 off (two launches per layer), -1 leaves it; the environment
- * variable APUS_HIP_LAYER1=0 turns it off at start-up. With faults: waits
- * for lane 0 and stores the number of workgroups that gave up waiting at the
- * barrier since the last such read (nonzero: the outputs of some launch are
- * not to be trusted; the barrier words are then reset). Returns 1 when on, 0 when off, -1 on
+ * variable APUS_HIP_LAYER1=0 turns it off at start-up. The barrier wait is
+ * bounded (about a second); a workgroup that gives up writes NaN into its
+ * 16 columns of y (and of the fused bf16(y + add) output) and flags the
+ * fault, so a result is never wrong and finite. The next
+ * apus_hip_synchronize (and every host-pointer hook's own wait) then returns
+ * nonzero with an error naming the fault; a caller that waits on the stream
+ * by other means polls the count here. With faults: waits for lane 0 and
+ * stores the number of workgroups that gave up since the last such read
+ * (the barrier words are then reset). Returns 1 when on, 0 when off, -1 on
  * error. No counterpart in the reference (a launch-structure switch). */
 int   apus_hip_layer1(int mode, unsigned *faults);
+/* Polls of the release word before a one-launch layer's barrier wait gives
+ * up (default 2^23, about a second); 0 makes every wait give up at once.
+ * A test hook for the fault path above (every kernel still exits normally).
+ * No counterpart in the reference. */
+int   apus_hip_layer1_spin_limit(unsigned spins);
 /* Device name and compute-unit count of the current device. */
 int   apus_hip_device_info(char *name, size_t cap, int *cus);
 

@@ -165,6 +165,11 @@ uint64_t orc_hash64(uint64_t seed, uint64_t stream, uint64_t index);
 void     orc_fill_bytes(uint64_t seed, uint64_t stream, uint64_t first,
                         uint8_t *out, size_t n, int kind);
 
+/* Checker bound, not a reference function: per output row, what the matrix
+ * cores' block-wise fixed-point addition can lose (tests/moe_check.py). */
+void     orc_fp4_mfma_slack(const uint8_t *w, const uint8_t *ws, const uint8_t *codes,
+                            const float *as, double *out, size_t O, size_t K, int window);
+
 #ifdef __cplusplus
 }
 #endif

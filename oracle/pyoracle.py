@@ -56,6 +56,7 @@ class Oracle:
                                       C.c_float, f32p, i32p, f32p, C.c_int, C.c_int, f32p]),
             "orc_fp4_truth_f64": (None, [u8p, u8p, u8p, f32p, f64p, f64p, sz, sz, sz]),
             "orc_fp8_truth_f64": (None, [u8p, u8p, u8p, f32p, f64p, f64p, sz, sz, sz]),
+            "orc_fp4_mfma_slack": (None, [u8p, u8p, u8p, f32p, f64p, sz, sz, C.c_int]),
             "orc_pin_unary": (C.c_uint64, [C.c_int, C.c_void_p, C.c_uint64, C.c_uint64,
                                            C.POINTER(C.c_uint32)]),
             "orc_hash64": (C.c_uint64, [C.c_uint64, C.c_uint64, C.c_uint64]),
@@ -155,6 +156,18 @@ class Oracle:
         self.L.orc_fp8_truth_f64(_p(w, u8p), _p(ws, u8p), _p(acodes, u8p), _p(asc, f32p),
                                  _p(out, f64p), _p(esc, f64p), M, O, K)
         return out, esc
+
+    def fp4_mfma_slack(self, w, ws, codes, scales, window):
+        """The MoE checker's per-output bound on the matrix cores' block-sum
+        loss (orc_fp4_mfma_slack) for one activation row."""
+        w, ws = np.ascontiguousarray(w, np.uint8), np.ascontiguousarray(ws, np.uint8)
+        codes = np.ascontiguousarray(np.asarray(codes).reshape(-1), np.uint8)
+        scales = np.ascontiguousarray(np.asarray(scales).reshape(-1), np.float32)
+        O, K = w.shape[0], codes.shape[0]
+        out = np.empty(O, np.float64)
+        self.L.orc_fp4_mfma_slack(_p(w, u8p), _p(ws, u8p), _p(codes, u8p), _p(scales, f32p),
+                                  _p(out, f64p), O, K, window)
+        return out
 
     def moe_routed(self, experts, x, idx, wgt, limit):
         x = np.ascontiguousarray(x, np.float32)
@@ -288,6 +301,8 @@ class Reference:
             "ref_moe_forward": (None, [C.c_int] * 4 + [C.c_float, C.c_float, C.c_int, f32p, f32p,
                                                         i64p, i64p] + [u8pp] * 6 + [u8p] * 6
                                 + [f32p, C.c_int, f32p, f32p, f32p, f32p, i32p, f32p]),
+            "ref_decode_layer": (None, [C.c_int, C.c_int, C.c_int, C.c_float] + [u8pp] * 6
+                                 + [f32p, u8p, u8p, C.c_int, f32p, f32p, f32p]),
             "apus_f32_linear": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
             "apus_bf16_linear": (None, [f32p, f32p, f32p, C.c_int, C.c_int, C.c_int]),
             "apus_head_gemv": (None, [C.c_void_p, f32p, f32p, C.c_int64, C.c_int64]),
@@ -445,6 +460,23 @@ class Reference:
         if rc != 0:
             raise RuntimeError("reference routing did not follow the forced expert ids")
         return rw, y
+
+
+def ref_decode_layer(R, experts, wgt, pw, pws, x, limit):
+    """One token through one config-4 layer on apus's own CPU kernels
+    (ref_decode_layer): experts = topk tuples (w1, w1s, w2, w2s, w3, w3s),
+    wgt [topk], FP8 projection pw [O8, dim] / pws; returns (y, proj)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    dim = x.shape[0]
+    topk = len(experts)
+    inter = experts[0][0].shape[0]
+    tabs = [(u8p * topk)(*[_p(e[i], u8p) for e in experts]) for i in range(6)]
+    wgt = np.ascontiguousarray(wgt, np.float32)
+    y = np.empty(dim, np.float32)
+    proj = np.empty(pw.shape[0], np.float32)
+    R.L.ref_decode_layer(topk, dim, inter, limit, *tabs, _p(wgt, f32p), _p(pw, u8p), _p(pws, u8p),
+                         pw.shape[0], _p(x, f32p), _p(y, f32p), _p(proj, f32p))
+    return y, proj
 
 
 def bf16_round_np(x):

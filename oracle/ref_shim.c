@@ -209,3 +209,29 @@ int ref_store_index(const char *dir, int n_layers, int n_mtp, int E, int32_t *sh
     apus_store_close(st);
     return 0;
 }
+
+/* One token through one decode layer of BASELINE config 4 on apus's own CPU
+ * kernels: the FP8 [O8, dim] projection of x (apus_fp8_linear, c/attn.h:
+ * 408-430) and the routed experts of the token as apus_moe_forward's s == 1
+ * path runs them (c/moe.h:435-450: apus_expert per pair, then y += w * eo
+ * in j order). w1..w3s hold the topk experts' tensors. Used as the timed
+ * CPU baseline of config 4. */
+void ref_decode_layer(int topk, int dim, int inter, float limit,
+                      const uint8_t *const *w1, const uint8_t *const *w1s,
+                      const uint8_t *const *w2, const uint8_t *const *w2s,
+                      const uint8_t *const *w3, const uint8_t *const *w3s,
+                      const float *wgt, const uint8_t *pw, const uint8_t *pws, int O8,
+                      const float *x, float *y, float *proj) {
+    ApusFp8W p = { pw, pws, O8, dim };
+    apus_fp8_linear(&p, x, proj, 1, dim, O8);
+    float *eo = malloc((size_t)dim * sizeof(float));
+    memset(y, 0, (size_t)dim * sizeof(float));
+    for (int j = 0; j < topk; j++) {
+        ApusFp4W e1 = { w1[j], w1s[j], inter, dim };
+        ApusFp4W e2 = { w2[j], w2s[j], dim, inter };
+        ApusFp4W e3 = { w3[j], w3s[j], inter, dim };
+        apus_expert(&e1, &e2, &e3, 0, limit, x, dim, inter, eo);
+        for (int i = 0; i < dim; i++) y[i] += wgt[j] * eo[i];
+    }
+    free(eo);
+}

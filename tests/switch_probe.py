@@ -1,0 +1,94 @@
+"""Child process of tests/test_gpu_switches.py: runs a fixed set of launches
+with whatever APUS_HIP_* schedule switches the parent put in the environment
+(they are read once per process) and writes every output to an .npz file.
+
+Usage: python tests/switch_probe.py OUT.npz
+
+Cases (all seeded, the same in every run):
+* routed dispatch over a 16-expert store at dim 4096 / inter 2048, top-6,
+  s = 1, 2, 4 (one-token and per-pair kernels) and 64 (sorted: few-row and
+  many-row schedules): y and the h codes / scale bytes of every pair;
+* the whole MoE sublayer at s = 8 (router, top-k, routed, FP8 shared
+  expert, sum): out, routed, shared;
+* dense decode-schedule launches: an FP8 [4096, 4096] GEMV at M = 1 and a
+  12-entry MXFP4 [2048, 4096] grouped GEMV (inputs saved for the oracle).
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+for p in (os.path.join(ROOT, "apus-deepseek-v4-flash_amd"), os.path.join(ROOT, "oracle"), HERE):
+    sys.path.insert(0, p)
+
+import apus_hip as hip  # noqa: E402
+from helpers import acts, bf16, fp4_weights, fp8_weights, topk_routing  # noqa: E402
+
+DIM, INTER, E, TOPK, LIMIT = 4096, 2048, 16, 6, 10.0
+
+
+def routed(L, st, s, rng, out):
+    x = bf16(acts(rng, s, DIM))
+    idx, wgt = topk_routing(rng, s, E, TOPK)
+    dx, di, dw = (hip.DevBuf.from_array(np.ascontiguousarray(a)) for a in (x, idx, wgt))
+    dy = hip.DevBuf(s * DIM * 4)
+    wsp = hip.DevBuf(L.apus_hip_moe_workspace(st, s, TOPK))
+    hip._check(L.apus_hip_moe_routed_dev(st, 0, dx.ptr, di.ptr, dw.ptr, s, TOPK, LIMIT, dy.ptr,
+                                         wsp.ptr), "routed_dev")
+    hc, he = hip.DevBuf(s * TOPK * INTER), hip.DevBuf(s * TOPK * (INTER // 128))
+    hip._check(L.apus_hip_moe_routed_h(st, s, TOPK, wsp.ptr, hc.ptr, he.ptr), "routed_h")
+    out[f"y{s}"] = dy.to_array(np.float32, (s, DIM))
+    out[f"hc{s}"] = hc.to_array(np.uint8, (s * TOPK, INTER))
+    out[f"he{s}"] = he.to_array(np.uint8, (s * TOPK, INTER // 128))
+
+
+def sublayer(L, st, rng, out):
+    from test_gpu_moe_forward import _case, _run_device
+    cfg, shared, x = _case(rng, E, DIM, INTER, 8, TOPK, False)
+    o, r, sh, _, idx, _ = _run_device(hip, st, cfg, shared, bf16(x), shared_tiled=True)
+    out["fwd_out"], out["fwd_routed"], out["fwd_shared"], out["fwd_idx"] = o, r, sh, idx
+
+
+def dense(rng, out):
+    w, ws = fp8_weights(rng, 4096, 4096)
+    c, s = hip.act_quant(acts(rng, 1, 4096))
+    out["fp8_w"], out["fp8_ws"], out["fp8_c"], out["fp8_s"] = w, ws, c, s
+    out["fp8_y"] = hip.fp8_gemm(w, ws, c, s)
+    c4, s4 = hip.act_quant(acts(rng, 1, 4096))
+    ents = []
+    for i in range(12):
+        w4, ws4 = fp4_weights(rng, 2048, 4096)
+        ents.append((w4, ws4, 0, 1))
+        out[f"fp4_w{i}"], out[f"fp4_ws{i}"] = w4, ws4
+    out["fp4_c"], out["fp4_s"] = c4, s4
+    for i, y in enumerate(hip.fp4_gemm_grouped(ents, c4, s4, 2048)):
+        out[f"fp4_y{i}"] = y
+
+
+def main():
+    hip.enable()
+    L = hip.lib()
+    err = C.create_string_buffer(256)
+    st = L.apus_hip_store_create(1, E, DIM, INTER, err, 256)
+    assert st, err.value
+    hip._check(L.apus_hip_store_fill_random(st, 31), "store fill")
+    out = {}
+    rng = np.random.default_rng(77)
+    for s in (1, 2, 4, 64):
+        print(f"switch_probe: routed s={s}", flush=True)
+        routed(L, st, s, rng, out)
+    print("switch_probe: sublayer s=8", flush=True)
+    sublayer(L, st, rng, out)
+    print("switch_probe: dense", flush=True)
+    dense(rng, out)
+    hip._check(L.apus_hip_synchronize(), "sync")
+    L.apus_hip_store_free(st)
+    np.savez(sys.argv[1], **out)
+    print("switch_probe: done", flush=True)
+
+
+if __name__ == "__main__":
+    main()

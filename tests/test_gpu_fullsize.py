@@ -9,21 +9,31 @@
   over a 256-expert store at dim 4096, inter 2048. The reference's gate
   (tests/m9b/test_m9b.c:1-20, tests/m9e/README.md:158-164): every token's
   batched result equals dispatching that token alone, bit for bit, and so do
-  the quantised SwiGLU activations h of every pair. A seeded sample of tokens
-  (for config 3, including rows of the most popular expert, which take the
-  many-row schedule) is then checked stage by stage against the oracle with
-  the per-element bounds of moe_check.py.
-* Config 4: one token through a 43-layer store (147 GB resident): layers 0,
-  21 and 42 checked stage by stage against host-regenerated experts, and the
-  FP8 [4096, 4096] projection of the same layers against the oracle.
+  the quantised SwiGLU activations h of every pair. Tokens are then checked
+  stage by stage against the oracle with the per-element bounds of
+  moe_check.py (whole token: h of every pair, eo and y): config 2, 8 seeded
+  tokens; config 3, 8 seeded tokens, a token of the most popular expert and
+  one of an expert with exactly 8 and one with exactly 9 rows (the few-row /
+  many-row boundary), and in addition the h of EVERY pair routed to the
+  most popular expert (so every 64-row chunk of its many-row work items,
+  the last partial one included, whatever order the counting sort gave).
+* Config 4: one token through a 43-layer store (147 GB resident): 6 layers
+  checked stage by stage against host-regenerated experts, and the FP8
+  [4096, 4096] projection of the same layers against the oracle.
+
+The host checks run in a thread pool (the oracle's C loops release the
+interpreter lock).
 """
 import ctypes as C
+import os
+import threading
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
 
 from helpers import bf16, bf16_linear_ok, err_esc, fp8_weights, max_rel
-from moe_check import check_token
+from moe_check import check_pair, check_token
 
 pytestmark = pytest.mark.gpu
 
@@ -100,12 +110,20 @@ def store1(hip):
 
 def _expert_cache(oracle, seed, layer):
     cache = {}
+    lock = threading.Lock()
 
     def get(e):
-        if e not in cache:
-            cache[e] = host_expert(oracle, seed, layer, e)
-        return cache[e]
+        with lock:
+            if e in cache:
+                return cache[e]
+        ex = host_expert(oracle, seed, layer, e)
+        with lock:
+            return cache.setdefault(e, ex)
     return get
+
+
+def _pool():
+    return ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
 
 
 def _batched_vs_per_token(store, x, idx, wgt):
@@ -118,13 +136,17 @@ def _batched_vs_per_token(store, x, idx, wgt):
     return yb, hb, eb
 
 
-def _stage_checks(oracle, store, x, idx, wgt, yb, hb, eb, tokens, layer=0):
-    experts = _expert_cache(oracle, store.seed, layer)
-    for t in tokens:
-        r = check_token(oracle, experts, x[t], idx[t], wgt[t], LIMIT, hb[t], eb[t], yb[t])
+def _stage_checks(oracle, store, x, idx, wgt, yb, hb, eb, tokens, layer=0, experts=None):
+    experts = experts or _expert_cache(oracle, store.seed, layer)
+    tokens = [int(t) for t in tokens]
+    with _pool() as ex:
+        rs = list(ex.map(lambda t: check_token(oracle, experts, x[t], idx[t], wgt[t], LIMIT, hb[t],
+                                               eb[t], yb[t]), tokens))
+    for t, r in zip(tokens, rs):
         print(f"token {t}: experts {[int(e) for e in idx[t]]}: h pinned {r['h_pinned']:.3f}, "
               f"y pinned {r['y_pinned']:.3f} (all pinned values exact), y max_rel "
               f"{r['y_max_rel']:.3g}", flush=True)
+    print(f"stage-checked {len(tokens)} of {x.shape[0]} tokens", flush=True)
 
 
 def _bf16_x(rng, s):
@@ -152,7 +174,7 @@ def test_config2_decode_moe(hip, oracle, store1):
     x = _bf16_x(rng, s)
     idx, wgt = gate_routing(rng, s)
     yb, hb, eb = _batched_vs_per_token(store1, x, idx, wgt)
-    _stage_checks(oracle, store1, x, idx, wgt, yb, hb, eb, rng.choice(s, 3, replace=False))
+    _stage_checks(oracle, store1, x, idx, wgt, yb, hb, eb, rng.choice(s, 8, replace=False))
 
 
 def test_config3_prefill_moe(hip, oracle, store1):
@@ -166,9 +188,27 @@ def test_config3_prefill_moe(hip, oracle, store1):
     # 64-row chunks, the rare ones through the few-row schedule
     assert counts[top] > 128 and ((counts > 0) & (counts <= 8)).any()
     yb, hb, eb = _batched_vs_per_token(store1, x, idx, wgt)
+    experts = _expert_cache(oracle, store1.seed, 0)
+    # h of every pair routed to the most popular expert: its many-row work
+    # items cover every 64-row chunk, the last partial one included
+    pairs = np.argwhere(idx == top)
+    with _pool() as ex:
+        pin = list(ex.map(lambda tj: check_pair(oracle, experts(top), x[tj[0]], LIMIT,
+                                                hb[tj[0], tj[1]], eb[tj[0], tj[1]]), pairs))
+    print(f"expert {top}: {len(pairs)} pairs ({-(-len(pairs) // 64)} chunks of 64), h stage-checked, "
+          f"pinned {np.mean(pin):.3f}", flush=True)
     with_top = np.nonzero((idx == top).any(1))[0]
+    tokens = [int(with_top[-1])] + [int(t) for t in rng.choice(s, 8, replace=False)]
+    for n in (8, 9):                                  # the few-row / many-row boundary
+        es = np.nonzero(counts == n)[0]
+        if es.size:
+            tokens.append(int(np.nonzero((idx == es[0]).any(1))[0][0]))
+            print(f"expert {int(es[0])} has {n} rows", flush=True)
+        else:
+            print(f"no expert with exactly {n} rows in this routing", flush=True)
     rare = np.nonzero((counts[idx] <= 8).any(1))[0]
-    _stage_checks(oracle, store1, x, idx, wgt, yb, hb, eb, [int(with_top[-1]), int(rare[0])])
+    tokens.append(int(rare[0]))
+    _stage_checks(oracle, store1, x, idx, wgt, yb, hb, eb, sorted(set(tokens)), experts=experts)
 
 
 @pytest.mark.timeout(600)
@@ -176,6 +216,7 @@ def test_config4_full_footprint(hip, oracle):
     """43 layers of 256 experts (147 GB of expert slabs) resident; one token
     through every layer (routed dispatch + FP8 projection per layer)."""
     layers, seed = 43, 44
+    CHECKED = (0, 8, 17, 21, 33, 42)
     L = hip.lib()
     st = Store(hip, layers, seed)
     try:
@@ -195,14 +236,19 @@ def test_config4_full_footprint(hip, oracle):
         for l in range(layers):
             hip._check(L.apus_hip_linear_dev(1, wd.ptr + l * O * K, wds.ptr + l * (O // 128) * (K // 128),
                                              dx.ptr, hd.ptr + l * DIM * 4, 1, K, O, wl.ptr), "fp8 linear")
-            outs[l] = st.routed(l, x, idx[l:l + 1], wgt[l:l + 1], read_h=l in (0, 21, 42))
+            outs[l] = st.routed(l, x, idx[l:l + 1], wgt[l:l + 1], read_h=l in CHECKED)
         proj = hd.to_array(np.float32, (layers, DIM))
-        for l in (0, 21, 42):
+
+        def one(l):
             y, hc, he = outs[l]
-            r = check_token(oracle, _expert_cache(oracle, seed, l), x[0], idx[l], wgt[l], LIMIT,
-                            hc[0], he[0], y[0])
+            return check_token(oracle, _expert_cache(oracle, seed, l), x[0], idx[l], wgt[l], LIMIT,
+                               hc[0], he[0], y[0])
+        with _pool() as ex:
+            rs = list(ex.map(one, CHECKED))
+        for l, r in zip(CHECKED, rs):
             print(f"layer {l}: h pinned {r['h_pinned']:.3f}, y pinned {r['y_pinned']:.3f}, "
                   f"y max_rel {r['y_max_rel']:.3g}", flush=True)
+        for l in CHECKED:
             nsc = (O // 128) * (K // 128)
             w8 = oracle.fill_bytes(seed, 1 << 40, O * K, 2, first=l * O * K).reshape(O, K)
             s8 = oracle.fill_bytes(seed, (1 << 40) + 1, nsc, 3, first=l * nsc).reshape(O // 128, K // 128)

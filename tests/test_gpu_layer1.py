@@ -178,3 +178,55 @@ def test_layer1_graph_replays(hip, st8):
         run()                                        # eager launches between replays
         hip._check(L.apus_hip_synchronize(), "sync")
     assert _faults(hip) == 0
+
+
+def test_layer1_barrier_timeout_poisons_output(hip, st8):
+    """A barrier wait that gives up never hands back a finite wrong result.
+
+    The host sets the wait's bound to zero polls, so every workgroup that
+    reaches its wait before the release gives up at once (the 64 workgroups
+    without phase-1 units arrive at the start and always do); every kernel
+    still exits normally. Each workgroup that gave up writes NaN into its 16
+    columns of y, the others (which saw the release, so every h code was
+    written) equal the two-launch result bit for bit; apus_hip_synchronize
+    returns nonzero naming the fault, the count reads back as the number of
+    NaN column blocks, and with the default bound the next launch is clean.
+    """
+    _layer1_available(hip)
+    L = hip.lib()
+    rng = np.random.default_rng(6)
+    x = bf16(rng.standard_normal((1, DIM)).astype(np.float32))
+    idx, wgt = topk_routing(rng, 1, E, TOPK)
+    assert L.apus_hip_layer1(0, None) == 0
+    ref = _routed(hip, st8, 2, x, idx, wgt)[0]
+    assert L.apus_hip_layer1(1, None) == 1
+    assert _faults(hip) == 0
+    dx, di, dw = (hip.DevBuf.from_array(np.ascontiguousarray(a)) for a in (x, idx, wgt))
+    dy = hip.DevBuf(DIM * 4)
+    wsp = hip.DevBuf(L.apus_hip_moe_workspace(st8, 1, TOPK))
+    hip._check(L.apus_hip_layer1_spin_limit(0), "spin_limit")
+    try:
+        hip._check(L.apus_hip_moe_routed_dev(st8, 2, dx.ptr, di.ptr, dw.ptr, 1, TOPK, LIMIT,
+                                             dy.ptr, wsp.ptr), "routed_dev")
+        rc = L.apus_hip_synchronize()
+        msg = L.apus_hip_last_error().decode()
+    finally:
+        hip._check(L.apus_hip_layer1_spin_limit(1 << 23), "spin_limit")
+    assert rc != 0 and "gave up waiting" in msg, (rc, msg)
+    y = dy.to_array(np.float32, (1, DIM))
+    nanblk = np.isnan(y.reshape(DIM // 16, 16))
+    assert (nanblk.all(1) | ~nanblk.any(1)).all()     # whole 16-column blocks
+    nb = int(nanblk.all(1).sum())
+    assert nb >= 64, nb                               # at least the workgroups without units
+    ok = ~np.isnan(y)
+    assert np.array_equal(y[ok].view(np.uint32), ref[ok].view(np.uint32))
+    f = _faults(hip)
+    print(f"timed-out workgroups: {f}, NaN column blocks: {nb}")
+    assert f == nb
+    # the default bound again: clean, bit-identical to the two launches
+    hip._check(L.apus_hip_moe_routed_dev(st8, 2, dx.ptr, di.ptr, dw.ptr, 1, TOPK, LIMIT,
+                                         dy.ptr, wsp.ptr), "routed_dev")
+    hip._check(L.apus_hip_synchronize(), "sync")
+    y = dy.to_array(np.float32, (1, DIM))
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
+    assert _faults(hip) == 0

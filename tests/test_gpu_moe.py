@@ -216,3 +216,81 @@ def test_moe_routed_many_pairs(hip, oracle, rng):
         assert np.array_equal(part.view(np.uint32), full[h:h + 400].view(np.uint32)), h
     want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
     assert max_rel(full, want) <= 2.0 ** -7
+
+
+def test_moe_routed_resolve_hook(hip, oracle, rng):
+    """apus_hip_moe_routed with ApusMoeW.hook_resolve set and w1/w2/w3 NULL
+    (the expert store's route, c/moe.h:45-56, :419-441).
+
+    * every unique routed expert gets one hint, in first-seen (t, j) order,
+      before any resolve; each is then resolved once per call;
+    * the result equals the array route bit for bit and the oracle within
+      the dispatch bar; the resolve returns fresh copies at new addresses on
+      every call (a tiered store moves slabs), which re-uses the resident
+      copy (nothing uploaded);
+    * a second layer_id with the same ids resolves and uploads again;
+    * changed bytes under the same (layer, id) are uploaded again and give
+      the new result;
+    * a resolve that fails returns nonzero with nothing launched or uploaded.
+    """
+    L = hip.lib()
+    E, dim, inter, s, topk = 16, 512, 256, 5, 4
+    experts = moe_experts(rng, E, dim, inter)
+    x = acts(rng, s, dim)
+    idx, wgt = topk_routing(rng, s, E, topk)
+    order = []
+    for e in idx.ravel():
+        if int(e) not in order:
+            order.append(int(e))
+    log = []
+
+    def resolve(layer, eid):
+        log.append(("r", layer, eid))
+        return tuple(a.copy() for a in experts[eid])
+
+    def hint(layer, eid):
+        log.append(("h", layer, eid))
+
+    want = oracle.moe_routed(experts, x, idx, wgt, 10.0)
+    base = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=4100)
+    got = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=4101, resolve=resolve, hint=hint)
+    assert log == [("h", 4101, e) for e in order] + [("r", 4101, e) for e in order]
+    assert np.array_equal(got.view(np.uint32), base.view(np.uint32))
+    assert max_rel(got, want) <= 2.0 ** -7
+
+    # the same layer again: resolved again, the resident copies are used
+    log.clear()
+    up0, d0 = L.apus_hip_bytes_uploaded(), L.apus_hip_dispatches()
+    again = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=4101, resolve=resolve, hint=hint)
+    assert [t for t in log if t[0] == "r"] == [("r", 4101, e) for e in order]
+    assert L.apus_hip_bytes_uploaded() == up0
+    assert np.array_equal(again.view(np.uint32), got.view(np.uint32))
+
+    # another layer with the same ids: resolved and uploaded again
+    log.clear()
+    other = hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=4102, resolve=resolve)
+    assert log == [("r", 4102, e) for e in order]
+    assert L.apus_hip_bytes_uploaded() > up0
+    assert np.array_equal(other.view(np.uint32), got.view(np.uint32))
+
+    # new bytes under the same (layer, id): uploaded again, new result
+    e0 = order[0]
+    fresh = moe_experts(rng, 1, dim, inter)[0]
+    changed = list(experts)
+    changed[e0] = fresh
+    up1 = L.apus_hip_bytes_uploaded()
+    new = hip.moe_routed(changed, x, idx, wgt, 10.0, layer_id=4102,
+                         resolve=lambda layer, eid: tuple(a.copy() for a in changed[eid]))
+    assert L.apus_hip_bytes_uploaded() > up1
+    want2 = oracle.moe_routed(changed, x, idx, wgt, 10.0)
+    assert max_rel(new, want2) <= 2.0 ** -7
+    assert not np.array_equal(new, got)
+
+    # a failing resolve: nonzero, nothing launched or uploaded
+    bad = order[len(order) // 2]
+    up2, d2 = L.apus_hip_bytes_uploaded(), L.apus_hip_dispatches()
+    with pytest.raises(hip.ApusHipError, match="resolve failed"):
+        hip.moe_routed(experts, x, idx, wgt, 10.0, layer_id=4103,
+                       resolve=lambda layer, eid: None if eid == bad else experts[eid])
+    assert L.apus_hip_bytes_uploaded() == up2
+    assert L.apus_hip_dispatches() == d2

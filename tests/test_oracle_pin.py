@@ -352,3 +352,20 @@ def test_wlinear_restatement_vs_reference(oracle, ref, rng, M, K, O):
     truth, esc = oracle.wlinear_truth(w, x, 0)
     got = oracle.wlinear(w, x, 0).astype(np.float64)
     assert np.all(np.abs(got - truth) <= K * 2.0 ** -24 * esc + 1e-30)
+
+
+def test_ref_decode_layer_vs_oracle(oracle, ref, rng):
+    """The config-4 CPU baseline's layer (ref_decode_layer: apus's own
+    apus_fp8_linear and the one-token routed loop of apus_moe_forward)
+    equals the oracle's FP8 linear and routed dispatch bit for bit."""
+    from pyoracle import ref_decode_layer
+    dim, inter, topk = 512, 256, 6
+    experts = moe_experts(rng, topk, dim, inter)
+    pw, pws = fp8_weights(rng, dim, dim)
+    x = acts(rng, 1, dim)
+    wgt = rng.random(topk).astype(np.float32)
+    y, proj = ref_decode_layer(ref, experts, wgt, pw, pws, x, 10.0)
+    want_y = oracle.moe_routed(experts, x, np.arange(topk, dtype=np.int32)[None, :], wgt[None, :], 10.0)
+    want_p = oracle.fp8_linear(pw, pws, x)
+    assert np.array_equal(y.view(np.uint32), want_y[0].view(np.uint32))
+    assert np.array_equal(proj.view(np.uint32), want_p[0].view(np.uint32))

@@ -2,7 +2,9 @@
 through the C ABI: two calls in a row, the second with fewer tokens, each
 bit-identical to apus_hip_moe_routed_dev with a caller workspace (the same
 kernels over the same workspace layout); a call whose workspace would not
-fit the static scratch is refused without running."""
+fit the static scratch is refused without running, and so is a call with a
+concurrency lane other than lane 0 selected (two lanes' calls would share
+the one static workspace)."""
 import ctypes as C
 
 import numpy as np
@@ -51,5 +53,15 @@ def test_noalloc_matches_workspace_entry(hip):
         rc = L.apus_hip_moe_routed_dev_noalloc(st, 0, dx.ptr, di.ptr, dw.ptr, s, TOPK, 10.0, y1.ptr)
         assert rc != 0 and b"static scratch" in L.apus_hip_last_error()
         assert L.apus_hip_dispatches() == d0
+        # a lane other than lane 0: refused, nothing launched
+        hip._check(L.apus_hip_lanes(2), "lanes")
+        hip._check(L.apus_hip_lane(1), "lane 1")
+        try:
+            s = 3
+            rc = L.apus_hip_moe_routed_dev_noalloc(st, 0, dx.ptr, di.ptr, dw.ptr, s, TOPK, 10.0, y1.ptr)
+            assert rc != 0 and b"lane 0 only" in L.apus_hip_last_error()
+            assert L.apus_hip_dispatches() == d0
+        finally:
+            hip._check(L.apus_hip_lane(0), "lane 0")
     finally:
         L.apus_hip_store_free(st)
