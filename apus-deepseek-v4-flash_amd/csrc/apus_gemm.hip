@@ -1295,6 +1295,184 @@ __global__ __launch_bounds__(64 * NW) void apus_gemm_tile_kernel(ApusGemmArgs ar
 }
 
 /*
+ * LDS tile schedule for dense FP8 GEMMs with more than 8 rows on MFMA-tiled
+ * weights (e.g. a 512-token projection): the same 64 x 128 output tile and
+ * the same accumulation chain per output (one chain over the 128-groups in
+ * order) as apus_gemm_tile_kernel, so the two give identical bits, but both
+ * operands travel global -> LDS directly (global_load_lds_dwordx4, no
+ * register staging) through NST stages of one 128-group each, read by 8
+ * waves (4 x 2, each 16 tokens x 64 weight rows). Per stage: 8 loads of 8
+ * whole activation rows (each row's 16-byte chunks XOR-swizzled by the row
+ * so the fragment reads are conflict-free) and 16 loads of 1 KB weight
+ * fragments (the tiled layout is the MFMA operand order), 3 per wave; the
+ * activation scales of every group go to LDS once, up front. Workgroup b
+ * takes tile (b & 7) * (tiles / 8) + (b >> 3) when tiles % 8 == 0, so each
+ * XCD (workgroups are dealt to the 8 XCDs round robin) works on one band of
+ * weight-row blocks and every token block: its weight bytes come from HBM
+ * once into that XCD's L2. Measured on gfx950 at M = 512, O = K = 4096 (a
+ * fresh weight copy per launch): 17.7 us against 20.6 us for the register-
+ * ring tile schedule; 3 / 4 / 5 stages 18.1 / 17.7 / 18.0 us; staging the
+ * output through LDS for whole-row stores 18.1; 256 x 128 tiles split over
+ * K in 2 or 4 (partners on one XCD, partial sums through L2) 20.9-25.5 us:
+ * the partial sums' traffic costs more than the operand bytes they save.
+ */
+#define APUS_LT_NST 4
+typedef __attribute__((address_space(3))) void apus_lds_void;
+typedef const __attribute__((address_space(1))) void apus_gbl_void;
+/* 16 (or 4) bytes per lane from global memory straight into LDS at
+ * lds + 16 * lane (4 * lane); lds must be the same in every lane */
+__device__ __forceinline__ void apus_g2lds16(const void *g, unsigned lds) {
+    __builtin_amdgcn_global_load_lds((apus_gbl_void *)g,
+                                     (apus_lds_void *)(uintptr_t)__builtin_amdgcn_readfirstlane(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void apus_g2lds4(const void *g, unsigned lds) {
+    __builtin_amdgcn_global_load_lds((apus_gbl_void *)g,
+                                     (apus_lds_void *)(uintptr_t)__builtin_amdgcn_readfirstlane(lds), 4, 0, 0);
+}
+template <int N>
+__device__ __forceinline__ void apus_wait_vm() { asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+template <int NQ>
+__global__ __launch_bounds__(512, 1) void apus_gemm_lds_kernel(ApusGemmArgs args) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int NST = APUS_LT_NST < NQ ? APUS_LT_NST : NQ;
+    constexpr int K = NQ * 128;
+    constexpr int BM = 64, AB = BM * 128, STB = AB + 128 * 128;
+    constexpr int LA = BM / 8, LPW = (LA + 16) / 8;
+    constexpr int SI = NQ;                     /* scale loads: one per group (64 rows) */
+    static_assert(SI % 8 == 0, "scale loads");
+    const ApusGemmEnt ent = args.ent0;
+    float *lsc = reinterpret_cast<float *>(lds + NST * STB);     /* [q][64 rows] fp32 */
+    const int M = ent.M;
+    const int MT = (M + BM - 1) / BM, tiles = MT * (args.O >> 7);
+    const int b = blockIdx.x;
+    const int t = (tiles & 7) == 0 ? (b & 7) * (tiles >> 3) + (b >> 3) : b;
+    const int mb = t % MT, nb = t / MT;
+    const int m0 = mb * BM, n0 = nb * 128;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;
+    const unsigned lbase = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+    /* this wave's loads of a stage: activation instructions ii < LA (8 rows
+     * each: lane -> row 8 ii + lane / 8, LDS slot lane % 8 holding 16-byte
+     * chunk (lane % 8) ^ swizzle(row)), then weight fragments */
+    const uint8_t *src[LPW];
+    unsigned dst[LPW], qs[LPW];
+#pragma unroll
+    for (int u = 0; u < LPW; ++u) {
+        const int ii = wave * LPW + u;
+        if (ii < LA) {
+            const int lr = 8 * ii + (lane >> 3), p = lane & 7;
+            const int row = ent.a0 + (m0 + lr < M ? m0 + lr : M - 1);
+            const int sw = ((lr & 15) ^ ((lr & 15) >> 3)) & 7;
+            src[u] = args.acodes + (size_t)row * K + (p ^ sw) * 16;
+            dst[u] = ii * 1024;
+            qs[u] = 128;
+        } else {
+            const int f = (ii - LA) >> 1, h = (ii - LA) & 1;
+            src[u] = ent.w + ((size_t)((n0 >> 4) + f) * NQ) * 2048 + h * 1024 + lane * 16;
+            dst[u] = AB + f * 2048 + h * 1024;
+            qs[u] = 2048;
+        }
+    }
+    auto issue = [&](int q, int slot) {
+#pragma unroll
+        for (int u = 0; u < LPW; ++u) apus_g2lds16(src[u] + q * qs[u], lbase + slot * STB + dst[u]);
+    };
+#pragma unroll
+    for (int u = 0; u < SI / 8; ++u) {
+        const int q = wave * (SI / 8) + u;
+        const int row = ent.a0 + (m0 + lane < M ? m0 + lane : M - 1);
+        apus_g2lds4(args.ascale + (size_t)row * NQ + q, lbase + NST * STB + q * BM * 4);
+    }
+#pragma unroll
+    for (int st = 0; st < NST; ++st) issue(st, st);
+    const uint8_t *wsp = ent.ws + (size_t)nb * NQ;     /* 128 x 128 tile scales of this block */
+    unsigned sbw[NQ / 4];
+#pragma unroll
+    for (int i = 0; i < NQ / 4; ++i) sbw[i] = __builtin_amdgcn_readfirstlane(apus_gld<unsigned>(wsp + 4 * i));
+
+    apus_v4f acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+    struct Frag { apus_v8i a, b[4]; int sa; };
+    const int arow = wm * 16 + r;
+    const int sw = (r ^ (r >> 3)) & 7;
+    auto read_frag = [&](Frag &f, int q) {
+        const uint8_t *stg = lds + (q % NST) * STB;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint8_t *p = stg + AB + (wn * 4 + i) * 2048 + lane * 16;
+            const apus_v4u lo = *reinterpret_cast<const apus_v4u *>(p);
+            const apus_v4u hi = *reinterpret_cast<const apus_v4u *>(p + 1024);
+            f.b[i] = apus_v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        }
+        const uint8_t *p = stg + arow * 128;
+        const apus_v4u lo = *reinterpret_cast<const apus_v4u *>(p + ((g ^ sw) << 4));
+        const apus_v4u hi = *reinterpret_cast<const apus_v4u *>(p + (((4 + g) ^ sw) << 4));
+        f.a = apus_v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        f.sa = (int)apus_e8m0_of(lsc[q * BM + arow]);
+    };
+    /* stage q is in LDS once at most (stages issued after it) x LPW loads
+     * are in flight: NST - 1 stages follow stage 0 before the loop; in the
+     * loop stage_ready(q) runs before stage q + NST - 1 is issued */
+    auto stage_ready = [&](int q) {
+        const int last = q == 0 ? NST - 1 : (q + NST - 2 < NQ - 1 ? q + NST - 2 : NQ - 1);
+        const int ahead = last - q;
+        if (ahead >= 3) apus_wait_vm<3 * LPW>();
+        else if (ahead == 2) apus_wait_vm<2 * LPW>();
+        else if (ahead == 1) apus_wait_vm<LPW>();
+        else apus_wait_vm<0>();
+        apus_lds_barrier();
+    };
+    static_assert(NST <= 4, "stage_ready waits for at most 3 stages ahead");
+    Frag fr[2];
+    stage_ready(0);
+    read_frag(fr[0], 0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        if (q + 1 < NQ) {
+            stage_ready(q + 1);
+            if (q + NST < NQ) issue(q + NST, (q + NST) % NST);
+            read_frag(fr[(q + 1) & 1], q + 1);
+        }
+        const Frag &f = fr[q & 1];
+        const int sbq = (int)((sbw[q >> 2] >> (8 * (q & 3))) & 0xffu);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            acc[i] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(f.a, f.b[i], acc[i], f.sa, sbq);
+    }
+    /* lane holds D[4g + j][r]: token m0 + 16 wm + 4 g + j, weight row n0 + 64 wn + 16 i + r */
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int mm = m0 + wm * 16 + 4 * g + j;
+        if (mm < M) {
+            float *d = ent.out + (size_t)(ent.o0 + mm) * args.ldo + n0 + wn * 64 + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v = acc[i][j];
+                if (args.round_out) v = apus_bf16_rne(v);
+                apus_gst<float>(d + i * 16, v);
+            }
+        }
+    }
+}
+
+/* launch the LDS tile schedule (returns false where it does not apply) */
+template <int NQ>
+bool apus_launch_lds_tile(const ApusGemmArgs &a, hipStream_t st) {
+    constexpr int NST = APUS_LT_NST < NQ ? APUS_LT_NST : NQ;
+    constexpr size_t lds = (size_t)NST * (64 + 128) * 128 + 64 * NQ * 4;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&apus_gemm_lds_kernel<NQ>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        (int)lds);
+    if (attr != hipSuccess) return false;
+    const int tiles = (a.ent0.M + 63) / 64 * (a.O / 128);
+    hipLaunchKernelGGL(apus_gemm_lds_kernel<NQ>, dim3(tiles), dim3(512), lds, st, a);
+    return true;
+}
+
+/*
  * One-token MoE dispatch kernels (few routed pairs, MXFP4 experts; with SH,
  * also the FP8 shared expert of each token in the same two launches).
  *
@@ -2276,6 +2454,16 @@ bool apus_pre_ra_w13() {
     return on;
 }
 
+/* the LDS tile schedule for dense FP8 GEMMs (APUS_HIP_LDS_TILE=0 turns it
+ * off: the register-ring tile schedule, identical bits) */
+bool apus_lds_tile_on() {
+    static const bool on = [] {
+        const char *e = getenv("APUS_HIP_LDS_TILE");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
 int apus_dec_ks(size_t row_tiles) {
     static const int forced = [] {
         const char *e = getenv("APUS_HIP_DEC_KS");
@@ -2431,6 +2619,17 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
 #endif
 
 #define APUS_TILE(NQ, PD) hipLaunchKernelGGL((apus_gemm_tile_kernel<WFC, NQ, (PD * APUS_TILE_PDX < NQ ? PD * APUS_TILE_PDX : NQ), APUS_TILE_DA, APUS_TILE_TM, APUS_TILE_NW(NQ)>), gt, bt, 0, st, *a)
+        /* FP8 on tiled weights, plain row ranges: the LDS tile schedule */
+        if (wfmt == APUS_W_FP8 && a->wtiled && !a->ent0.arows && !a->ent0.orows && apus_lds_tile_on()) {
+            bool ok = false;
+            switch (a->K) {
+            case 1024: ok = apus_launch_lds_tile<8>(*a, st); break;
+            case 2048: ok = apus_launch_lds_tile<16>(*a, st); break;
+            case 4096: ok = apus_launch_lds_tile<32>(*a, st); break;
+            default:   ok = apus_launch_lds_tile<64>(*a, st); break;
+            }
+            if (ok) return hipGetLastError();
+        }
         if (wfmt == APUS_W_FP4) {
             constexpr int WFC = APUS_W_FP4;
             switch (a->K) {

@@ -11,7 +11,9 @@ Cases (all seeded, the same in every run):
 * the whole MoE sublayer at s = 8 (router, top-k, routed, FP8 shared
   expert, sum): out, routed, shared;
 * dense decode-schedule launches: an FP8 [4096, 4096] GEMV at M = 1 and a
-  12-entry MXFP4 [2048, 4096] grouped GEMV (inputs saved for the oracle).
+  12-entry MXFP4 [2048, 4096] grouped GEMV; dense tile-schedule launches:
+  FP8 GEMMs of 100 x 512 x 4096 and 70 x 384 x 2048 (inputs saved for the
+  oracle).
 """
 import ctypes as C
 import os
@@ -64,6 +66,13 @@ def dense(rng, out):
         ents.append((w4, ws4, 0, 1))
         out[f"fp4_w{i}"], out[f"fp4_ws{i}"] = w4, ws4
     out["fp4_c"], out["fp4_s"] = c4, s4
+    # dense FP8 GEMMs with more than 8 rows (the tile schedules; weights kept
+    # MFMA-tiled by the dense cache)
+    for name, (M, O, K) in (("t1", (100, 512, 4096)), ("t2", (70, 384, 2048))):
+        w, ws = fp8_weights(rng, O, K)
+        c, sc = hip.act_quant(acts(rng, M, K))
+        out[f"{name}_w"], out[f"{name}_ws"], out[f"{name}_c"], out[f"{name}_s"] = w, ws, c, sc
+        out[f"{name}_y"] = hip.fp8_gemm(w, ws, c, sc)
     for i, y in enumerate(hip.fp4_gemm_grouped(ents, c4, s4, 2048)):
         out[f"fp4_y{i}"] = y
 

@@ -13,6 +13,10 @@ outputs with a child run without switches:
   APUS_HIP_LAYER1=0 (two launches per one-token layer): the routed dispatch
   keeps one accumulation order in every schedule, so y and the h codes must
   be bit-identical, and so must the sublayer's outputs;
+* APUS_HIP_LDS_TILE=0 (dense FP8 GEMMs with more than 8 rows on the
+  register-ring tile schedule instead of the LDS one): both form one chain
+  per output over the 128-groups in order, so the dense outputs must be
+  bit-identical too;
 * APUS_HIP_DEC_KS=1 / 2 / 4 (waves splitting K in the few-row schedule):
   dense outputs change only in fp32 summation order, so they are held to
   the oracle's bars (max-rel 1e-3, err/esc 1e-4); routed outputs stay
@@ -36,7 +40,7 @@ pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
 PROBE = os.path.join(HERE, "switch_probe.py")
 SWITCHES = ["APUS_HIP_PRE_RA", "APUS_HIP_PRE_RA13", "APUS_HIP_DEC_KS", "APUS_HIP_PAIR13_WIDE",
-            "APUS_HIP_MOE_PAIRS", "APUS_HIP_MOE_SIDE", "APUS_HIP_LAYER1"]
+            "APUS_HIP_MOE_PAIRS", "APUS_HIP_MOE_SIDE", "APUS_HIP_LAYER1", "APUS_HIP_LDS_TILE"]
 
 
 def _probe(tmp_path, name, env_set):
@@ -68,7 +72,7 @@ def _same(a, b):
                                      ("APUS_HIP_MOE_PAIRS", "0"), ("APUS_HIP_MOE_PAIRS", "64"),
                                      ("APUS_HIP_MOE_SIDE", "0"), ("APUS_HIP_LAYER1", "0"),
                                      ("APUS_HIP_DEC_KS", "1"), ("APUS_HIP_DEC_KS", "2"),
-                                     ("APUS_HIP_DEC_KS", "4")])
+                                     ("APUS_HIP_DEC_KS", "4"), ("APUS_HIP_LDS_TILE", "0")])
 def test_switch(oracle, tmp_path, default_run, var, val):
     got = _probe(tmp_path, f"{var}_{val}", {var: val})
     base = default_run
@@ -86,6 +90,12 @@ def test_switch(oracle, tmp_path, default_run, var, val):
     if var != "APUS_HIP_DEC_KS":
         for k in keys:
             assert _same(got[k], base[k]), k
+    for name in ("t1", "t2"):
+        y = got[f"{name}_y"]
+        assert _same(y, base[f"{name}_y"]), f"{var}={val}: {name} differs from the default schedule"
+        args = (got[f"{name}_w"], got[f"{name}_ws"], got[f"{name}_c"], got[f"{name}_s"])
+        truth, esc = oracle.fp8_truth(*args)
+        assert max_rel(y, oracle.fp8_gemm(*args)) <= 1e-3 and err_esc(y, truth, esc) <= 1e-4, name
     want = oracle.fp8_gemm(got["fp8_w"], got["fp8_ws"], got["fp8_c"], got["fp8_s"])
     truth, esc = oracle.fp8_truth(got["fp8_w"], got["fp8_ws"], got["fp8_c"], got["fp8_s"])
     assert max_rel(got["fp8_y"], want) <= 1e-3
