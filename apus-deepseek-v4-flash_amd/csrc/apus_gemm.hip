@@ -1317,6 +1317,9 @@ __global__ __launch_bounds__(64 * NW) void apus_gemm_tile_kernel(ApusGemmArgs ar
  * the partial sums' traffic costs more than the operand bytes they save.
  */
 #define APUS_LT_NST 4
+#ifndef APUS_PRE_LDS_NST
+#define APUS_PRE_LDS_NST 3
+#endif
 typedef __attribute__((address_space(3))) void apus_lds_void;
 typedef const __attribute__((address_space(1))) void apus_gbl_void;
 /* 16 (or 4) bytes per lane from global memory straight into LDS at
@@ -1469,6 +1472,177 @@ bool apus_launch_lds_tile(const ApusGemmArgs &a, hipStream_t st) {
     if (attr != hipSuccess) return false;
     const int tiles = (a.ent0.M + 63) / 64 * (a.O / 128);
     hipLaunchKernelGGL(apus_gemm_lds_kernel<NQ>, dim3(tiles), dim3(512), lds, st, a);
+    return true;
+}
+
+/*
+ * LDS many-row schedule for the routed MXFP4 experts (grouped launches from
+ * the route kernel's work list, MFMA-tiled weights, K 2048 / 4096): one
+ * workgroup per (64-row chunk of an expert, 128 weight rows), whole K, both
+ * operands global -> LDS through NST stages of one 128-group as in
+ * apus_gemm_lds_kernel: per stage 8 loads of 8 gathered activation rows
+ * (row table of the entry) and 8 loads of 1 KB weight fragments (FP4: a
+ * 16-row tile's 128-group is 1 KB); the weight scales of the 8 tiles (one
+ * contiguous block) and the chunk's activation scales go to LDS up front.
+ * 8 waves of 16 chunk rows x 64 weight rows; waves whose 16 rows lie past
+ * the chunk's end skip their MFMAs. Accumulation per output: one chain over
+ * the 128-groups (w1/w3), or with FOLD four chains from zero over the
+ * quarters of K added left to right (w2), the orders of the one-token
+ * kernels, so results equal the other schedules bit for bit.
+ */
+template <int NS, bool FOLD, int NST>
+__global__ __launch_bounds__(512, 2) void apus_gemm_prefill_lds_kernel(ApusGemmArgs args) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    constexpr int K = NS * 512, NQ = NS * 4, ROWS = 64;
+    constexpr int AB = ROWS * 128, STB = AB + 8 * 1024;
+    constexpr int SCB = 8 * NS * 256;                          /* weight scales of 8 tiles */
+    static_assert(!FOLD || NS == 4, "K-quarter order at K = 2048");
+    static_assert(NQ % 8 == 0 && SCB % 8192 == 0, "loads per wave");
+    const int2 it = apus_gld<int2>(args.items + blockIdx.y);
+    if (it.x < 0) return;
+    const ApusGemmEnt ent = apus_gld<ApusGemmEnt>(args.ents + it.x);
+    if (ent.M <= args.m_min || (args.m_max > 0 && ent.M > args.m_max)) return;
+    const int c0 = it.y;
+    const int rows = min(ROWS, ent.M - c0);
+    const int n0 = blockIdx.x * 128;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int wm = wave >> 1, wn = wave & 1;
+    uint8_t *lws = lds + NST * STB;                            /* [8 tiles][NS][16 rows][16 B] */
+    float *lsa = reinterpret_cast<float *>(lws + SCB);         /* [q][64 rows] fp32 */
+    const unsigned lbase = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)lds);
+    auto arow_of = [&](int lr) {
+        const int mm = c0 + (lr < rows ? lr : rows - 1);
+        return ent.arows ? apus_gld<int>(ent.arows + mm) : ent.a0 + mm;
+    };
+    /* stage loads of this wave: activation instruction `wave` (8 rows:
+     * lane -> row 8 wave + lane / 8, LDS slot lane % 8 holding 16-byte chunk
+     * (lane % 8) ^ swizzle(row)) and weight tile `wave` */
+    const int alr = 8 * wave + (lane >> 3);
+    const int asw = ((alr & 15) ^ ((alr & 15) >> 3)) & 7;
+    const uint8_t *asrc = args.acodes + (size_t)arow_of(alr) * K + ((lane & 7) ^ asw) * 16;
+    const uint8_t *bsrc = ent.w + ((size_t)((n0 >> 4) + wave) * NQ) * 1024 + lane * 16;
+    auto issue = [&](int q, int slot) {
+        apus_g2lds16(asrc + q * 128, lbase + slot * STB + wave * 1024);
+        apus_g2lds16(bsrc + q * 1024, lbase + slot * STB + AB + wave * 1024);
+    };
+    /* up front: the weight scales (8 tiles x NS slices x 256 B, contiguous)
+     * and the activation scales of the chunk (one dword load per group and
+     * 64 rows) */
+    const uint8_t *wsrc = ent.ws + (size_t)(n0 >> 4) * NS * 256;
+#pragma unroll
+    for (int u = 0; u < SCB / 8192; ++u)
+        apus_g2lds16(wsrc + (size_t)(u * 8 + wave) * 1024 + lane * 16, lbase + NST * STB + (u * 8 + wave) * 1024);
+    const int srow = arow_of(lane);
+#pragma unroll
+    for (int u = 0; u < NQ / 8; ++u) {
+        const int q = u * 8 + wave;
+        apus_g2lds4(args.ascale + (size_t)srow * NQ + q, lbase + NST * STB + SCB + q * ROWS * 4);
+    }
+#pragma unroll
+    for (int st = 0; st < NST; ++st) issue(st, st);
+    constexpr int PRE = SCB / 8192 + NQ / 8;                   /* up-front loads of a wave */
+    (void)PRE;
+
+    apus_v4f acc[4], tot[FOLD ? 4 : 1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+    if constexpr (FOLD) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) tot[i] = apus_v4f{-0.f, -0.f, -0.f, -0.f};
+    }
+    const bool live = wm * 16 < rows;                          /* wave-uniform */
+    const int arow = wm * 16 + r;
+    const int sw = (r ^ (r >> 3)) & 7;
+    struct Frag { apus_v8i a; apus_v4u b[4]; int sa; unsigned sb[4]; };
+    auto read_frag = [&](Frag &f, int q) {
+        const uint8_t *stg = lds + (q % NST) * STB;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tl = wn * 4 + i;
+            f.b[i] = *reinterpret_cast<const apus_v4u *>(stg + AB + tl * 1024 + lane * 16);
+            f.sb[i] = *reinterpret_cast<const unsigned *>(lws + (tl * NS + (q >> 2)) * 256 + r * 16 + (q & 3) * 4);
+        }
+        const uint8_t *p = stg + arow * 128;
+        const apus_v4u lo = *reinterpret_cast<const apus_v4u *>(p + ((g ^ sw) << 4));
+        const apus_v4u hi = *reinterpret_cast<const apus_v4u *>(p + (((4 + g) ^ sw) << 4));
+        f.a = apus_v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+        f.sa = (int)apus_e8m0_of(lsa[q * ROWS + arow]);
+    };
+    /* stage q is in LDS once at most (stages issued after it) x 2 loads are
+     * in flight: NST - 1 stages follow stage 0 before the loop (which also
+     * covers the up-front scale loads, issued first); in the loop
+     * stage_ready(q) runs before stage q + NST - 1 is issued */
+    auto stage_ready = [&](int q) {
+        const int last = q == 0 ? NST - 1 : (q + NST - 2 < NQ - 1 ? q + NST - 2 : NQ - 1);
+        const int ahead = last - q;
+        if (ahead >= 3) apus_wait_vm<6>();
+        else if (ahead == 2) apus_wait_vm<4>();
+        else if (ahead == 1) apus_wait_vm<2>();
+        else apus_wait_vm<0>();
+        apus_lds_barrier();
+    };
+    static_assert(NST <= 4 && NST <= NQ, "stage_ready waits for at most 3 stages ahead");
+    Frag fr[2];
+    stage_ready(0);
+    read_frag(fr[0], 0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+        if (q + 1 < NQ) {
+            stage_ready(q + 1);
+            if (q + NST < NQ) issue(q + NST, (q + NST) % NST);
+            read_frag(fr[(q + 1) & 1], q + 1);
+        }
+        const Frag &f = fr[q & 1];
+        if (live) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const apus_v8i b = apus_v8i{(int)f.b[i].x, (int)f.b[i].y, (int)f.b[i].z, (int)f.b[i].w, 0, 0, 0, 0};
+                acc[i] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(f.a, b, acc[i], f.sa,
+                                                                             (int)((f.sb[i] >> (8 * g)) & 0xffu));
+            }
+        }
+        if constexpr (FOLD) {
+            if ((q & 3) == 3) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    tot[i] += acc[i];
+                    acc[i] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+        }
+    }
+    if (!live) return;
+    /* lane holds D[4g + j][r]: chunk row 16 wm + 4 g + j, weight row n0 + 64 wn + 16 i + r */
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int lr = wm * 16 + 4 * g + j;
+        if (lr < rows) {
+            const int mm = c0 + lr;
+            const int orow = ent.orows ? apus_gld<int>(ent.orows + mm) : ent.o0 + mm;
+            float *d = ent.out + (size_t)orow * args.ldo + n0 + wn * 64 + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float v = FOLD ? tot[FOLD ? i : 0][j] : acc[i][j];
+                if (args.round_out) v = apus_bf16_rne(v);
+                apus_gst<float>(d + i * 16, v);
+            }
+        }
+    }
+}
+
+/* launch the LDS many-row schedule over a work list (returns false where it
+ * does not apply) */
+template <int NS, bool FOLD>
+bool apus_launch_pre_lds(const ApusGemmArgs &p, int n_items, hipStream_t st) {
+    constexpr int NST = APUS_PRE_LDS_NST;
+    constexpr size_t lds = (size_t)NST * (64 * 128 + 8 * 1024) + 8 * NS * 256 + 64 * NS * 4 * 4;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&apus_gemm_prefill_lds_kernel<NS, FOLD, NST>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess || p.O % 128 || !p.wtiled) return false;
+    hipLaunchKernelGGL((apus_gemm_prefill_lds_kernel<NS, FOLD, NST>), dim3(p.O / 128, n_items), dim3(512), lds,
+                       st, p);
     return true;
 }
 
@@ -2454,6 +2628,19 @@ bool apus_pre_ra_w13() {
     return on;
 }
 
+/* the LDS many-row schedule for work-list launches (APUS_HIP_PRE_LDS=0
+ * turns it off: the resident-activation or prefill schedule, identical
+ * bits; 1, the default: one-chain launches only; 2: the K-quarter ones as
+ * well) */
+int apus_pre_lds_mode() {
+    static const int m = [] {
+        const char *e = getenv("APUS_HIP_PRE_LDS");
+        return e ? atoi(e) : 1;
+    }();
+    return m;
+}
+bool apus_pre_lds_on() { return apus_pre_lds_mode() != 0; }
+
 /* the LDS tile schedule for dense FP8 GEMMs (APUS_HIP_LDS_TILE=0 turns it
  * off: the register-ring tile schedule, identical bits) */
 bool apus_lds_tile_on() {
@@ -2580,6 +2767,19 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
             /* activations resident in LDS, NCB column blocks per workgroup
              * (work-list launches whose column blocks divide evenly) */
             const bool ra = a->items && TT4 == 4 && a->O % (128 * APUS_PRE_RA_NCB) == 0 && apus_pre_ra_on();
+            /* one-chain work lists on tiled weights (the routed w1/w3): the
+             * LDS many-row schedule (config 3 w1/w3 126 -> 121 us; for the
+             * K-quarter w2 at K = 2048 it measured 89.5 against 78.9 us for
+             * the resident-activation schedule, which keeps the chunk's
+             * activations in LDS across four column blocks, so w2 stays
+             * there; APUS_HIP_PRE_LDS=2 runs it for w2 as well) */
+            if (a->items && a->wtiled && TT4 == 4 && apus_pre_lds_on()) {
+                bool ok = false;
+                if (a->kchain == 4) ok = apus_pre_lds_mode() == 2 && a->K == 2048 && apus_launch_pre_lds<4, true>(p, n_ent, st);
+                else ok = a->K == 4096 ? apus_launch_pre_lds<8, false>(p, n_ent, st)
+                                       : apus_launch_pre_lds<4, false>(p, n_ent, st);
+                if (ok) return hipGetLastError();
+            }
             if (a->kchain == 4) {
                 if (a->K == 4096) {
                     hipLaunchKernelGGL((apus_gemm_prefill_kernel<APUS_W_FP4, 8, TT4, APUS_PRE_PD4, true>), gp, bp, 0, st, p);

@@ -5,8 +5,11 @@ tests/switch_probe.py in a child process with one switch set (one process on
 the GPU at a time: the child runs while this one waits) and compares its
 outputs with a child run without switches:
 
-* APUS_HIP_PRE_RA=0 / APUS_HIP_PRE_RA13=0 (many-row w2 / w1-w3 on the
-  double-buffered prefill schedule instead of the resident-activation one),
+* APUS_HIP_PRE_LDS=0 / 2 (many-row w1/w3 work items on the resident-
+  activation schedule instead of the LDS one / the w2 ones on the LDS
+  schedule too), with APUS_HIP_PRE_RA=0 /
+  APUS_HIP_PRE_RA13=0 as well (many-row w2 / w1-w3 on the double-buffered
+  prefill schedule),
   APUS_HIP_PAIR13_WIDE=0 / 1 (narrow or wide one-token w1/w3 workgroups),
   APUS_HIP_MOE_PAIRS=0 / 64 (always sort by expert / per-pair kernels up to
   64 pairs), APUS_HIP_MOE_SIDE=0 (the shared expert on the caller's stream),
@@ -39,8 +42,9 @@ pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 PROBE = os.path.join(HERE, "switch_probe.py")
-SWITCHES = ["APUS_HIP_PRE_RA", "APUS_HIP_PRE_RA13", "APUS_HIP_DEC_KS", "APUS_HIP_PAIR13_WIDE",
-            "APUS_HIP_MOE_PAIRS", "APUS_HIP_MOE_SIDE", "APUS_HIP_LAYER1", "APUS_HIP_LDS_TILE"]
+SWITCHES = ["APUS_HIP_PRE_LDS", "APUS_HIP_PRE_RA", "APUS_HIP_PRE_RA13", "APUS_HIP_DEC_KS",
+            "APUS_HIP_PAIR13_WIDE", "APUS_HIP_MOE_PAIRS", "APUS_HIP_MOE_SIDE", "APUS_HIP_LAYER1",
+            "APUS_HIP_LDS_TILE"]
 
 
 def _probe(tmp_path, name, env_set):
@@ -67,14 +71,21 @@ def _same(a, b):
     return a.shape == b.shape and np.array_equal(a.view(np.uint8), b.view(np.uint8))
 
 
-@pytest.mark.parametrize("var,val", [("APUS_HIP_PRE_RA", "0"), ("APUS_HIP_PRE_RA13", "0"),
-                                     ("APUS_HIP_PAIR13_WIDE", "0"), ("APUS_HIP_PAIR13_WIDE", "1"),
-                                     ("APUS_HIP_MOE_PAIRS", "0"), ("APUS_HIP_MOE_PAIRS", "64"),
-                                     ("APUS_HIP_MOE_SIDE", "0"), ("APUS_HIP_LAYER1", "0"),
-                                     ("APUS_HIP_DEC_KS", "1"), ("APUS_HIP_DEC_KS", "2"),
-                                     ("APUS_HIP_DEC_KS", "4"), ("APUS_HIP_LDS_TILE", "0")])
-def test_switch(oracle, tmp_path, default_run, var, val):
-    got = _probe(tmp_path, f"{var}_{val}", {var: val})
+CASES = [{"APUS_HIP_PRE_LDS": "0"}, {"APUS_HIP_PRE_LDS": "2"},
+         {"APUS_HIP_PRE_LDS": "0", "APUS_HIP_PRE_RA": "0"},
+         {"APUS_HIP_PRE_LDS": "0", "APUS_HIP_PRE_RA13": "0"},
+         {"APUS_HIP_PAIR13_WIDE": "0"}, {"APUS_HIP_PAIR13_WIDE": "1"},
+         {"APUS_HIP_MOE_PAIRS": "0"}, {"APUS_HIP_MOE_PAIRS": "64"},
+         {"APUS_HIP_MOE_SIDE": "0"}, {"APUS_HIP_LAYER1": "0"},
+         {"APUS_HIP_DEC_KS": "1"}, {"APUS_HIP_DEC_KS": "2"}, {"APUS_HIP_DEC_KS": "4"},
+         {"APUS_HIP_LDS_TILE": "0"}]
+
+
+@pytest.mark.parametrize("env", CASES, ids=lambda e: ",".join(f"{k[9:]}={v}" for k, v in e.items()))
+def test_switch(oracle, tmp_path, default_run, env):
+    var = "APUS_HIP_DEC_KS" if "APUS_HIP_DEC_KS" in env else next(iter(env))
+    val = env[var]
+    got = _probe(tmp_path, "_".join(f"{k}_{v}" for k, v in env.items()), env)
     base = default_run
     dense_chain = {"fwd_shared", "fwd_out"} if var == "APUS_HIP_DEC_KS" else set()
     for k in ROUTED:
