@@ -26,6 +26,7 @@ interpreter lock).
 """
 import ctypes as C
 import os
+import sys
 import threading
 from concurrent.futures import ThreadPoolExecutor
 
@@ -126,6 +127,13 @@ def _pool():
     return ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
 
 
+def report(msg):
+    """Stage-check figures go to the real stderr, so they appear in the run's
+    log even when pytest captures the test's output."""
+    print(msg, flush=True)
+    print(f"[fullsize] {msg}", file=sys.__stderr__, flush=True)
+
+
 def _batched_vs_per_token(store, x, idx, wgt):
     yb, hb, eb = store.routed(0, x, idx, wgt, read_h=True)
     s = x.shape[0]
@@ -143,10 +151,10 @@ def _stage_checks(oracle, store, x, idx, wgt, yb, hb, eb, tokens, layer=0, exper
         rs = list(ex.map(lambda t: check_token(oracle, experts, x[t], idx[t], wgt[t], LIMIT, hb[t],
                                                eb[t], yb[t]), tokens))
     for t, r in zip(tokens, rs):
-        print(f"token {t}: experts {[int(e) for e in idx[t]]}: h pinned {r['h_pinned']:.3f}, "
-              f"y pinned {r['y_pinned']:.3f} (all pinned values exact), y max_rel "
-              f"{r['y_max_rel']:.3g}", flush=True)
-    print(f"stage-checked {len(tokens)} of {x.shape[0]} tokens", flush=True)
+        report(f"token {t}: experts {[int(e) for e in idx[t]]}: h pinned {r['h_pinned']:.3f}, "
+               f"y pinned {r['y_pinned']:.3f} (all pinned values exact), y max_rel "
+               f"{r['y_max_rel']:.3g}")
+    report(f"stage-checked {len(tokens)} of {x.shape[0]} tokens")
 
 
 def _bf16_x(rng, s):
@@ -164,7 +172,7 @@ def test_config1_fp8_gemm_m512(hip, oracle, ref):
     rows = np.sort(rng.choice(M, 16, replace=False))
     truth, esc = oracle.fp8_truth(w, ws, c[rows].copy(), s[rows].copy())
     ee = err_esc(got[rows], truth, esc)
-    print(f"config 1 M=512: max_rel {mr:.3g}, err/esc {ee:.3g} on rows {[int(r) for r in rows]}")
+    report(f"config 1 M=512: max_rel {mr:.3g}, err/esc {ee:.3g} on rows {[int(r) for r in rows]}")
     assert mr <= 1e-3 and ee <= 1e-4
 
 
@@ -195,17 +203,17 @@ def test_config3_prefill_moe(hip, oracle, store1):
     with _pool() as ex:
         pin = list(ex.map(lambda tj: check_pair(oracle, experts(top), x[tj[0]], LIMIT,
                                                 hb[tj[0], tj[1]], eb[tj[0], tj[1]]), pairs))
-    print(f"expert {top}: {len(pairs)} pairs ({-(-len(pairs) // 64)} chunks of 64), h stage-checked, "
-          f"pinned {np.mean(pin):.3f}", flush=True)
+    report(f"expert {top}: {len(pairs)} pairs ({-(-len(pairs) // 64)} chunks of 64), h stage-checked, "
+           f"pinned {np.mean(pin):.3f}")
     with_top = np.nonzero((idx == top).any(1))[0]
     tokens = [int(with_top[-1])] + [int(t) for t in rng.choice(s, 8, replace=False)]
     for n in (8, 9):                                  # the few-row / many-row boundary
         es = np.nonzero(counts == n)[0]
         if es.size:
             tokens.append(int(np.nonzero((idx == es[0]).any(1))[0][0]))
-            print(f"expert {int(es[0])} has {n} rows", flush=True)
+            report(f"expert {int(es[0])} has {n} rows")
         else:
-            print(f"no expert with exactly {n} rows in this routing", flush=True)
+            report(f"no expert with exactly {n} rows in this routing")
     rare = np.nonzero((counts[idx] <= 8).any(1))[0]
     tokens.append(int(rare[0]))
     _stage_checks(oracle, store1, x, idx, wgt, yb, hb, eb, sorted(set(tokens)), experts=experts)
@@ -246,8 +254,8 @@ def test_config4_full_footprint(hip, oracle):
         with _pool() as ex:
             rs = list(ex.map(one, CHECKED))
         for l, r in zip(CHECKED, rs):
-            print(f"layer {l}: h pinned {r['h_pinned']:.3f}, y pinned {r['y_pinned']:.3f}, "
-                  f"y max_rel {r['y_max_rel']:.3g}", flush=True)
+            report(f"layer {l}: h pinned {r['h_pinned']:.3f}, y pinned {r['y_pinned']:.3f}, "
+                   f"y max_rel {r['y_max_rel']:.3g}")
         for l in CHECKED:
             nsc = (O // 128) * (K // 128)
             w8 = oracle.fill_bytes(seed, 1 << 40, O * K, 2, first=l * O * K).reshape(O, K)
