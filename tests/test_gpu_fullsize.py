@@ -26,7 +26,6 @@ interpreter lock).
 """
 import ctypes as C
 import os
-import sys
 import threading
 from concurrent.futures import ThreadPoolExecutor
 
@@ -127,11 +126,22 @@ def _pool():
     return ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
 
 
+_TERM = []
+
+
+@pytest.fixture(autouse=True)
+def _terminal(request):
+    _TERM[:] = [request.config.pluginmanager.get_plugin("terminalreporter")]
+    yield
+
+
 def report(msg):
-    """Stage-check figures go to the real stderr, so they appear in the run's
-    log even when pytest captures the test's output."""
+    """Stage-check figures go straight to pytest's terminal, so they appear
+    in the run's log even when the test's output is captured."""
     print(msg, flush=True)
-    print(f"[fullsize] {msg}", file=sys.__stderr__, flush=True)
+    tr = _TERM[0] if _TERM else None
+    if tr is not None:
+        tr.write_line(f"[fullsize] {msg}")
 
 
 def _batched_vs_per_token(store, x, idx, wgt):

@@ -25,6 +25,8 @@ Exact ties (identical gate rows, equal bias) must pick the lowest index, as
 the CPU's strict-greater-than scan does (c/attn.h:668-686).
 """
 import ctypes as C
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -221,7 +223,8 @@ def test_moe_forward_dev_model_shape(hip, oracle, store1, rng, hash_, shared_til
     first = host_expert(oracle, seed, 0, 0, E, dim, inter)
     probe = oracle.moe_forward(cfg, [first] * E, shared, x)
     used = sorted(set(int(e) for e in probe[4].ravel()))
-    host = {e: host_expert(oracle, seed, 0, e, E, dim, inter) for e in used}
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4)) as ex:
+        host = dict(zip(used, ex.map(lambda e: host_expert(oracle, seed, 0, e, E, dim, inter), used)))
     experts = [host.get(e, first) for e in range(E)]
     want = oracle.moe_forward(cfg, experts, shared, x)
     ws = []

@@ -10,6 +10,8 @@ dispatch (apus_hip_moe_routed_dev).
 * store_put / store_get round-trip the six tensors of an expert.
 """
 import ctypes as C
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import pytest
@@ -85,8 +87,12 @@ def stage_check(hip, oracle, st, experts_of, x, idx, wgt, y, wsp, inter, tokens=
     hip._check(L_.apus_hip_moe_routed_h(st, s, topk, wsp.ptr, hc.ptr, he.ptr), "routed_h")
     hcodes = hc.to_array(np.uint8, (s, topk, inter))
     he8 = he.to_array(np.uint8, (s, topk, inter // 128))
-    for t in (range(s) if tokens is None else tokens):
-        r = check_token(oracle, experts_of, x[t], idx[t], wgt[t], limit, hcodes[t], he8[t], y[t])
+    toks = list(range(s) if tokens is None else tokens)
+    # tokens in parallel (the oracle's C loops release the interpreter lock)
+    with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4)) as ex:
+        rs = list(ex.map(lambda t: check_token(oracle, experts_of, x[t], idx[t], wgt[t], limit,
+                                               hcodes[t], he8[t], y[t]), toks))
+    for t, r in zip(toks, rs):
         print(f"token {t}: h pinned {r['h_pinned']:.3f}, y pinned {r['y_pinned']:.3f}, "
               f"y max_rel {r['y_max_rel']:.3g}", flush=True)
 
