@@ -46,3 +46,11 @@ def hip():
 @pytest.fixture
 def rng():
     return np.random.default_rng(20260729)
+
+
+def pytest_terminal_summary(terminalreporter):
+    from helpers import SUMMARY_LINES
+    if SUMMARY_LINES:
+        terminalreporter.section("figures reported by the tests")
+        for line in SUMMARY_LINES:
+            terminalreporter.write_line(line)

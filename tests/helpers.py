@@ -8,6 +8,11 @@ Metrics follow the reference's own gates:
 import numpy as np
 
 
+# lines a test wants in the run's log whatever the capture mode (printed by
+# tests/conftest.py at the end of the session)
+SUMMARY_LINES = []
+
+
 def fp4_weights(rng, O, K, lo=118, hi=130):
     """MXFP4 weight [O, K/2] with uniform nibbles and E8M0 bytes in lo..hi."""
     w = rng.integers(0, 256, (O, K // 2), dtype=np.uint8)

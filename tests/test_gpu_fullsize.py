@@ -32,7 +32,7 @@ from concurrent.futures import ThreadPoolExecutor
 import numpy as np
 import pytest
 
-from helpers import bf16, bf16_linear_ok, err_esc, fp8_weights, max_rel
+from helpers import SUMMARY_LINES, bf16, bf16_linear_ok, err_esc, fp8_weights, max_rel
 from moe_check import check_pair, check_token
 
 pytestmark = pytest.mark.gpu
@@ -126,22 +126,12 @@ def _pool():
     return ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
 
 
-_TERM = []
-
-
-@pytest.fixture(autouse=True)
-def _terminal(request):
-    _TERM[:] = [request.config.pluginmanager.get_plugin("terminalreporter")]
-    yield
-
-
 def report(msg):
-    """Stage-check figures go straight to pytest's terminal, so they appear
-    in the run's log even when the test's output is captured."""
+    """Stage-check figures: printed, and kept for the end-of-run summary
+    (tests/conftest.py prints them even when the test's output is
+    captured)."""
     print(msg, flush=True)
-    tr = _TERM[0] if _TERM else None
-    if tr is not None:
-        tr.write_line(f"[fullsize] {msg}")
+    SUMMARY_LINES.append(f"[fullsize] {msg}")
 
 
 def _batched_vs_per_token(store, x, idx, wgt):
