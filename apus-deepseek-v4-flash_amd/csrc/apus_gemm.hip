@@ -1461,6 +1461,173 @@ __global__ __launch_bounds__(512, 1) void apus_gemm_lds_kernel(ApusGemmArgs args
     }
 }
 
+/*
+ * Narrow schedule for dense FP8 GEMMs with 9..64 rows on tiled weights
+ * (batched decode: a projection of 16-64 tokens). The tile schedules give
+ * such a launch only O / 128 workgroups (32 for a 4096-row weight), each
+ * streaming 512 KB: 14-17 us where M = 1 takes 6.5. Here a workgroup owns one
+ * 16-row weight tile and all M rows (TM 16-row token tiles), and its 4 waves
+ * split K in four contiguous quarters (every fragment then has exactly one
+ * reader). Each wave streams its weight fragments into a register ring and
+ * its activation rows global -> LDS into a wave-private ring (8 whole
+ * 128-byte rows per load, 16-byte chunks XOR-swizzled by row for
+ * conflict-free fragment reads; activation fragments loaded straight into
+ * registers instead measured 6.2 / 12.3 us at M = 16 / 64), PD = 4 groups
+ * ahead (3: 6.2 / 10.8, 2: 6.6 / 11.0). The four partial sums meet in LDS
+ * and are added in K order.
+ * Measured at O = K = 4096 (fresh weight copy per launch): M = 16 5.9 us,
+ * M = 64 10.4 us, against 14.0 / 16.7 on the tile schedules; 8 waves splitting
+ * K 12.9-13.0 at M = 64, 2 waves 13.1, two weight tiles per workgroup
+ * 16.0, four 23.5, whole-K single-wave workgroups 80 (all before the LDS
+ * activation ring).
+ */
+template <int NQ, int TM, int PDM, bool AL>
+__global__ __launch_bounds__(256) void apus_gemm_narrow_kernel(ApusGemmArgs args) {
+    constexpr int K = NQ * 128, NG = NQ / 4, PD = NG < PDM ? NG : PDM;
+    constexpr int NL = 2 + 3 * TM;                   /* vector loads per group */
+    constexpr int SLOT = TM * 2048;                  /* activation bytes per group */
+    __shared__ apus_v4f red[4][TM][64];
+    extern __shared__ __align__(16) uint8_t lring[];    /* AL: 4 waves x PD x SLOT */
+    const ApusGemmEnt ent = args.ent0;
+    const int M = ent.M;
+    const int tile = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int q0 = wave * NG;
+    const uint8_t *ap[TM], *lp[2 * TM];
+    const float *sp[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) {
+        const int row = ent.a0 + (16 * t + r < M ? 16 * t + r : M - 1);
+        ap[t] = args.acodes + (size_t)row * K + g * 16;
+        sp[t] = args.ascale + (size_t)row * NQ;
+        /* LDS loads: instruction (t, hh) brings rows 16 t + 8 hh + lane / 8 */
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int lr = 8 * hh + (lane >> 3);
+            const int rw = ent.a0 + (16 * t + lr < M ? 16 * t + lr : M - 1);
+            const int sw = (lr ^ (lr >> 3)) & 7;
+            lp[2 * t + hh] = args.acodes + (size_t)rw * K + ((lane & 7) ^ sw) * 16;
+        }
+    }
+    uint8_t *wring = lring + (AL ? wave * PD * SLOT : 0);
+    const unsigned wbase = __builtin_amdgcn_readfirstlane((unsigned)(uintptr_t)wring);
+    const uint8_t *bp = ent.w + ((size_t)tile * NQ * 128 + lane) * 16;
+    const uint8_t *wsp = ent.ws + (size_t)(tile >> 3) * NQ + q0;     /* 128 x 128 tile scales */
+    unsigned sbw[(NG + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (NG + 3) / 4; ++i)
+        sbw[i] = __builtin_amdgcn_readfirstlane(apus_gld<unsigned>(wsp + 4 * i));
+    struct Grp { apus_v4u b0, b1, a0[AL ? 1 : TM], a1[AL ? 1 : TM]; float s[TM]; };
+    auto load = [&](Grp &f, int i) {
+        const int q = q0 + i;
+        f.b0 = apus_ld16_stream(bp + (size_t)q * 2048);
+        f.b1 = apus_ld16_stream(bp + (size_t)q * 2048 + 1024);
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            if constexpr (AL) {
+                apus_g2lds16(lp[2 * t] + q * 128, wbase + (i % PD) * SLOT + t * 2048);
+                apus_g2lds16(lp[2 * t + 1] + q * 128, wbase + (i % PD) * SLOT + t * 2048 + 1024);
+            } else {
+                f.a0[t] = apus_gld<apus_v4u>(ap[t] + q * 128);
+                f.a1[t] = apus_gld<apus_v4u>(ap[t] + q * 128 + 64);
+            }
+            f.s[t] = apus_gld<float>(sp[t] + q);
+        }
+        /* the waits below count NL loads per group: keep the compiler from
+         * merging one group's scale loads with the next group's (adjacent
+         * floats of a row) */
+        if constexpr (AL) asm volatile("" ::: "memory");
+    };
+    Grp ring[PD];
+#pragma unroll
+    for (int i = 0; i < PD; ++i) load(ring[i], i);
+    apus_v4f acc[TM];
+#pragma unroll
+    for (int t = 0; t < TM; ++t) acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
+    const int sw = (r ^ (r >> 3)) & 7;
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        Grp &cur = ring[i % PD];
+        if constexpr (AL) {
+            /* group i's loads are complete once only the later groups' are
+             * in flight (loads complete in order) */
+            const int later = NG - 1 - i < PD - 1 ? NG - 1 - i : PD - 1;
+            if (later >= 3) apus_wait_vm<3 * NL>();
+            else if (later == 2) apus_wait_vm<2 * NL>();
+            else if (later == 1) apus_wait_vm<NL>();
+            else apus_wait_vm<0>();
+        }
+        const apus_v8i b = apus_v8i{(int)cur.b0.x, (int)cur.b0.y, (int)cur.b0.z, (int)cur.b0.w,
+                                    (int)cur.b1.x, (int)cur.b1.y, (int)cur.b1.z, (int)cur.b1.w};
+        const int sbq = (int)((sbw[i >> 2] >> (8 * (i & 3))) & 0xffu);
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            apus_v4u lo, hi;
+            if constexpr (AL) {
+                const uint8_t *pp = wring + (i % PD) * SLOT + t * 2048 + r * 128;
+                lo = *reinterpret_cast<const apus_v4u *>(pp + ((g ^ sw) << 4));
+                hi = *reinterpret_cast<const apus_v4u *>(pp + (((4 + g) ^ sw) << 4));
+            } else {
+                lo = cur.a0[AL ? 0 : t];
+                hi = cur.a1[AL ? 0 : t];
+            }
+            const apus_v8i a = apus_v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            acc[t] = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc[t], (int)apus_e8m0_of(cur.s[t]),
+                                                                         sbq);
+        }
+        if constexpr (AL) asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   /* slot read before refill */
+        if (i + PD < NG) load(cur, i + PD);
+    }
+#pragma unroll
+    for (int t = 0; t < TM; ++t) red[wave][t][lane] = acc[t];
+    __syncthreads();
+    if (wave == 0) {
+        /* lane holds D[4g + j][r]: token 16 t + 4 g + j, weight row 16 tile + r;
+         * the four K quarters added in order */
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+            apus_v4f v = red[0][t][lane];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) v += red[w][t][lane];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int mm = 16 * t + 4 * g + j;
+                if (mm < M) {
+                    float x = v[j];
+                    if (args.round_out) x = apus_bf16_rne(x);
+                    apus_gst<float>(ent.out + (size_t)(ent.o0 + mm) * args.ldo + tile * 16 + r, x);
+                }
+            }
+        }
+    }
+}
+
+#ifndef APUS_NARROW_PD
+#define APUS_NARROW_PD 4
+#endif
+#ifndef APUS_NARROW_AL
+#define APUS_NARROW_AL 1
+#endif
+template <int NQ, int TM>
+bool apus_launch_narrow_tm(const ApusGemmArgs &a, hipStream_t st) {
+    constexpr int PD0 = APUS_NARROW_PD, NG = NQ / 4, PD = NG < PD0 ? NG : PD0;
+    constexpr bool AL = APUS_NARROW_AL != 0;
+    constexpr size_t lds = AL ? (size_t)4 * PD * TM * 2048 : 0;
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void *>(&apus_gemm_narrow_kernel<NQ, TM, PD0, AL>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return false;
+    hipLaunchKernelGGL((apus_gemm_narrow_kernel<NQ, TM, PD0, AL>), dim3(a.O / 16), dim3(256), lds, st, a);
+    return true;
+}
+template <int NQ>
+bool apus_launch_narrow(const ApusGemmArgs &a, hipStream_t st) {
+    if (a.ent0.M <= 16) return apus_launch_narrow_tm<NQ, 1>(a, st);
+    if (a.ent0.M <= 32) return apus_launch_narrow_tm<NQ, 2>(a, st);
+    return apus_launch_narrow_tm<NQ, 4>(a, st);
+}
+
 /* launch the LDS tile schedule (returns false where it does not apply) */
 template <int NQ>
 bool apus_launch_lds_tile(const ApusGemmArgs &a, hipStream_t st) {
@@ -2641,6 +2808,16 @@ int apus_pre_lds_mode() {
 }
 bool apus_pre_lds_on() { return apus_pre_lds_mode() != 0; }
 
+/* the narrow schedule for dense FP8 GEMMs of 9..64 rows (APUS_HIP_NARROW=0
+ * turns it off: the tile schedules) */
+bool apus_narrow_on() {
+    static const bool on = [] {
+        const char *e = getenv("APUS_HIP_NARROW");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
 /* the LDS tile schedule for dense FP8 GEMMs (APUS_HIP_LDS_TILE=0 turns it
  * off: the register-ring tile schedule, identical bits) */
 bool apus_lds_tile_on() {
@@ -2819,6 +2996,19 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
 #endif
 
 #define APUS_TILE(NQ, PD) hipLaunchKernelGGL((apus_gemm_tile_kernel<WFC, NQ, (PD * APUS_TILE_PDX < NQ ? PD * APUS_TILE_PDX : NQ), APUS_TILE_DA, APUS_TILE_TM, APUS_TILE_NW(NQ)>), gt, bt, 0, st, *a)
+        /* FP8 on tiled weights, plain row ranges, up to 64 rows: the narrow
+         * schedule */
+        if (wfmt == APUS_W_FP8 && a->wtiled && !a->ent0.arows && !a->ent0.orows && a->ent0.M <= 64 &&
+            apus_narrow_on()) {
+            bool ok = false;
+            switch (a->K) {
+            case 1024: ok = apus_launch_narrow<8>(*a, st); break;
+            case 2048: ok = apus_launch_narrow<16>(*a, st); break;
+            case 4096: ok = apus_launch_narrow<32>(*a, st); break;
+            default:   ok = apus_launch_narrow<64>(*a, st); break;
+            }
+            if (ok) return hipGetLastError();
+        }
         /* FP8 on tiled weights, plain row ranges: the LDS tile schedule */
         if (wfmt == APUS_W_FP8 && a->wtiled && !a->ent0.arows && !a->ent0.orows && apus_lds_tile_on()) {
             bool ok = false;

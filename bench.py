@@ -275,7 +275,8 @@ def bench_fp4_gemv(H, dev, steps, warmup, O=2048, K=4096, copies=None, group=12,
 # ------------------------------------------------------------------ config 1
 
 def bench_fp8(H, dev, steps, O=4096, K=4096):
-    """Config 1: FP8 [4096, 4096] GEMV (M = 1) and GEMM (M = 512) on
+    """Config 1: FP8 [4096, 4096] GEMV (M = 1) and GEMM (M = 512), and the
+    same projection at batched-decode sizes M = 16, 64, on
     MFMA-tiled weights; every timed and warm-up launch reads its own weight
     copy (steps + 4 copies, 4.4 GB at 256 steps), so each launch streams its
     16.8 MB from HBM."""
@@ -294,7 +295,7 @@ def bench_fp8(H, dev, steps, O=4096, K=4096):
     dev.free(w)
     w = tw
     res = {}
-    for M in (1, 512):
+    for M in (1, 16, 64, 512):
         x = np.random.default_rng(1).standard_normal((M, K)).astype(np.float32)
         dx = dev.upload(x)
         codes, scales = dev.alloc(M * K), dev.alloc(M * K // 128 * 4)
@@ -307,7 +308,7 @@ def bench_fp8(H, dev, steps, O=4096, K=4096):
                                              scales.ptr, out.ptr + (i % 2) * M * O * 4, M, O, K,
                                              H.W_TILED), "fp8 gemm")
 
-        n = steps if M == 1 else max(10, steps // 10)
+        n = steps if M == 1 else max(10, steps // (4 if M <= 64 else 10))
         # eager launches queued behind a device-side hold, as the headline
         # (a graph replay of these GEMMs measured slower than the launches
         # themselves); warm-up on copies the timed launches do not read
@@ -905,6 +906,9 @@ def main():
         extras["config1_fp8_M1_GBs"] = round(f8["M1"]["gbs"], 1)
         extras["config1_fp8_M1_us"] = round(f8["M1"]["us"], 2)
         extras["config1_fp8_M512_TFLOPs"] = round(f8["M512"]["tflops"], 1)
+        for mm in (16, 64):   # batched-decode sizes of the same projection
+            extras[f"fp8_4096x4096_M{mm}_us"] = round(f8[f"M{mm}"]["us"], 2)
+            extras[f"fp8_4096x4096_M{mm}_GBs"] = round(f8[f"M{mm}"]["gbs"], 1)
         extras["config1_fp8_M512_us"] = round(f8["M512"]["us"], 2)
     if not args.skip_extras and want("attn"):
         hd = bench_head(H, dev)

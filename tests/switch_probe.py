@@ -12,8 +12,8 @@ Cases (all seeded, the same in every run):
   expert, sum): out, routed, shared;
 * dense decode-schedule launches: an FP8 [4096, 4096] GEMV at M = 1 and a
   12-entry MXFP4 [2048, 4096] grouped GEMV; dense tile-schedule launches:
-  FP8 GEMMs of 100 x 512 x 4096 and 70 x 384 x 2048 (inputs saved for the
-  oracle).
+  FP8 GEMMs of 100 x 512 x 4096 and 70 x 384 x 2048, and of 48, 12 and 29
+  rows (the narrow schedule) (inputs saved for the oracle).
 """
 import ctypes as C
 import os
@@ -68,7 +68,8 @@ def dense(rng, out):
     out["fp4_c"], out["fp4_s"] = c4, s4
     # dense FP8 GEMMs with more than 8 rows (the tile schedules; weights kept
     # MFMA-tiled by the dense cache)
-    for name, (M, O, K) in (("t1", (100, 512, 4096)), ("t2", (70, 384, 2048))):
+    for name, (M, O, K) in (("t1", (100, 512, 4096)), ("t2", (70, 384, 2048)), ("t3", (48, 512, 4096)),
+                            ("t4", (12, 256, 2048)), ("t5", (29, 384, 4096))):
         w, ws = fp8_weights(rng, O, K)
         c, sc = hip.act_quant(acts(rng, M, K))
         out[f"{name}_w"], out[f"{name}_ws"], out[f"{name}_c"], out[f"{name}_s"] = w, ws, c, sc

@@ -19,7 +19,9 @@ outputs with a child run without switches:
 * APUS_HIP_LDS_TILE=0 (dense FP8 GEMMs with more than 8 rows on the
   register-ring tile schedule instead of the LDS one): both form one chain
   per output over the 128-groups in order, so the dense outputs must be
-  bit-identical too;
+  bit-identical too; APUS_HIP_NARROW=0 (9..64-row dense FP8 GEMMs on the
+  tile schedule instead of the narrow one, which splits K in four): those
+  outputs held to the oracle's bars;
 * APUS_HIP_DEC_KS=1 / 2 / 4 (waves splitting K in the few-row schedule):
   dense outputs change only in fp32 summation order, so they are held to
   the oracle's bars (max-rel 1e-3, err/esc 1e-4); routed outputs stay
@@ -44,7 +46,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PROBE = os.path.join(HERE, "switch_probe.py")
 SWITCHES = ["APUS_HIP_PRE_LDS", "APUS_HIP_PRE_RA", "APUS_HIP_PRE_RA13", "APUS_HIP_DEC_KS",
             "APUS_HIP_PAIR13_WIDE", "APUS_HIP_MOE_PAIRS", "APUS_HIP_MOE_SIDE", "APUS_HIP_LAYER1",
-            "APUS_HIP_LDS_TILE"]
+            "APUS_HIP_LDS_TILE", "APUS_HIP_NARROW"]
 
 
 def _probe(tmp_path, name, env_set):
@@ -78,7 +80,7 @@ CASES = [{"APUS_HIP_PRE_LDS": "0"}, {"APUS_HIP_PRE_LDS": "2"},
          {"APUS_HIP_MOE_PAIRS": "0"}, {"APUS_HIP_MOE_PAIRS": "64"},
          {"APUS_HIP_MOE_SIDE": "0"}, {"APUS_HIP_LAYER1": "0"},
          {"APUS_HIP_DEC_KS": "1"}, {"APUS_HIP_DEC_KS": "2"}, {"APUS_HIP_DEC_KS": "4"},
-         {"APUS_HIP_LDS_TILE": "0"}]
+         {"APUS_HIP_LDS_TILE": "0"}, {"APUS_HIP_NARROW": "0"}]
 
 
 @pytest.mark.parametrize("env", CASES, ids=lambda e: ",".join(f"{k[9:]}={v}" for k, v in e.items()))
@@ -101,9 +103,13 @@ def test_switch(oracle, tmp_path, default_run, env):
     if var != "APUS_HIP_DEC_KS":
         for k in keys:
             assert _same(got[k], base[k]), k
-    for name in ("t1", "t2"):
+    for name in ("t1", "t2", "t3", "t4", "t5"):
+        if var == "APUS_HIP_NARROW" and name in ("t3", "t4", "t5"):
+            continue    # another K split: held to the oracle's bars below
         y = got[f"{name}_y"]
         assert _same(y, base[f"{name}_y"]), f"{var}={val}: {name} differs from the default schedule"
+    for name in ("t1", "t2", "t3", "t4", "t5"):
+        y = got[f"{name}_y"]
         args = (got[f"{name}_w"], got[f"{name}_ws"], got[f"{name}_c"], got[f"{name}_s"])
         truth, esc = oracle.fp8_truth(*args)
         assert max_rel(y, oracle.fp8_gemm(*args)) <= 1e-3 and err_esc(y, truth, esc) <= 1e-4, name

@@ -14,7 +14,7 @@ import ctypes as C
 import numpy as np
 import pytest
 
-from helpers import acts, err_esc, fp4_weights, fp8_weights, max_rel
+from helpers import acts, bf16_linear_ok, err_esc, fp4_weights, fp8_weights, max_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -110,7 +110,9 @@ def test_tiled_grouped_equals_rowmajor(hip, oracle, rng, fmt, O, K, Ms):
                                        (1, 40, 256, 8192), (0, 2, 256, 1024)])
 def test_tiled_dense(hip, oracle, rng, fmt, M, O, K):
     """Dense GEMM entry points on tiled weights: more than 8 rows (tile
-    schedule, bitwise equal to row-major) and few rows (oracle bar)."""
+    schedule, bitwise equal to row-major; FP8 with 9..64 rows runs the narrow
+    schedule, whose four K quarters add in another order: oracle bar) and few
+    rows (oracle bar)."""
     L = hip.lib()
     w, ws = (fp4_weights if fmt == 0 else fp8_weights)(rng, O, K)
     c, s = oracle.act_quant(acts(rng, M, K, 2.0))
@@ -124,17 +126,22 @@ def test_tiled_dense(hip, oracle, rng, fmt, M, O, K):
         hip._check(fn(pw.ptr, pws.ptr, dc.ptr, ds.ptr, do.ptr, M, O, K, flag), "gemm")
         hip._check(L.apus_hip_synchronize(), "sync")
         outs.append(do.to_array(np.float32, (M, O)).copy())
-    if M > 8:
+    if M > 8 and not (fmt == 1 and M <= 64):
         assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
-    want = (oracle.fp4_gemm if fmt == 0 else oracle.fp8_gemm)(w, ws, c, s)
+    args = (w, ws, c, s)
+    want = (oracle.fp4_gemm if fmt == 0 else oracle.fp8_gemm)(*args)
+    truth, esc = (oracle.fp4_truth if fmt == 0 else oracle.fp8_truth)(*args)
     assert max_rel(outs[1], want) <= 1e-3
+    assert err_esc(outs[1], truth, esc) <= 1e-4
 
 
 @pytest.mark.parametrize("fmt,M,O,K", [(1, 1, 4096, 4096), (0, 6, 2048, 4096), (1, 20, 1024, 2048),
                                        (1, 8, 1024, 8192), (0, 1, 512, 1024)])
-def test_tiled_linear_dev(hip, rng, fmt, M, O, K):
+def test_tiled_linear_dev(hip, oracle, rng, fmt, M, O, K):
     """apus_hip_linear_dev on tiled weights equals the row-major linear bit
-    for bit (the same schedule for the same M)."""
+    for bit (the same schedule for the same M), except FP8 with 9..64 rows
+    (the narrow schedule: another fp32 summation order, so the BF16 outputs
+    are held to the oracle's linear bar)."""
     L = hip.lib()
     w, ws = (fp4_weights if fmt == 0 else fp8_weights)(rng, O, K)
     x = acts(rng, M, K)
@@ -149,4 +156,9 @@ def test_tiled_linear_dev(hip, rng, fmt, M, O, K):
                                          wsp.ptr), "linear")
         hip._check(L.apus_hip_synchronize(), "sync")
         outs.append(do.to_array(np.float32, (M, O)).copy())
+    if fmt == 1 and 8 < M <= 64:
+        c, s = oracle.act_quant(x)
+        unrounded = oracle.fp8_gemm(w, ws, c, s)
+        assert bf16_linear_ok(outs[1], unrounded, 1e-4 * np.abs(unrounded).max()).all()
+        return
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
