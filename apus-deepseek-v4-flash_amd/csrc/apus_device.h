@@ -89,6 +89,28 @@ __device__ __forceinline__ float apus_wave_max(float v) {
     return v;
 }
 
+/* The same maximum with DPP moves inside each 16-lane row (quad
+ * permutations, half-row and row mirrors) and the four row results read
+ * from lanes 0, 16, 32, 48; every lane must be active. fmaxf is
+ * order-independent, so the result equals apus_wave_max's. */
+template <int CTRL>
+__device__ __forceinline__ float apus_dpp_max(float v) {
+    const int o = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true);
+    return fmaxf(v, __builtin_bit_cast(float, o));
+}
+__device__ __forceinline__ float apus_wave_max_dpp(float v) {
+    v = apus_dpp_max<0xB1>(v);     /* quad_perm [1, 0, 3, 2] */
+    v = apus_dpp_max<0x4E>(v);     /* quad_perm [2, 3, 0, 1] */
+    v = apus_dpp_max<0x141>(v);    /* row_half_mirror */
+    v = apus_dpp_max<0x140>(v);    /* row_mirror */
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 /* h = bf16(silu(g') * u') with g' = min(g, limit), u' = clamp(u, +-limit)
  * when limit > 0 (c/moe.h:113-126); every step rounded as written. */
 __device__ __forceinline__ float apus_swiglu_h(float g, float u, float limit) {

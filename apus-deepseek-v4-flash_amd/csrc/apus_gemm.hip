@@ -1628,6 +1628,179 @@ bool apus_launch_narrow(const ApusGemmArgs &a, hipStream_t st) {
     return apus_launch_narrow_tm<NQ, 4>(a, st);
 }
 
+/*
+ * Split-K GEMV for dense FP8 launches with at most 8 rows on tiled weights
+ * (the attention's wq_a [1024, 4096] and wkv [512, 4096] at decode, the
+ * 4096-row projections at M = 1). The few-row schedule gives each 16-row
+ * tile 4 waves that stream it through a 2-group register ring, so a
+ * 512-row weight ran as long as a 1024-row one (4.7 us each): each wave's
+ * 16 KB took that long. Here one workgroup of NW waves owns a tile, the
+ * waves split K into runs of NG = NQ / NW 128-groups (NG <= 4), and every
+ * load of a wave is issued before its first MFMA (a scheduling barrier keeps
+ * the compiler from sinking the weight loads below the quantisation).
+ * Activations come as codes + scales (ASRC = codes) or as fp32 rows
+ * quantised in the wave (ASRC = f32): each (row, group) of the wave's share
+ * spread over the 64 lanes, two elements a lane, the group's absolute
+ * maximum a wave-wide max, every element rounded to BF16, scaled and
+ * converted as in the staging (so the codes are the act-quant kernel's bit
+ * for bit), codes and scale byte handed to the fragment lanes through a
+ * wave-private LDS slot. Quantising in the fragment layout instead (32
+ * elements a lane, one live row in 16) cost ~8 us of SIMD time at
+ * [4096, 8192]. Only lanes of rows below M read activation fragments (rows
+ * past M are zero and not stored): lanes loading the same address still cost
+ * the address unit a lane each.
+ * Sums: each wave one chain over its groups, the waves added in order in
+ * LDS. Splitting a tile over 2-8 workgroups (partial sums through
+ * device-coherent stores and a ticket, the last workgroup adding them in
+ * order) measured slower at every size: wq_a 5.0-5.4 against 3.8 us, wkv
+ * 4.8-5.6 against 3.7.
+ */
+template <int NQ, int NW, int ASRC>
+__global__ __launch_bounds__(NW * 64) void apus_gemv_split_kernel(ApusGemmArgs args) {
+    constexpr int K = NQ * 128, NG = NQ / NW;
+    static_assert(NG >= 1 && NQ % NW == 0, "split shape");
+    __shared__ apus_v4f red[NW][64];
+    /* fp32 rows: the wave's codes [group][row][128] and scale bytes */
+    __shared__ __align__(16) uint8_t lq[ASRC == APUS_A_F32 ? NW : 1][NG][8][128];
+    __shared__ uint8_t lsc[ASRC == APUS_A_F32 ? NW : 1][NG][8];
+    const ApusGemmEnt ent = args.ent0;
+    const int M = ent.M;
+    const int tile = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int q0 = wave * NG;
+    const bool live = r < M;
+    const uint8_t *bp = ent.w + ((size_t)tile * NQ * 128 + (size_t)q0 * 128 + lane) * 16;
+    const uint8_t *wsp = ent.ws + (size_t)(tile >> 3) * NQ + q0;
+    /* issue order: activations (L2 hits), then the weight stream, then the
+     * weight scales; nothing waits before the last load is out (the scale
+     * bytes stay per-lane operands: a readfirstlane would wait for them) */
+    apus_v4u lo[NG], hi[NG];
+    float sa[NG];
+    float2 xr[ASRC == APUS_A_F32 ? NG : 1][8];
+    if constexpr (ASRC == APUS_A_CODES) {
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            lo[i] = hi[i] = apus_v4u{0u, 0u, 0u, 0u};
+            sa[i] = 1.0f;
+        }
+        if (live) {
+            const uint8_t *ap = args.acodes + (size_t)(ent.a0 + r) * K + (size_t)q0 * 128 + g * 16;
+            const float *sap = args.ascale + (size_t)(ent.a0 + r) * NQ + q0;
+#pragma unroll
+            for (int i = 0; i < NG; ++i) {
+                lo[i] = apus_gld<apus_v4u>(ap + i * 128);
+                hi[i] = apus_gld<apus_v4u>(ap + i * 128 + 64);
+                sa[i] = apus_gld<float>(sap + i);
+            }
+        }
+    } else {
+        /* fp32 rows: lane l holds elements 2 l, 2 l + 1 of each (row, group) */
+        const float *xp = args.ax + (size_t)ent.a0 * K + (size_t)q0 * 128 + 2 * lane;
+#pragma unroll
+        for (int m = 0; m < 8; ++m)
+            if (m < M) {
+#pragma unroll
+                for (int i = 0; i < NG; ++i) xr[i][m] = apus_gld<float2>(xp + (size_t)m * K + i * 128);
+            }
+    }
+    apus_v4u b0[NG], b1[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        b0[i] = apus_ld16_stream(bp + (size_t)i * 2048);
+        b1[i] = apus_ld16_stream(bp + (size_t)i * 2048 + 1024);
+    }
+    int sb[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) sb[i] = (int)apus_gld<uint8_t>(wsp + i);
+    /* keep the scheduler from sinking the weight loads below the
+     * quantisation (it would wait for the activations first) */
+    __builtin_amdgcn_sched_barrier(0);
+    apus_v4f acc = apus_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        apus_v8i a;
+        int ea;
+        if constexpr (ASRC == APUS_A_CODES) {
+            a = apus_v8i{(int)lo[i].x, (int)lo[i].y, (int)lo[i].z, (int)lo[i].w,
+                         (int)hi[i].x, (int)hi[i].y, (int)hi[i].z, (int)hi[i].w};
+            ea = (int)apus_e8m0_of(sa[i]);
+        } else {
+            /* quantise the group's M rows across the wave (two elements a
+             * lane), codes and scale bytes through the wave's LDS slot, then
+             * the fragment of lane (r, g) from row r */
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+                if (m < M) {
+                    const float v0 = apus_bf16_rne(xr[i][m].x), v1 = apus_bf16_rne(xr[i][m].y);
+                    const float amax = apus_wave_max_dpp(fmaxf(fabsf(v0), fabsf(v1)));
+                    const uint32_t e = apus_act_scale_exp(amax);
+                    const float inv = apus_inv_pow2_from_exp(e);
+                    reinterpret_cast<uint16_t *>(lq[wave][i][m])[lane] =
+                        (uint16_t)apus_e4m3_pack2_hw(v0 * inv, v1 * inv);
+                    if (lane == 0) lsc[wave][i][m] = (uint8_t)e;
+                }
+            apus_v4u l4 = apus_v4u{0u, 0u, 0u, 0u}, h4 = l4;
+            ea = 127;
+            if (live) {
+                l4 = *reinterpret_cast<const apus_v4u *>(&lq[wave][i][r][16 * g]);
+                h4 = *reinterpret_cast<const apus_v4u *>(&lq[wave][i][r][64 + 16 * g]);
+                ea = lsc[wave][i][r];
+            }
+            a = apus_v8i{(int)l4.x, (int)l4.y, (int)l4.z, (int)l4.w, (int)h4.x, (int)h4.y, (int)h4.z, (int)h4.w};
+        }
+        const apus_v8i b = apus_v8i{(int)b0[i].x, (int)b0[i].y, (int)b0[i].z, (int)b0[i].w,
+                                    (int)b1[i].x, (int)b1[i].y, (int)b1[i].z, (int)b1[i].w};
+        acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, ea, sb[i]);
+    }
+    if constexpr (NW > 1) {
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
+        acc = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) acc += red[w][lane];
+    }
+    /* lane holds D[4 g + j][r]: row 4 g + j, weight row 16 tile + r */
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int mm = 4 * g + j;
+        if (mm < M) {
+            float x = acc[j];
+            if (args.round_out) x = apus_bf16_rne(x);
+            apus_gst<float>(ent.out + (size_t)(ent.o0 + mm) * args.ldo + tile * 16 + r, x);
+        }
+    }
+}
+
+/* waves per workgroup of the split-K GEMV: one 128-group a wave where 16
+ * waves cover K (K <= 2048), else NQ / 16. Measured (us, wq_a / wkv /
+ * wo_b / wq_b fp32-row linears, FP8 [4096, 4096] codes at M = 1): 1 group
+ * 3.85 / 3.75 / 8.4 / 7.5 / 4.85; at most 2 (fp32) / 4 (codes) 3.85 / 3.77 /
+ * 8.5 / 7.75 / 5.2; 4 groups for fp32 4.2 / 4.1 / 8.5 / 8.0 */
+#ifndef APUS_SPLIT_NG_CODES
+#define APUS_SPLIT_NG_CODES 1
+#endif
+#ifndef APUS_SPLIT_NG_F32
+#define APUS_SPLIT_NG_F32 1
+#endif
+template <int NQ, int ASRC>
+void apus_launch_split_k(const ApusGemmArgs &a, hipStream_t st) {
+    constexpr int NW0 = NQ / (ASRC == APUS_A_F32 ? APUS_SPLIT_NG_F32 : APUS_SPLIT_NG_CODES);
+    constexpr int NW = NW0 < 1 ? 1 : NW0 > 16 ? 16 : NW0;
+    static_assert(NQ / NW <= 4, "at most 4 groups a wave");
+    hipLaunchKernelGGL((apus_gemv_split_kernel<NQ, NW, ASRC>), dim3(a.O / 16), dim3(NW * 64), 0, st, a);
+}
+template <int ASRC>
+void apus_launch_split(const ApusGemmArgs &a, hipStream_t st) {
+    switch (a.K) {
+    case 1024: apus_launch_split_k<8, ASRC>(a, st); break;
+    case 2048: apus_launch_split_k<16, ASRC>(a, st); break;
+    case 4096: apus_launch_split_k<32, ASRC>(a, st); break;
+    default:   apus_launch_split_k<64, ASRC>(a, st); break;
+    }
+}
+
 /* launch the LDS tile schedule (returns false where it does not apply) */
 template <int NQ>
 bool apus_launch_lds_tile(const ApusGemmArgs &a, hipStream_t st) {
@@ -2818,6 +2991,16 @@ bool apus_narrow_on() {
     return on;
 }
 
+/* the split-K GEMV for few-row dense FP8 launches with few output rows
+ * (APUS_HIP_SPLIT=0 turns it off: the few-row schedule) */
+bool apus_split_on() {
+    static const bool on = [] {
+        const char *e = getenv("APUS_HIP_SPLIT");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
 /* the LDS tile schedule for dense FP8 GEMMs (APUS_HIP_LDS_TILE=0 turns it
  * off: the register-ring tile schedule, identical bits) */
 bool apus_lds_tile_on() {
@@ -2828,12 +3011,18 @@ bool apus_lds_tile_on() {
     return on;
 }
 
-int apus_dec_ks(size_t row_tiles) {
+int apus_dec_ks_env() {
     static const int forced = [] {
         const char *e = getenv("APUS_HIP_DEC_KS");
         const int v = e ? atoi(e) : 0;
         return (v == 1 || v == 2 || v == 4) ? v : 0;
     }();
+    return forced;
+}
+bool apus_dec_ks_forced() { return apus_dec_ks_env() != 0; }
+
+int apus_dec_ks(size_t row_tiles) {
+    const int forced = apus_dec_ks_env();
     if (forced) return forced;
     return row_tiles >= 1024 ? 1 : row_tiles >= 512 ? 2 : 4;
 }
@@ -2854,6 +3043,16 @@ hipError_t apus_launch_gemm_few(int wfmt, const ApusGemmArgs *a, int n_ent, int 
         (n_ent > 2 || (n_ent == 2 && (a->ent1.a0 != a->ent0.a0 || a->ent1.arows != a->ent0.arows ||
                                       a->ent1.M != a->ent0.M))))
         return hipErrorInvalidValue;
+    /* one dense FP8 entry on tiled weights with few output rows: the
+     * split-K GEMV (unless a K split is forced) */
+    if (n_ent == 1 && !ks && !a->kchain && wfmt == APUS_W_FP8 && a->wtiled && !a->ents && !a->pidx &&
+        !a->acc_y && !a->add_out && !a->items && !a->hq && !a->rdout && !a->zero && !a->ent0.arows &&
+        !a->ent0.orows && a->ent0.M <= 8 && (a->asrc == APUS_A_CODES || a->asrc == APUS_A_F32) &&
+        apus_split_on() && !apus_dec_ks_forced()) {
+        if (a->asrc == APUS_A_CODES) apus_launch_split<APUS_A_CODES>(*a, st);
+        else                         apus_launch_split<APUS_A_F32>(*a, st);
+        return hipGetLastError();
+    }
     if (!ks) ks = apus_dec_ks((size_t)n_ent * (a->O / 16));
     /* a required accumulation order (kchain) fixes the K split: one chain
      * needs whole-K waves; the K-quarter order takes whole-K waves (folded

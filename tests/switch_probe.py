@@ -13,7 +13,9 @@ Cases (all seeded, the same in every run):
 * dense decode-schedule launches: an FP8 [4096, 4096] GEMV at M = 1 and a
   12-entry MXFP4 [2048, 4096] grouped GEMV; dense tile-schedule launches:
   FP8 GEMMs of 100 x 512 x 4096 and 70 x 384 x 2048, and of 48, 12 and 29
-  rows (the narrow schedule) (inputs saved for the oracle).
+  rows (the narrow schedule); split-K GEMV launches: FP8 GEMMs of 3 x 512 x
+  4096 and 1 x 1024 x 8192 and a 4-row fp32 linear 512 x 4096 (inputs saved
+  for the oracle).
 """
 import ctypes as C
 import os
@@ -74,6 +76,17 @@ def dense(rng, out):
         c, sc = hip.act_quant(acts(rng, M, K))
         out[f"{name}_w"], out[f"{name}_ws"], out[f"{name}_c"], out[f"{name}_s"] = w, ws, c, sc
         out[f"{name}_y"] = hip.fp8_gemm(w, ws, c, sc)
+    # few-row dense FP8 on tiled weights with few output rows (the split-K
+    # GEMV): codes in, and an fp32-row linear (quantised in the kernel)
+    for name, (M, O, K) in (("t6", (3, 512, 4096)), ("t7", (1, 1024, 8192))):
+        w, ws = fp8_weights(rng, O, K)
+        c, sc = hip.act_quant(acts(rng, M, K))
+        out[f"{name}_w"], out[f"{name}_ws"], out[f"{name}_c"], out[f"{name}_s"] = w, ws, c, sc
+        out[f"{name}_y"] = hip.fp8_gemm(w, ws, c, sc)
+    w, ws = fp8_weights(rng, 512, 4096)
+    x = acts(rng, 4, 4096)
+    out["l1_w"], out["l1_ws"], out["l1_x"] = w, ws, x
+    out["l1_y"] = hip.fp8_linear(w, ws, x)
     for i, y in enumerate(hip.fp4_gemm_grouped(ents, c4, s4, 2048)):
         out[f"fp4_y{i}"] = y
 

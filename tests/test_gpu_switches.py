@@ -21,7 +21,9 @@ outputs with a child run without switches:
   per output over the 128-groups in order, so the dense outputs must be
   bit-identical too; APUS_HIP_NARROW=0 (9..64-row dense FP8 GEMMs on the
   tile schedule instead of the narrow one, which splits K in four): those
-  outputs held to the oracle's bars;
+  outputs held to the oracle's bars; APUS_HIP_SPLIT=0 (FP8 launches of at
+  most 8 rows on tiled weights on the few-row schedule instead of the
+  split-K GEMV, another K split): those outputs held to the oracle's bars;
 * APUS_HIP_DEC_KS=1 / 2 / 4 (waves splitting K in the few-row schedule):
   dense outputs change only in fp32 summation order, so they are held to
   the oracle's bars (max-rel 1e-3, err/esc 1e-4); routed outputs stay
@@ -38,7 +40,7 @@ import sys
 import numpy as np
 import pytest
 
-from helpers import err_esc, max_rel
+from helpers import bf16_linear_ok, err_esc, max_rel
 
 pytestmark = pytest.mark.gpu
 
@@ -46,7 +48,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PROBE = os.path.join(HERE, "switch_probe.py")
 SWITCHES = ["APUS_HIP_PRE_LDS", "APUS_HIP_PRE_RA", "APUS_HIP_PRE_RA13", "APUS_HIP_DEC_KS",
             "APUS_HIP_PAIR13_WIDE", "APUS_HIP_MOE_PAIRS", "APUS_HIP_MOE_SIDE", "APUS_HIP_LAYER1",
-            "APUS_HIP_LDS_TILE", "APUS_HIP_NARROW"]
+            "APUS_HIP_LDS_TILE", "APUS_HIP_NARROW", "APUS_HIP_SPLIT"]
 
 
 def _probe(tmp_path, name, env_set):
@@ -80,7 +82,7 @@ CASES = [{"APUS_HIP_PRE_LDS": "0"}, {"APUS_HIP_PRE_LDS": "2"},
          {"APUS_HIP_MOE_PAIRS": "0"}, {"APUS_HIP_MOE_PAIRS": "64"},
          {"APUS_HIP_MOE_SIDE": "0"}, {"APUS_HIP_LAYER1": "0"},
          {"APUS_HIP_DEC_KS": "1"}, {"APUS_HIP_DEC_KS": "2"}, {"APUS_HIP_DEC_KS": "4"},
-         {"APUS_HIP_LDS_TILE": "0"}, {"APUS_HIP_NARROW": "0"}]
+         {"APUS_HIP_LDS_TILE": "0"}, {"APUS_HIP_NARROW": "0"}, {"APUS_HIP_SPLIT": "0"}]
 
 
 @pytest.mark.parametrize("env", CASES, ids=lambda e: ",".join(f"{k[9:]}={v}" for k, v in e.items()))
@@ -98,17 +100,26 @@ def test_switch(oracle, tmp_path, default_run, env):
             assert d.mean() <= 2.0 ** -9 * np.abs(base[k]).mean(), k
             continue
         assert _same(got[k], base[k]), f"{var}={val}: {k} differs from the default schedule"
-    # dense launches: bitwise unless the K split was forced
-    keys = ["fp8_y"] + [f"fp4_y{i}" for i in range(12)]
+    # dense launches: bitwise unless the K split was changed (a forced few-row
+    # split also turns the split-K GEMV off)
+    split = var in ("APUS_HIP_SPLIT", "APUS_HIP_DEC_KS")
+    keys = [f"fp4_y{i}" for i in range(12)] + ([] if split else ["fp8_y"])
     if var != "APUS_HIP_DEC_KS":
         for k in keys:
             assert _same(got[k], base[k]), k
-    for name in ("t1", "t2", "t3", "t4", "t5"):
+    for name in ("t1", "t2", "t3", "t4", "t5", "t6", "t7", "l1"):
         if var == "APUS_HIP_NARROW" and name in ("t3", "t4", "t5"):
             continue    # another K split: held to the oracle's bars below
+        if split and name in ("t6", "t7", "l1"):
+            continue
         y = got[f"{name}_y"]
         assert _same(y, base[f"{name}_y"]), f"{var}={val}: {name} differs from the default schedule"
-    for name in ("t1", "t2", "t3", "t4", "t5"):
+    want = oracle.fp8_linear(got["l1_w"], got["l1_ws"], got["l1_x"])
+    c, s = oracle.act_quant(got["l1_x"])
+    unrounded = oracle.fp8_gemm(got["l1_w"], got["l1_ws"], c, s)
+    assert bf16_linear_ok(got["l1_y"], unrounded, 1e-4 * np.abs(unrounded).max()).all()
+    assert max_rel(got["l1_y"], want) <= 2.0 ** -6
+    for name in ("t1", "t2", "t3", "t4", "t5", "t6", "t7"):
         y = got[f"{name}_y"]
         args = (got[f"{name}_w"], got[f"{name}_ws"], got[f"{name}_c"], got[f"{name}_s"])
         truth, esc = oracle.fp8_truth(*args)
