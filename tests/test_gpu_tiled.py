@@ -135,6 +135,55 @@ def test_tiled_dense(hip, oracle, rng, fmt, M, O, K):
     assert err_esc(outs[1], truth, esc) <= 1e-4
 
 
+@pytest.mark.parametrize("fmt,O,K,Ms", [(0, 2048, 4096, [1] * 12), (0, 4096, 2048, [1, 3, 8, 0, 2]),
+                                        (1, 2048, 4096, [1, 7, 1]), (1, 1024, 2048, [8, 1])])
+def test_tiled_grouped_few_rows(hip, oracle, rng, fmt, O, K, Ms):
+    """Grouped launches whose entries all have at most 8 rows (max_m given,
+    the few-row schedule only) on tiled weights: every entry against the
+    oracle's GEMM bar, entries gathering their rows (arows) and scattering
+    their outputs (orows) as well as plain row ranges."""
+    L = hip.lib()
+    w, ws = (fp4_weights if fmt == 0 else fp8_weights)(rng, O, K)
+    _, _, (tw, tws) = dev_pack(hip, fmt, w, ws, O, K)
+    dws = hip.DevBuf.from_array(ws)
+    pws = tws if fmt == 0 else dws
+    rows = sum(Ms)
+    c, s = oracle.act_quant(acts(rng, rows + 3, K, 2.0))
+    dc, ds = hip.DevBuf.from_array(c), hip.DevBuf.from_array(s)
+    dout = hip.DevBuf(rows * O * 4)                                 # plain entries
+    dout2 = hip.DevBuf((rows + 2) * O * 4)                           # scattered entries
+    perm = rng.permutation(rows + 3)[:rows].astype(np.int32)       # gathered rows
+    operm = rng.permutation(rows + 2)[:rows].astype(np.int32)      # scattered outputs
+    dperm, doperm = hip.DevBuf.from_array(perm), hip.DevBuf.from_array(operm)
+    ents = (hip.ApusHipGemmEnt * len(Ms))()
+    m0 = 0
+    for i, M in enumerate(Ms):
+        if i % 2:
+            ents[i] = hip.ApusHipGemmEnt(tw.ptr, pws.ptr, dout2.ptr, dperm.ptr + 4 * m0, doperm.ptr + 4 * m0,
+                                         0, 0, M, 0)
+        else:
+            ents[i] = hip.ApusHipGemmEnt(tw.ptr, pws.ptr, dout.ptr, None, None, m0, m0, M, 0)
+        m0 += M
+    de = hip.DevBuf(C.sizeof(ents))
+    hip._check(L.apus_hip_h2d(de.ptr, C.addressof(ents), C.sizeof(ents)), "h2d")
+    hip._check(L.apus_hip_gemm_grouped_dev(fmt | hip.W_TILED, de.ptr, len(Ms), dc.ptr, ds.ptr, O, K, O, 0,
+                                           max(Ms)), "grouped")
+    hip._check(L.apus_hip_synchronize(), "sync")
+    out, out2 = dout.to_array(np.float32, (rows, O)), dout2.to_array(np.float32, (rows + 2, O))
+    m0 = 0
+    for i, M in enumerate(Ms):
+        if M:
+            src = perm[m0:m0 + M] if i % 2 else np.arange(m0, m0 + M)
+            dst = operm[m0:m0 + M] if i % 2 else np.arange(m0, m0 + M)
+            cc, ss = c[src].copy(), s[src].copy()
+            want = (oracle.fp4_gemm if fmt == 0 else oracle.fp8_gemm)(w, ws, cc, ss)
+            truth, esc = (oracle.fp4_truth if fmt == 0 else oracle.fp8_truth)(w, ws, cc, ss)
+            got = (out2 if i % 2 else out)[dst]
+            assert max_rel(got, want) <= 1e-3, i
+            assert err_esc(got, truth, esc) <= 1e-4, i
+        m0 += M
+
+
 @pytest.mark.parametrize("fmt,M,O,K", [(1, 1, 4096, 4096), (0, 6, 2048, 4096), (1, 20, 1024, 2048),
                                        (1, 8, 1024, 8192), (0, 1, 512, 1024)])
 def test_tiled_linear_dev(hip, oracle, rng, fmt, M, O, K):
