@@ -2496,9 +2496,13 @@ struct ApusLayerBar {
  * measured at ~3 us per launch here): the data that crosses it (the h
  * codes) is written with device-coherent stores that have completed
  * (s_waitcnt) before the writer's workgroup arrives, and read only after it,
- * by loads that cannot hit stale cache lines (no workgroup reads those lines
- * before the barrier in a launch, and a launch starts with invalidated
- * caches). */
+ * by loads that cannot hit stale cache lines: no workgroup reads those lines
+ * before the barrier in a launch, and every launch starts with invalidated
+ * caches (HIP's stream order: a kernel, a graph node included, sees every
+ * earlier kernel's writes, so the non-coherent L1 / L2 are invalidated at
+ * its start). Reading them with device-coherent loads instead (two 8-byte
+ * sc1 loads per 16 bytes) measured 975-991 against 1019-1030 tok/s at
+ * config 4 on one box: those loads skip L2 on the barrier's critical path. */
 #define APUS_L1_WGS 256u
 __device__ __forceinline__ void apus_l1_arrive(const ApusLayerBar &bar) {
     unsigned *gc = bar.w + APUS_L1_GROUP(blockIdx.x & 7u);
