@@ -1801,6 +1801,163 @@ void apus_launch_split(const ApusGemmArgs &a, hipStream_t st) {
     }
 }
 
+/*
+ * Grouped GEMV for grouped launches of tiled MXFP4 / FP8 entries with at most
+ * 8 rows each and no required accumulation order (config 0: twelve
+ * [2048, 4096] MXFP4 GEMVs at M = 1). One workgroup of NW waves owns a
+ * (16-row weight tile, entry); each wave takes a contiguous run of NG
+ * 128-groups (8 KB of weight bytes) and issues all its loads before its
+ * first MFMA; the waves' sums are added in order in LDS.
+ * Activations: each wave fetches its groups of each live row with one
+ * contiguous load instruction per row (64 lanes x 16 bytes) into a
+ * wave-private LDS slot and reads its fragments from there. Measured on the
+ * config-0 launch shape (standalone, 53.6 MB per launch, fresh copies): the
+ * weight stream alone with this shape 9.1 us; fragments loaded straight from
+ * the codes by the lanes of live rows (a dozen 4-lane loads per wave) 11.7
+ * us; through one load per row and LDS 9.9 us (the cost is per load
+ * instruction, not per byte). In the library the launch takes 10.6-10.8 us
+ * against 11.3-11.7 on the few-row schedule, which runs one whole-K wave per
+ * tile through a register ring and stages 8 activation rows per workgroup
+ * whatever M is; 4 KB waves (8 per tile) and 4-lane fragment loads measured
+ * 11.9 us.
+ */
+template <int WF, int NQ, int NW, int MR>
+__global__ __launch_bounds__(NW * 64) void apus_gemv_grp_kernel(ApusGemmArgs args) {
+    constexpr int K = NQ * 128, NG = NQ / NW;
+    constexpr int QB = WF == APUS_W_FP4 ? 1024 : 2048;        /* weight bytes per group */
+    static_assert(NQ % NW == 0 && NG * 16 <= 128 && NG % 4 == 0, "grouped GEMV shape");
+    __shared__ apus_v4f red[NW][64];
+    /* MR: rows an entry may have (1 or 8) */
+    __shared__ __align__(16) uint8_t lx[NW][MR][NG * 128];     /* wave's codes [row][group bytes] */
+    __shared__ float lsa[NW][MR][NG];
+    /* grouped launches only: the entry straight from the table (the generic
+     * lookup's checks cost dependent scalar loads before the first address) */
+    const ApusGemmEnt ent = args.ents[blockIdx.y];
+    /* every field in one batch of scalar loads: else the early return below
+     * costs a round trip of its own for M (config-0 launch 10.7-10.8 against
+     * 10.9 us; pinning the kernel arguments the same way turned the entry
+     * fetch into vector loads, 11.3-11.4 us) */
+    asm volatile("" ::"s"(ent.w), "s"(ent.ws), "s"(ent.out), "s"(ent.arows), "s"(ent.orows), "s"(ent.a0),
+                 "s"(ent.o0), "s"(ent.M));
+    const int M = ent.M < MR ? ent.M : MR;     /* the launcher checks max_m <= MR */
+    if (M <= 0) return;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, g = lane >> 4;
+    const int tile = blockIdx.x, o = tile * 16 + r;
+    const int q0 = wave * NG;
+    /* activation rows first (L2 hits: they return before the weights, and
+     * their LDS hand-off runs while the weights stream): row m's NG groups
+     * are NG * 128 contiguous bytes, one load instruction; the M x NG scales
+     * one more. Row indices of a gathered entry: one load, lane m. */
+    constexpr int XL = NG * 8;                                  /* lanes of one row's load */
+    apus_v4u xv[MR];
+    float xsv = 0.0f;
+    if (ent.arows) {
+        /* gathered rows: the indices first (one round trip) */
+        const int rv = lane < M ? apus_gld<int>(ent.arows + lane) : 0;
+        const int srow = __shfl(rv, lane / NG, 64);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+            if (m < M && lane < XL) {
+                const int row = __builtin_amdgcn_readlane(rv, m);
+                xv[m] = apus_gld<apus_v4u>(args.acodes + (size_t)row * K + (size_t)q0 * 128 + lane * 16);
+            }
+        }
+        if (lane < M * NG) xsv = apus_gld<float>(args.ascale + (size_t)srow * NQ + q0 + lane % NG);
+    } else {
+        const uint8_t *xa = args.acodes + (size_t)ent.a0 * K + (size_t)q0 * 128 + lane * 16;
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+            if (m < M && lane < XL) xv[m] = apus_gld<apus_v4u>(xa + (size_t)m * K);
+        if (lane < M * NG) xsv = apus_gld<float>(args.ascale + (size_t)(ent.a0 + lane / NG) * NQ + q0 + lane % NG);
+    }
+    const ApusWLane wl = apus_wlane<WF>(ent, true, o, lane, K);
+    apus_v4u b0[NG], b1[WF == APUS_W_FP8 ? NG : 1];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        b0[i] = apus_ld16_stream(wl.w + (size_t)(q0 + i) * wl.qs);
+        if constexpr (WF == APUS_W_FP8) b1[i] = apus_ld16_stream(wl.w + (size_t)(q0 + i) * wl.qs + 1024);
+    }
+    (void)QB;
+    apus_v4u sc4[WF == APUS_W_FP4 ? NG / 4 : 1];
+    unsigned sc1[WF == APUS_W_FP8 ? NG : 1];
+    if constexpr (WF == APUS_W_FP4) {
+        /* the 16 scale bytes of the lane's row per 512-slice */
+#pragma unroll
+        for (int j = 0; j < NG / 4; ++j) sc4[j] = apus_gld<apus_v4u>(wl.s + (size_t)((q0 >> 2) + j) * wl.ss);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NG; ++i) sc1[i] = apus_gld<uint8_t>(wl.s + q0 + i);
+    }
+    /* activation rows to the wave's LDS slot, then every lane's fragments */
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+        if (m < M && lane < XL) *reinterpret_cast<apus_v4u *>(&lx[wave][m][lane * 16]) = xv[m];
+    if (lane < M * NG) (&lsa[wave][0][0])[lane] = xsv;
+    const bool live = r < M;
+    const int rr = live ? r : 0;
+    apus_v8i av[NG];
+    int ea[NG];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const apus_v4u l4 = *reinterpret_cast<const apus_v4u *>(&lx[wave][rr][i * 128 + g * 16]);
+        const apus_v4u h4 = *reinterpret_cast<const apus_v4u *>(&lx[wave][rr][i * 128 + 64 + g * 16]);
+        const int z = live ? -1 : 0;
+        av[i] = apus_v8i{(int)l4.x & z, (int)l4.y & z, (int)l4.z & z, (int)l4.w & z,
+                         (int)h4.x & z, (int)h4.y & z, (int)h4.z & z, (int)h4.w & z};
+        ea[i] = live ? (int)apus_e8m0_of(lsa[wave][rr][i]) : 127;
+    }
+    apus_v4f acc = apus_v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        if constexpr (WF == APUS_W_FP4) {
+            const int sb = (int)((sc4[i >> 2][i & 3] >> (8 * g)) & 0xffu);
+            const apus_v8i b = apus_v8i{(int)b0[i].x, (int)b0[i].y, (int)b0[i].z, (int)b0[i].w, 0, 0, 0, 0};
+            acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(av[i], b, acc, ea[i], sb);
+        } else {
+            const apus_v8i b = apus_v8i{(int)b0[i].x, (int)b0[i].y, (int)b0[i].z, (int)b0[i].w,
+                                        (int)b1[i].x, (int)b1[i].y, (int)b1[i].z, (int)b1[i].w};
+            acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(av[i], b, acc, ea[i], (int)sc1[i]);
+        }
+    }
+    if constexpr (NW > 1) {
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
+        acc = red[0][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) acc += red[w][lane];
+    }
+    /* lane holds D[4 g + j][r]: row 4 g + j, weight row o */
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int mm = 4 * g + j;
+        if (mm < M) {
+            float x = acc[j];
+            if (args.round_out) x = apus_bf16_rne(x);
+            const int orow = ent.orows ? apus_gld<int>(ent.orows + mm) : ent.o0 + mm;
+            apus_gst<float>(ent.out + (size_t)orow * args.ldo + o, x);
+        }
+    }
+}
+
+/* 8 KB of weight bytes a wave: FP4 8 groups (4 waves at K = 4096, 2 at
+ * 2048), FP8 4 groups */
+template <int WF, int NQ>
+void apus_launch_grp_k(const ApusGemmArgs &a, int n_ent, hipStream_t st) {
+    constexpr int NG = WF == APUS_W_FP4 ? 8 : 4;
+    constexpr int NW = NQ / NG;
+    if (a.max_m == 1)
+        hipLaunchKernelGGL((apus_gemv_grp_kernel<WF, NQ, NW, 1>), dim3(a.O / 16, n_ent), dim3(NW * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((apus_gemv_grp_kernel<WF, NQ, NW, 8>), dim3(a.O / 16, n_ent), dim3(NW * 64), 0, st, a);
+}
+template <int WF>
+void apus_launch_grp(const ApusGemmArgs &a, int n_ent, hipStream_t st) {
+    if (a.K == 4096) apus_launch_grp_k<WF, 32>(a, n_ent, st);
+    else             apus_launch_grp_k<WF, 16>(a, n_ent, st);
+}
+
 /* launch the LDS tile schedule (returns false where it does not apply) */
 template <int NQ>
 bool apus_launch_lds_tile(const ApusGemmArgs &a, hipStream_t st) {
@@ -2995,6 +3152,16 @@ bool apus_narrow_on() {
     return on;
 }
 
+/* the grouped GEMV for few-row grouped launches on tiled weights
+ * (APUS_HIP_GRP=0 turns it off: the few-row schedule) */
+bool apus_grp_on() {
+    static const bool on = [] {
+        const char *e = getenv("APUS_HIP_GRP");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
 /* the split-K GEMV for few-row dense FP8 launches with few output rows
  * (APUS_HIP_SPLIT=0 turns it off: the few-row schedule) */
 bool apus_split_on() {
@@ -3125,6 +3292,14 @@ hipError_t apus_launch_gemm(int wfmt, const ApusGemmArgs *a, int n_ent,
         apus_group_k(a->K) && a->O % 128 == 0) {
         const bool run_dec = !(a->min_m >= R);
         const bool run_pre = !(a->max_m > 0 && a->max_m <= R);
+        /* few-row entries only, no required order, tiled weights: the
+         * grouped GEMV */
+        if (!run_pre && a->wtiled && !a->kchain && !a->pidx && !a->acc_y && !a->add_out && !a->items &&
+            !a->zero && a->max_m > 0 && apus_grp_on()) {
+            if (wfmt == APUS_W_FP4) apus_launch_grp<APUS_W_FP4>(*a, n_ent, st);
+            else                    apus_launch_grp<APUS_W_FP8>(*a, n_ent, st);
+            return hipGetLastError();
+        }
         if (run_dec) {
             ApusGemmArgs d = *a;
             d.m_min = 0;

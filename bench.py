@@ -39,7 +39,7 @@ METRIC = "MXFP4 expert GEMV GB/s (%HBM peak) @M=1; MoE grouped-GEMM TFLOP/s @512
 # HBM bytes per grouped 12-GEMV launch measured with rocprofv3 FETCH_SIZE and
 # WRITE_SIZE (FETCH scaled x2.0 from a 256 MiB copy calibration); command and
 # counts in profiles/config0_mxfp4_gemv_m1.txt. Re-measure when the kernel changes.
-CONFIG0_TRAFFIC_BYTES = 53752438
+CONFIG0_TRAFFIC_BYTES = 53663744
 
 
 def log(*a):
@@ -1014,7 +1014,7 @@ def main():
                      "achieved": round(g["launch_bytes"] / (g["tiled_launch_us"] * 1e-6) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(g["launch_bytes"] / (g["tiled_launch_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                     "kernel": "apus_gemm_decode_kernel (grouped, 12 GEMVs, tiled weights)",
+                     "kernel": "apus_gemv_grp_kernel (grouped, 12 GEMVs, tiled weights)",
                      "launch_us": round(g["tiled_launch_us"], 3), "bytes_per_launch": g["launch_bytes"],
                      "traffic": CONFIG0_TRAFFIC_BYTES,
                      "traffic_source": "rocprofv3 FETCH_SIZE + WRITE_SIZE per launch, calibrated "

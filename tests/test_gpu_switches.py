@@ -24,6 +24,9 @@ outputs with a child run without switches:
   outputs held to the oracle's bars; APUS_HIP_SPLIT=0 (FP8 launches of at
   most 8 rows on tiled weights on the few-row schedule instead of the
   split-K GEMV, another K split): those outputs held to the oracle's bars;
+  APUS_HIP_GRP=0 (grouped launches of few-row entries on tiled weights on
+  the few-row schedule instead of the grouped GEMV): the grouped MXFP4
+  outputs held to the oracle's bars;
 * APUS_HIP_DEC_KS=1 / 2 / 4 (waves splitting K in the few-row schedule):
   dense outputs change only in fp32 summation order, so they are held to
   the oracle's bars (max-rel 1e-3, err/esc 1e-4); routed outputs stay
@@ -48,7 +51,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PROBE = os.path.join(HERE, "switch_probe.py")
 SWITCHES = ["APUS_HIP_PRE_LDS", "APUS_HIP_PRE_RA", "APUS_HIP_PRE_RA13", "APUS_HIP_DEC_KS",
             "APUS_HIP_PAIR13_WIDE", "APUS_HIP_MOE_PAIRS", "APUS_HIP_MOE_SIDE", "APUS_HIP_LAYER1",
-            "APUS_HIP_LDS_TILE", "APUS_HIP_NARROW", "APUS_HIP_SPLIT"]
+            "APUS_HIP_LDS_TILE", "APUS_HIP_NARROW", "APUS_HIP_SPLIT", "APUS_HIP_GRP"]
 
 
 def _probe(tmp_path, name, env_set):
@@ -82,7 +85,8 @@ CASES = [{"APUS_HIP_PRE_LDS": "0"}, {"APUS_HIP_PRE_LDS": "2"},
          {"APUS_HIP_MOE_PAIRS": "0"}, {"APUS_HIP_MOE_PAIRS": "64"},
          {"APUS_HIP_MOE_SIDE": "0"}, {"APUS_HIP_LAYER1": "0"},
          {"APUS_HIP_DEC_KS": "1"}, {"APUS_HIP_DEC_KS": "2"}, {"APUS_HIP_DEC_KS": "4"},
-         {"APUS_HIP_LDS_TILE": "0"}, {"APUS_HIP_NARROW": "0"}, {"APUS_HIP_SPLIT": "0"}]
+         {"APUS_HIP_LDS_TILE": "0"}, {"APUS_HIP_NARROW": "0"}, {"APUS_HIP_SPLIT": "0"},
+         {"APUS_HIP_GRP": "0"}]
 
 
 @pytest.mark.parametrize("env", CASES, ids=lambda e: ",".join(f"{k[9:]}={v}" for k, v in e.items()))
@@ -103,7 +107,8 @@ def test_switch(oracle, tmp_path, default_run, env):
     # dense launches: bitwise unless the K split was changed (a forced few-row
     # split also turns the split-K GEMV off)
     split = var in ("APUS_HIP_SPLIT", "APUS_HIP_DEC_KS")
-    keys = [f"fp4_y{i}" for i in range(12)] + ([] if split else ["fp8_y"])
+    keys = ([] if var == "APUS_HIP_GRP" else [f"fp4_y{i}" for i in range(12)]) + \
+        ([] if split else ["fp8_y"])
     if var != "APUS_HIP_DEC_KS":
         for k in keys:
             assert _same(got[k], base[k]), k

@@ -136,12 +136,14 @@ def test_tiled_dense(hip, oracle, rng, fmt, M, O, K):
 
 
 @pytest.mark.parametrize("fmt,O,K,Ms", [(0, 2048, 4096, [1] * 12), (0, 4096, 2048, [1, 3, 8, 0, 2]),
-                                        (1, 2048, 4096, [1, 7, 1]), (1, 1024, 2048, [8, 1])])
+                                        (1, 2048, 4096, [1, 7, 1]), (1, 1024, 2048, [8, 1]),
+                                        (1, 1024, 4096, [1, 1, 0, 1]), (0, 1024, 2048, [1, 1])])
 def test_tiled_grouped_few_rows(hip, oracle, rng, fmt, O, K, Ms):
-    """Grouped launches whose entries all have at most 8 rows (max_m given,
-    the few-row schedule only) on tiled weights: every entry against the
-    oracle's GEMM bar, entries gathering their rows (arows) and scattering
-    their outputs (orows) as well as plain row ranges."""
+    """Grouped launches whose entries all have at most 8 rows (max_m given)
+    on tiled weights take the grouped GEMV (one row per entry or up to 8):
+    every entry against the oracle's GEMM bar, entries gathering their rows
+    (arows) and scattering their outputs (orows) as well as plain row
+    ranges."""
     L = hip.lib()
     w, ws = (fp4_weights if fmt == 0 else fp8_weights)(rng, O, K)
     _, _, (tw, tws) = dev_pack(hip, fmt, w, ws, O, K)
