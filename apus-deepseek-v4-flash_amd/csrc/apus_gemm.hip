@@ -1839,8 +1839,10 @@ __global__ __launch_bounds__(NW * 64) void apus_gemv_grp_kernel(ApusGemmArgs arg
      * fetch into vector loads, 11.3-11.4 us) */
     asm volatile("" ::"s"(ent.w), "s"(ent.ws), "s"(ent.out), "s"(ent.arows), "s"(ent.orows), "s"(ent.a0),
                  "s"(ent.o0), "s"(ent.M));
-    const int M = ent.M < MR ? ent.M : MR;     /* the launcher checks max_m <= MR */
-    if (M <= 0) return;
+    /* entries past the launch's row bound are skipped, as on the few-row
+     * schedule */
+    const int M = ent.M;
+    if (M <= 0 || M > MR) return;
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, g = lane >> 4;
     const int tile = blockIdx.x, o = tile * 16 + r;
@@ -1942,7 +1944,11 @@ __global__ __launch_bounds__(NW * 64) void apus_gemv_grp_kernel(ApusGemmArgs arg
 }
 
 /* 8 KB of weight bytes a wave: FP4 8 groups (4 waves at K = 4096, 2 at
- * 2048), FP8 4 groups */
+ * 2048), FP8 4 groups. Not used for the routed dispatch: its few-row tables
+ * have a slot per expert (up to 256, mostly empty at config 2), and a
+ * workgroup per (tile, slot) that reads its entry before it can leave made
+ * the K-quarter w2 (whose order 4 waves of a quarter each would keep bit
+ * for bit) twice as slow: config 2 874 against 440 us. */
 template <int WF, int NQ>
 void apus_launch_grp_k(const ApusGemmArgs &a, int n_ent, hipStream_t st) {
     constexpr int NG = WF == APUS_W_FP4 ? 8 : 4;
