@@ -369,7 +369,15 @@ __device__ __forceinline__ void apus_expert_ptrs(const ApusGemmArgs &a, int mat,
 
 /* the entry of launch row y: table, routed pair, or the single entry */
 __device__ __forceinline__ ApusGemmEnt apus_entry_of(const ApusGemmArgs &a, int y) {
-    if (a.ents) return apus_gld<ApusGemmEnt>(a.ents + y);
+    if (a.ents) {
+        /* y is uniform (the launch row): one batch of scalar loads for every
+         * field (a vector load of the entry measured the same to 1 % slower
+         * at configs 2 and 3) */
+        const ApusGemmEnt e = a.ents[y];
+        asm volatile("" ::"s"(e.w), "s"(e.ws), "s"(e.out), "s"(e.arows), "s"(e.orows), "s"(e.a0),
+                     "s"(e.o0), "s"(e.M));
+        return e;
+    }
     if (!a.pidx) return y == 0 ? a.ent0 : a.ent1;
     ApusGemmEnt ent;
     const int p = y / a.nmat, mat = y - p * a.nmat;
