@@ -1741,7 +1741,9 @@ __global__ __launch_bounds__(NW * 64) void apus_gemv_split_kernel(ApusGemmArgs a
             for (int m = 0; m < 8; ++m)
                 if (m < M) {
                     const float v0 = apus_bf16_rne(xr[i][m].x), v1 = apus_bf16_rne(xr[i][m].y);
-                    const float amax = apus_wave_max_dpp(fmaxf(fabsf(v0), fabsf(v1)));
+                    /* seeded with 0 as the staging's max: a group of NaN only
+                     * gets 0, not NaN */
+                    const float amax = apus_wave_max_dpp(fmaxf(fmaxf(0.0f, fabsf(v0)), fabsf(v1)));
                     const uint32_t e = apus_act_scale_exp(amax);
                     const float inv = apus_inv_pow2_from_exp(e);
                     reinterpret_cast<uint16_t *>(lq[wave][i][m])[lane] =

@@ -16,6 +16,10 @@
   (+inf) and signed-zero codes for its finite elements, and its GEMM row
   comes out NaN while the other rows are unaffected.
 * apus_hip_memset refuses to run while a graph capture is open.
+* The split-K GEMV's in-kernel quantisation of fp32 rows (FP8 linears of up
+  to 8 rows on tiled weights) equals act-quant followed by the same GEMV on
+  codes, bit for bit, with NaN-only, infinite, zero, subnormal and large
+  groups.
 """
 import ctypes as C
 
@@ -213,3 +217,41 @@ def test_act_quant_dev_unaligned(hip, oracle):
         hip._check(hip.lib().apus_hip_act_quant_dev(ptr, M, K, dc.ptr, ds.ptr), "act_quant_dev")
         assert np.array_equal(dc.to_array(np.uint8, (M, K)), rc), off
         assert np.array_equal(ds.to_array(np.float32, (M, K // 128)), rs), off
+
+
+@pytest.mark.parametrize("M,O,K", [(1, 512, 4096), (3, 1024, 1024), (8, 512, 8192), (2, 256, 2048)])
+def test_split_linear_quant_equals_act_quant(hip, rng, M, O, K):
+    """FP8 linears of at most 8 rows on tiled weights quantise x inside the
+    split-K GEMV; the result equals act-quant then the same GEMV on codes,
+    bit for bit, with groups of NaN only, an infinity, zeros, subnormals and
+    large values among ordinary ones."""
+    L = hip.lib()
+    w, ws = fp8_weights(rng, O, K)
+    x = acts(rng, M, K, 2.0)
+    x[0, 0:128] = np.nan                                  # a group of NaN only
+    x[0, 200] = np.inf                                    # an infinity
+    x[M - 1, 256:384] = 0.0                               # zeros
+    x[M - 1, 384:512] = np.float32(3e-39) * rng.standard_normal(128).astype(np.float32)   # subnormals
+    if K >= 1024:
+        x[0, 640:768] *= np.float32(1e30)                 # large values
+    dx = hip.DevBuf.from_array(np.ascontiguousarray(x, np.float32))
+    dw, dws = hip.DevBuf.from_array(w), hip.DevBuf.from_array(ws)
+    tw = hip.DevBuf(O * K)
+    hip._check(L.apus_hip_pack_weights_dev(1, dw.ptr, None, tw.ptr, None, O, K), "pack")
+    wsp = hip.DevBuf(L.apus_hip_linear_workspace(M, K))
+    y1 = hip.DevBuf(M * O * 4)
+    hip._check(L.apus_hip_linear_dev(1 | hip.W_TILED, tw.ptr, dws.ptr, dx.ptr, y1.ptr, M, K, O, wsp.ptr),
+               "linear_dev")
+    dc, ds = hip.DevBuf(M * K), hip.DevBuf(M * (K // 128) * 4)
+    hip._check(L.apus_hip_act_quant_dev(dx.ptr, M, K, dc.ptr, ds.ptr), "act_quant_dev")
+    y2 = hip.DevBuf(M * O * 4)
+    hip._check(L.apus_hip_fp8_gemm_dev(tw.ptr, dws.ptr, dc.ptr, ds.ptr, y2.ptr, M, O, K, 1 | hip.W_TILED),
+               "fp8_gemm_dev")
+    hip._check(L.apus_hip_synchronize(), "sync")
+    a, b = y1.to_array(np.float32, (M, O)), y2.to_array(np.float32, (M, O))
+    assert np.array_equal(np.isnan(a), np.isnan(b))
+    fin = ~np.isnan(a)
+    assert np.array_equal(a[fin].view(np.uint32), b[fin].view(np.uint32))
+    assert np.isnan(a[0]).all()                           # row 0 holds an infinity
+    assert np.isfinite(a[1:]).all()
+
