@@ -2626,8 +2626,9 @@ hipError_t apus_launch_moe_pair2(const ApusGemmArgs *a, hipStream_t st) {
  *    registers (wave group i takes pairs 3i..3i+2, its 4 waves the K
  *    quarters, as apus_moe_pair2 with G = 2); these bytes stream during the
  *    hand-off and barrier latency, not in front of the phase-1 refills;
- *  - the rider, if any: every workgroup multiplies its 16-row tile b of the
- *    rider's weight (wave w: K slice w), 16.8 MB that do not depend on h;
+ *  - the rider, if any: the 64 workgroups without pair units multiply 4
+ *    16-row tiles of the rider's weight each (wave w: K slice w), 16.8 MB
+ *    that do not depend on h;
  *    out = bf16(sum of the 8 slice chains in order), which may differ from
  *    the two-launch path's single K chain by fp32 rounding;
  *  - waits at the barrier (apus_l1_arrive / apus_l1_wait);
@@ -2758,7 +2759,7 @@ struct ApusLayer1Lds {
     uint8_t sc[32];
     float gu[2][2][2][64];                    /* [half][mat][tile][lane] */
     float red[4][6][64];                      /* [K quarter][pair][lane] */
-    float rr[8][64];                          /* rider partial sums [wave][lane] */
+    float rr[4][8][64];                       /* rider partial sums [tile][wave][lane] */
     int last[2];
     int tmo;                                  /* the barrier wait gave up */
 };
@@ -2854,14 +2855,25 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
         for (int v = 0; v < PD1; ++v) apus_load_b_full<APUS_W_FP4, false>(ring1[v], wl1, v);
     }
     ApusBFrag<APUS_W_FP4> ring2[NPG];
-    /* the rider's rows of this workgroup: 16-row tile b of its [4096, 4096]
-     * weight, wave w taking the 512-slice w of K (loaded after the
-     * workgroup's arrival, below) */
-    ApusWLane wlr{};
+    /* the rider's rows of this workgroup: RT 16-row tiles of its [4096, 4096]
+     * weight from tile rt0, wave w taking the 512-slice w of K (loaded after
+     * the workgroup's arrival, below). With APUS_L1_RIDER2 the 64
+     * workgroups without pair units take all 256 tiles (4 each), so that
+     * the pair workgroups (256 KB of phase-1 weights each) stream only their
+     * w2 share after arriving (config 4 +0.3 to +1.6 % in five same-box
+     * pairs, e.g. 1030 against 1014 tok/s); else every workgroup takes tile
+     * b. The tiles' sums are the same chains either way. */
+#ifndef APUS_L1_RIDER2
+#define APUS_L1_RIDER2 1
+#endif
+    constexpr int RT = APUS_L1_RIDER2 ? (ROLE == 2 ? 4 : 0) : 1;
+    const int rt0 = APUS_L1_RIDER2 ? (b - 192) * 4 : b;
+    ApusWLane wlr[RT > 0 ? RT : 1];
     if (rd) {
         ApusGemmEnt er;
         er.w = a1.rdw; er.ws = a1.rdws;
-        wlr = apus_wlane<APUS_W_FP8>(er, true, o2, lane, K1);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) wlr[t] = apus_wlane<APUS_W_FP8>(er, true, (rt0 + t) * 16 + r, lane, K1);
     }
 
     apus_stage_quant<K1, APUS_A_F32>(a1, raw, L.codes, L.sc);
@@ -2935,8 +2947,11 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
      * with LDS-only barriers in the hand-off, and at the start in the
      * workgroups without pair units, measured 5 % slower per layer); the
      * MFMAs run before the wait. */
-    ApusBFrag<APUS_W_FP8> fr;
-    if (rd) apus_load_b_full<APUS_W_FP8>(fr, wlr, wave);
+    ApusBFrag<APUS_W_FP8> fr[RT > 0 ? RT : 1];
+    if (rd) {
+#pragma unroll
+        for (int t = 0; t < RT; ++t) apus_load_b_full<APUS_W_FP8>(fr[t], wlr[t], wave);
+    }
     /* the w2 share (wave group `half` takes pairs 3 half .. 3 half + 2, wave
      * w4 the K quarter w4, one 512-slice each), issued after the arrival:
      * issued with the phase-1 ring, its bytes sat in front of the chain's
@@ -2948,20 +2963,24 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
     if (rd) {
         const int z = r == 0 ? -1 : 0;
         const uint8_t *arow = L.codes + g * 16;
-        apus_v4f accr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const int q = wave * 4 + st;
-            const uint4 x0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
-            const uint4 x1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
-            const apus_v8i a = apus_v8i{(int)x0.x & z, (int)x0.y & z, (int)x0.z & z, (int)x0.w & z,
-                                        (int)x1.x & z, (int)x1.y & z, (int)x1.z & z, (int)x1.w & z};
-            const apus_v4u w0 = fr.w[st][0], w1 = fr.w[st][1];
-            const apus_v8i bb = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
-                                         (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
-            accr = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, bb, accr, (int)L.sc[q], (int)fr.s[st]);
+        for (int t = 0; t < RT; ++t) {
+            apus_v4f accr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const int q = wave * 4 + st;
+                const uint4 x0 = *reinterpret_cast<const uint4 *>(arow + q * 128);
+                const uint4 x1 = *reinterpret_cast<const uint4 *>(arow + q * 128 + 64);
+                const apus_v8i a = apus_v8i{(int)x0.x & z, (int)x0.y & z, (int)x0.z & z, (int)x0.w & z,
+                                            (int)x1.x & z, (int)x1.y & z, (int)x1.z & z, (int)x1.w & z};
+                const apus_v4u w0 = fr[t].w[st][0], w1 = fr[t].w[st][1];
+                const apus_v8i bb = apus_v8i{(int)w0.x, (int)w0.y, (int)w0.z, (int)w0.w,
+                                             (int)w1.x, (int)w1.y, (int)w1.z, (int)w1.w};
+                accr = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, bb, accr, (int)L.sc[q],
+                                                                           (int)fr[t].s[st]);
+            }
+            L.rr[t][wave][lane] = accr[0];            /* lane (g 0, r): weight row 16 (rt0 + t) + r */
         }
-        L.rr[wave][lane] = accr[0];                   /* lane (g 0, r): weight row 16 b + r */
     }
     /* a workgroup that gave up waiting may read h codes not yet written:
      * its y (and add_out) columns are written as NaN */
@@ -3016,13 +3035,14 @@ __device__ __forceinline__ void apus_layer1_role(const ApusGemmArgs &a1, const A
         apus_gst<float>(a2.acc_y + oo, y);
         if (a2.add_out)
             apus_gst<float>(a2.add_out + oo, apus_bf16_rne(y + apus_gld<float>(a2.add_src + oo)));
-    } else if (rd && threadIdx.x < 32) {
-        /* the rider's row 16 b + i: bf16 of the 8 K-slice sums in order */
-        const int i = threadIdx.x - 16;
-        float v = L.rr[0][i];
+    } else if (rd && RT > 0 && threadIdx.x < 16 + 16 * RT) {
+        /* the rider's row 16 (rt0 + t) + i: bf16 of the 8 K-slice sums in
+         * order */
+        const int t = (threadIdx.x - 16) >> 4, i = (threadIdx.x - 16) & 15;
+        float v = L.rr[t][0][i];
 #pragma unroll
-        for (int w = 1; w < 8; ++w) v += L.rr[w][i];
-        apus_gst<float>(a1.rdout + (size_t)b * 16 + i, apus_bf16_rne(v));
+        for (int w = 1; w < 8; ++w) v += L.rr[t][w][i];
+        apus_gst<float>(a1.rdout + (size_t)(rt0 + t) * 16 + i, apus_bf16_rne(v));
     }
 }
 
