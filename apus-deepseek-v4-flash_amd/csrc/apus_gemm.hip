@@ -1834,7 +1834,6 @@ void apus_launch_split(const ApusGemmArgs &a, hipStream_t st) {
 template <int WF, int NQ, int NW, int MR>
 __global__ __launch_bounds__(NW * 64) void apus_gemv_grp_kernel(ApusGemmArgs args) {
     constexpr int K = NQ * 128, NG = NQ / NW;
-    constexpr int QB = WF == APUS_W_FP4 ? 1024 : 2048;        /* weight bytes per group */
     static_assert(NQ % NW == 0 && NG * 16 <= 128 && NG % 4 == 0, "grouped GEMV shape");
     __shared__ apus_v4f red[NW][64];
     /* MR: rows an entry may have (1 or 8) */
@@ -1890,7 +1889,6 @@ __global__ __launch_bounds__(NW * 64) void apus_gemv_grp_kernel(ApusGemmArgs arg
         b0[i] = apus_ld16_stream(wl.w + (size_t)(q0 + i) * wl.qs);
         if constexpr (WF == APUS_W_FP8) b1[i] = apus_ld16_stream(wl.w + (size_t)(q0 + i) * wl.qs + 1024);
     }
-    (void)QB;
     apus_v4u sc4[WF == APUS_W_FP4 ? NG / 4 : 1];
     unsigned sc1[WF == APUS_W_FP8 ? NG : 1];
     if constexpr (WF == APUS_W_FP4) {
