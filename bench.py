@@ -324,8 +324,10 @@ def bench_fp8(H, dev, steps, O=4096, K=4096):
 # ------------------------------------------------------------------ MoE (configs 2, 3)
 
 # the model's dense FP8 projections (reference/config.json: dim 4096, q_lora
-# 1024, 64 heads x 512, o_lora 1024 x 8 groups); name -> (O, K)
-ATTN_FP8 = {"wq_a": (1024, 4096), "wq_b": (32768, 1024), "wkv": (512, 4096), "wo_b": (4096, 8192)}
+# 1024, 64 heads x 512, o_lora 1024 x 8 groups; the indexer's query
+# projection 64 index heads x 128, c/attn.h:1116); name -> (O, K)
+ATTN_FP8 = {"wq_a": (1024, 4096), "wq_b": (32768, 1024), "wkv": (512, 4096), "wo_b": (4096, 8192),
+            "idx_wq_b": (8192, 1024)}
 
 
 def bench_attn_fp8(H, dev, steps=64, M=1, tiled=True):
