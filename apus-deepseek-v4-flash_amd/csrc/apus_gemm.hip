@@ -1656,7 +1656,9 @@ bool apus_launch_narrow(const ApusGemmArgs &a, hipStream_t st) {
  * elements a lane, one live row in 16) cost ~8 us of SIMD time at
  * [4096, 8192]. Only lanes of rows below M read activation fragments (rows
  * past M are zero and not stored): lanes loading the same address still cost
- * the address unit a lane each.
+ * the address unit a lane each. (Codes fetched with one load per 8 / NG rows
+ * into the LDS slot instead, as the grouped GEMV does: FP8 [4096, 4096] at
+ * M = 1 5.05-5.08 against 5.02-5.04 us, so the fragment loads stay.)
  * Sums: each wave one chain over its groups, the waves added in order in
  * LDS. Splitting a tile over 2-8 workgroups (partial sums through
  * device-coherent stores and a ticket, the last workgroup adding them in
