@@ -1637,9 +1637,11 @@ bool apus_launch_narrow(const ApusGemmArgs &a, hipStream_t st) {
 }
 
 /*
- * Split-K GEMV for dense FP8 launches with at most 8 rows on tiled weights
- * (the attention's wq_a [1024, 4096] and wkv [512, 4096] at decode, the
- * 4096-row projections at M = 1). The few-row schedule gives each 16-row
+ * Split-K GEMV for dense FP8 and MXFP4 launches with at most 8 rows on
+ * tiled weights (the attention's wq_a [1024, 4096] and wkv [512, 4096] at
+ * decode, the 4096-row projections at M = 1, one expert's MXFP4 linear:
+ * [2048, 4096] fp32 rows 4.1 against 5.0 us per kernel on the few-row
+ * schedule). The few-row schedule gives each 16-row
  * tile 4 waves that stream it through a 2-group register ring, so a
  * 512-row weight ran as long as a 1024-row one (4.7 us each): each wave's
  * 16 KB took that long. Here one workgroup of NW waves owns a tile, the
@@ -1665,10 +1667,10 @@ bool apus_launch_narrow(const ApusGemmArgs &a, hipStream_t st) {
  * order) measured slower at every size: wq_a 5.0-5.4 against 3.8 us, wkv
  * 4.8-5.6 against 3.7.
  */
-template <int NQ, int NW, int ASRC>
+template <int WF, int NQ, int NW, int ASRC>
 __global__ __launch_bounds__(NW * 64) void apus_gemv_split_kernel(ApusGemmArgs args) {
     constexpr int K = NQ * 128, NG = NQ / NW;
-    static_assert(NG >= 1 && NQ % NW == 0, "split shape");
+    static_assert(NG >= 1 && NQ % NW == 0 && (WF == APUS_W_FP8 || 4 % NG == 0 || NG % 4 == 0), "split shape");
     __shared__ apus_v4f red[NW][64];
     /* fp32 rows: the wave's codes [group][row][128] and scale bytes */
     __shared__ __align__(16) uint8_t lq[ASRC == APUS_A_F32 ? NW : 1][NG][8][128];
@@ -1680,8 +1682,10 @@ __global__ __launch_bounds__(NW * 64) void apus_gemv_split_kernel(ApusGemmArgs a
     const int r = lane & 15, g = lane >> 4;
     const int q0 = wave * NG;
     const bool live = r < M;
-    const uint8_t *bp = ent.w + ((size_t)tile * NQ * 128 + (size_t)q0 * 128 + lane) * 16;
-    const uint8_t *wsp = ent.ws + (size_t)(tile >> 3) * NQ + q0;
+    /* the wave's weight stream: FP8 groups of 2 KB (two 16-byte pieces a
+     * lane) with 128 x 128 tile scales; MXFP4 groups of 1 KB with the 16
+     * scale bytes of the lane's row per 512-slice */
+    const ApusWLane wl = apus_wlane<WF>(ent, true, tile * 16 + r, lane, K);
     /* issue order: activations (L2 hits), then the weight stream, then the
      * weight scales; nothing waits before the last load is out (the scale
      * bytes stay per-lane operands: a readfirstlane would wait for them) */
@@ -1714,15 +1718,27 @@ __global__ __launch_bounds__(NW * 64) void apus_gemv_split_kernel(ApusGemmArgs a
                 for (int i = 0; i < NG; ++i) xr[i][m] = apus_gld<float2>(xp + (size_t)m * K + i * 128);
             }
     }
-    apus_v4u b0[NG], b1[NG];
+    apus_v4u b0[NG], b1[WF == APUS_W_FP8 ? NG : 1];
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
-        b0[i] = apus_ld16_stream(bp + (size_t)i * 2048);
-        b1[i] = apus_ld16_stream(bp + (size_t)i * 2048 + 1024);
+        b0[i] = apus_ld16_stream(wl.w + (size_t)(q0 + i) * wl.qs);
+        if constexpr (WF == APUS_W_FP8) b1[i] = apus_ld16_stream(wl.w + (size_t)(q0 + i) * wl.qs + 1024);
     }
     int sb[NG];
+    if constexpr (WF == APUS_W_FP8) {
 #pragma unroll
-    for (int i = 0; i < NG; ++i) sb[i] = (int)apus_gld<uint8_t>(wsp + i);
+        for (int i = 0; i < NG; ++i) sb[i] = (int)apus_gld<uint8_t>(wl.s + q0 + i);
+    } else {
+        constexpr int NSL = NG < 4 ? 1 : NG / 4;              /* 512-slices of the wave */
+        apus_v4u sc4[NSL];
+#pragma unroll
+        for (int j = 0; j < NSL; ++j) sc4[j] = apus_gld<apus_v4u>(wl.s + (size_t)((q0 >> 2) + j) * wl.ss);
+#pragma unroll
+        for (int i = 0; i < NG; ++i) {
+            const int q = q0 + i;
+            sb[i] = (int)((sc4[(q >> 2) - (q0 >> 2)][q & 3] >> (8 * g)) & 0xffu);
+        }
+    }
     /* keep the scheduler from sinking the weight loads below the
      * quantisation (it would wait for the activations first) */
     __builtin_amdgcn_sched_barrier(0);
@@ -1761,9 +1777,14 @@ __global__ __launch_bounds__(NW * 64) void apus_gemv_split_kernel(ApusGemmArgs a
             }
             a = apus_v8i{(int)l4.x, (int)l4.y, (int)l4.z, (int)l4.w, (int)h4.x, (int)h4.y, (int)h4.z, (int)h4.w};
         }
-        const apus_v8i b = apus_v8i{(int)b0[i].x, (int)b0[i].y, (int)b0[i].z, (int)b0[i].w,
-                                    (int)b1[i].x, (int)b1[i].y, (int)b1[i].z, (int)b1[i].w};
-        acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, ea, sb[i]);
+        if constexpr (WF == APUS_W_FP8) {
+            const apus_v8i b = apus_v8i{(int)b0[i].x, (int)b0[i].y, (int)b0[i].z, (int)b0[i].w,
+                                        (int)b1[i].x, (int)b1[i].y, (int)b1[i].z, (int)b1[i].w};
+            acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E4M3, 0, 0>(a, b, acc, ea, sb[i]);
+        } else {
+            const apus_v8i b = apus_v8i{(int)b0[i].x, (int)b0[i].y, (int)b0[i].z, (int)b0[i].w, 0, 0, 0, 0};
+            acc = apus_mfma_scaled<APUS_FMT_E4M3, APUS_FMT_E2M1, 0, 0>(a, b, acc, ea, sb[i]);
+        }
     }
     if constexpr (NW > 1) {
         red[wave][lane] = acc;
@@ -1790,26 +1811,29 @@ __global__ __launch_bounds__(NW * 64) void apus_gemv_split_kernel(ApusGemmArgs a
  * wo_b / wq_b fp32-row linears, FP8 [4096, 4096] codes at M = 1): 1 group
  * 3.85 / 3.75 / 8.4 / 7.5 / 4.85; at most 2 (fp32) / 4 (codes) 3.85 / 3.77 /
  * 8.5 / 7.75 / 5.2; 4 groups for fp32 4.2 / 4.1 / 8.5 / 8.0 */
+#ifndef APUS_SPLIT_FP4
+#define APUS_SPLIT_FP4 1
+#endif
 #ifndef APUS_SPLIT_NG_CODES
 #define APUS_SPLIT_NG_CODES 1
 #endif
 #ifndef APUS_SPLIT_NG_F32
 #define APUS_SPLIT_NG_F32 1
 #endif
-template <int NQ, int ASRC>
+template <int WF, int NQ, int ASRC>
 void apus_launch_split_k(const ApusGemmArgs &a, hipStream_t st) {
     constexpr int NW0 = NQ / (ASRC == APUS_A_F32 ? APUS_SPLIT_NG_F32 : APUS_SPLIT_NG_CODES);
     constexpr int NW = NW0 < 1 ? 1 : NW0 > 16 ? 16 : NW0;
     static_assert(NQ / NW <= 4, "at most 4 groups a wave");
-    hipLaunchKernelGGL((apus_gemv_split_kernel<NQ, NW, ASRC>), dim3(a.O / 16), dim3(NW * 64), 0, st, a);
+    hipLaunchKernelGGL((apus_gemv_split_kernel<WF, NQ, NW, ASRC>), dim3(a.O / 16), dim3(NW * 64), 0, st, a);
 }
-template <int ASRC>
+template <int WF, int ASRC>
 void apus_launch_split(const ApusGemmArgs &a, hipStream_t st) {
     switch (a.K) {
-    case 1024: apus_launch_split_k<8, ASRC>(a, st); break;
-    case 2048: apus_launch_split_k<16, ASRC>(a, st); break;
-    case 4096: apus_launch_split_k<32, ASRC>(a, st); break;
-    default:   apus_launch_split_k<64, ASRC>(a, st); break;
+    case 1024: apus_launch_split_k<WF, 8, ASRC>(a, st); break;
+    case 2048: apus_launch_split_k<WF, 16, ASRC>(a, st); break;
+    case 4096: apus_launch_split_k<WF, 32, ASRC>(a, st); break;
+    default:   apus_launch_split_k<WF, 64, ASRC>(a, st); break;
     }
 }
 
@@ -3198,7 +3222,7 @@ bool apus_grp_on() {
     return on;
 }
 
-/* the split-K GEMV for few-row dense FP8 launches with few output rows
+/* the split-K GEMV for few-row dense FP8 / MXFP4 launches on tiled weights
  * (APUS_HIP_SPLIT=0 turns it off: the few-row schedule) */
 bool apus_split_on() {
     static const bool on = [] {
@@ -3250,14 +3274,20 @@ hipError_t apus_launch_gemm_few(int wfmt, const ApusGemmArgs *a, int n_ent, int 
         (n_ent > 2 || (n_ent == 2 && (a->ent1.a0 != a->ent0.a0 || a->ent1.arows != a->ent0.arows ||
                                       a->ent1.M != a->ent0.M))))
         return hipErrorInvalidValue;
-    /* one dense FP8 entry on tiled weights with few output rows: the
-     * split-K GEMV (unless a K split is forced) */
-    if (n_ent == 1 && !ks && !a->kchain && wfmt == APUS_W_FP8 && a->wtiled && !a->ents && !a->pidx &&
+    /* one dense FP8 / MXFP4 entry on tiled weights: the split-K GEMV
+     * (unless a K split is forced) */
+    if (n_ent == 1 && !ks && !a->kchain && (wfmt == APUS_W_FP8 || APUS_SPLIT_FP4) && a->wtiled && !a->ents &&
+        !a->pidx &&
         !a->acc_y && !a->add_out && !a->items && !a->hq && !a->rdout && !a->zero && !a->ent0.arows &&
         !a->ent0.orows && a->ent0.M <= 8 && (a->asrc == APUS_A_CODES || a->asrc == APUS_A_F32) &&
         apus_split_on() && !apus_dec_ks_forced()) {
-        if (a->asrc == APUS_A_CODES) apus_launch_split<APUS_A_CODES>(*a, st);
-        else                         apus_launch_split<APUS_A_F32>(*a, st);
+        if (wfmt == APUS_W_FP8) {
+            if (a->asrc == APUS_A_CODES) apus_launch_split<APUS_W_FP8, APUS_A_CODES>(*a, st);
+            else                         apus_launch_split<APUS_W_FP8, APUS_A_F32>(*a, st);
+        } else {
+            if (a->asrc == APUS_A_CODES) apus_launch_split<APUS_W_FP4, APUS_A_CODES>(*a, st);
+            else                         apus_launch_split<APUS_W_FP4, APUS_A_F32>(*a, st);
+        }
         return hipGetLastError();
     }
     if (!ks) ks = apus_dec_ks((size_t)n_ent * (a->O / 16));

@@ -1,11 +1,12 @@
 """Dense FP8 schedules on tiled weights, swept over their instances.
 
-The host FP8 entry points keep weights MFMA-tiled in the dense cache when K
+The host FP8 and MXFP4 entry points keep weights MFMA-tiled in the dense cache when K
 is 1024, 2048, 4096 or 8192 and O % 128 == 0, so these calls reach:
 
 * the split-K GEMV (at most 8 rows; one workgroup per 16-row weight tile,
-  16 waves or 8 at K = 1024 splitting K): codes through apus_hip_fp8_gemm,
-  fp32 rows quantised in the kernel through apus_hip_fp8_linear;
+  16 waves or 8 at K = 1024 splitting K), FP8 and MXFP4 weights: codes
+  through apus_hip_fp8_gemm / apus_hip_fp4_gemm, fp32 rows quantised in the
+  kernel through apus_hip_fp8_linear / apus_hip_fp4_linear;
 * the narrow schedule (9..64 rows; 1, 2 or 4 token tiles, 4 waves splitting
   K in quarters).
 
@@ -37,6 +38,23 @@ def test_narrow_instances(hip, oracle, rng, M, K):
     truth, esc = oracle.fp8_truth(w, ws, c, s)
     assert max_rel(got, oracle.fp8_gemm(w, ws, c, s)) <= 1e-3
     assert err_esc(got, truth, esc) <= 1e-4
+
+
+@pytest.mark.parametrize("K", KS)
+@pytest.mark.parametrize("M", (1, 2, 5, 8))
+def test_split_instances_fp4(hip, oracle, rng, M, K):
+    """MXFP4 weights on the split-K GEMV: codes and fp32 rows."""
+    O = 384
+    w, ws = fp4_weights(rng, O, K)
+    x = acts(rng, M, K, 2.0)
+    c, s = oracle.act_quant(x)
+    got = hip.fp4_gemm(w, ws, c, s)
+    unrounded = oracle.fp4_gemm(w, ws, c, s)
+    truth, esc = oracle.fp4_truth(w, ws, c, s)
+    assert max_rel(got, unrounded) <= 1e-3
+    assert err_esc(got, truth, esc) <= 1e-4
+    lin = hip.fp4_linear(w, ws, x)
+    assert bf16_linear_ok(lin, unrounded, 1e-4 * np.abs(unrounded).max()).all()
 
 
 @pytest.mark.parametrize("K", KS)

@@ -190,10 +190,10 @@ def test_tiled_grouped_few_rows(hip, oracle, rng, fmt, O, K, Ms):
                                        (1, 8, 1024, 8192), (0, 1, 512, 1024)])
 def test_tiled_linear_dev(hip, oracle, rng, fmt, M, O, K):
     """apus_hip_linear_dev on tiled weights equals the row-major linear bit
-    for bit (the same schedule for the same M), except FP8 up to 64 rows
-    (the split-K GEMV and the narrow schedule, which read tiled weights
-    only: another fp32 summation order, so the BF16 outputs are held to the
-    oracle's linear bar)."""
+    for bit (the same schedule for the same M), except where tiled weights
+    take a schedule of their own — the split-K GEMV (FP8 and MXFP4, up to 8
+    rows) and the narrow schedule (FP8, 9..64 rows): another fp32 summation
+    order, so the BF16 outputs are held to the oracle's linear bar."""
     L = hip.lib()
     w, ws = (fp4_weights if fmt == 0 else fp8_weights)(rng, O, K)
     x = acts(rng, M, K)
@@ -208,9 +208,9 @@ def test_tiled_linear_dev(hip, oracle, rng, fmt, M, O, K):
                                          wsp.ptr), "linear")
         hip._check(L.apus_hip_synchronize(), "sync")
         outs.append(do.to_array(np.float32, (M, O)).copy())
-    if fmt == 1 and M <= 64:
+    if M <= 8 or (fmt == 1 and M <= 64):
         c, s = oracle.act_quant(x)
-        unrounded = oracle.fp8_gemm(w, ws, c, s)
+        unrounded = (oracle.fp4_gemm if fmt == 0 else oracle.fp8_gemm)(w, ws, c, s)
         assert bf16_linear_ok(outs[1], unrounded, 1e-4 * np.abs(unrounded).max()).all()
         return
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
