@@ -14,8 +14,9 @@ Cases (all seeded, the same in every run):
   12-entry MXFP4 [2048, 4096] grouped GEMV; dense tile-schedule launches:
   FP8 GEMMs of 100 x 512 x 4096 and 70 x 384 x 2048, and of 48, 12 and 29
   rows (the narrow schedule); split-K GEMV launches: FP8 GEMMs of 3 x 512 x
-  4096 and 1 x 1024 x 8192 and a 4-row fp32 linear 512 x 4096 (inputs saved
-  for the oracle).
+  4096 and 1 x 1024 x 8192 and a 4-row fp32 linear 512 x 4096, MXFP4 GEMMs
+  of 2 x 384 x 4096 and a 4-row fp32 linear 2048 x 4096 (inputs saved for
+  the oracle).
 """
 import ctypes as C
 import os
@@ -87,6 +88,16 @@ def dense(rng, out):
     x = acts(rng, 4, 4096)
     out["l1_w"], out["l1_ws"], out["l1_x"] = w, ws, x
     out["l1_y"] = hip.fp8_linear(w, ws, x)
+    # the same on MXFP4 weights: codes in (2 x 384 x 4096) and an fp32-row
+    # linear (4 x 2048 x 4096)
+    w, ws = fp4_weights(rng, 384, 4096)
+    c, sc = hip.act_quant(acts(rng, 2, 4096))
+    out["f1_w"], out["f1_ws"], out["f1_c"], out["f1_s"] = w, ws, c, sc
+    out["f1_y"] = hip.fp4_gemm(w, ws, c, sc)
+    w, ws = fp4_weights(rng, 2048, 4096)
+    x = acts(rng, 4, 4096)
+    out["l2_w"], out["l2_ws"], out["l2_x"] = w, ws, x
+    out["l2_y"] = hip.fp4_linear(w, ws, x)
     for i, y in enumerate(hip.fp4_gemm_grouped(ents, c4, s4, 2048)):
         out[f"fp4_y{i}"] = y
 

@@ -21,9 +21,9 @@ outputs with a child run without switches:
   per output over the 128-groups in order, so the dense outputs must be
   bit-identical too; APUS_HIP_NARROW=0 (9..64-row dense FP8 GEMMs on the
   tile schedule instead of the narrow one, which splits K in four): those
-  outputs held to the oracle's bars; APUS_HIP_SPLIT=0 (FP8 launches of at
-  most 8 rows on tiled weights on the few-row schedule instead of the
-  split-K GEMV, another K split): those outputs held to the oracle's bars;
+  outputs held to the oracle's bars; APUS_HIP_SPLIT=0 (FP8 and MXFP4
+  launches of at most 8 rows on tiled weights on the few-row schedule
+  instead of the split-K GEMV, another K split): those outputs held to the oracle's bars;
   APUS_HIP_GRP=0 (grouped launches of few-row entries on tiled weights on
   the few-row schedule instead of the grouped GEMV): the grouped MXFP4
   outputs held to the oracle's bars;
@@ -112,10 +112,10 @@ def test_switch(oracle, tmp_path, default_run, env):
     if var != "APUS_HIP_DEC_KS":
         for k in keys:
             assert _same(got[k], base[k]), k
-    for name in ("t1", "t2", "t3", "t4", "t5", "t6", "t7", "l1"):
+    for name in ("t1", "t2", "t3", "t4", "t5", "t6", "t7", "l1", "f1", "l2"):
         if var == "APUS_HIP_NARROW" and name in ("t3", "t4", "t5"):
             continue    # another K split: held to the oracle's bars below
-        if split and name in ("t6", "t7", "l1"):
+        if split and name in ("t6", "t7", "l1", "f1", "l2"):
             continue
         y = got[f"{name}_y"]
         assert _same(y, base[f"{name}_y"]), f"{var}={val}: {name} differs from the default schedule"
@@ -129,6 +129,12 @@ def test_switch(oracle, tmp_path, default_run, env):
         args = (got[f"{name}_w"], got[f"{name}_ws"], got[f"{name}_c"], got[f"{name}_s"])
         truth, esc = oracle.fp8_truth(*args)
         assert max_rel(y, oracle.fp8_gemm(*args)) <= 1e-3 and err_esc(y, truth, esc) <= 1e-4, name
+    args = (got["f1_w"], got["f1_ws"], got["f1_c"], got["f1_s"])
+    truth, esc = oracle.fp4_truth(*args)
+    assert max_rel(got["f1_y"], oracle.fp4_gemm(*args)) <= 1e-3 and err_esc(got["f1_y"], truth, esc) <= 1e-4
+    c, s = oracle.act_quant(got["l2_x"])
+    unrounded = oracle.fp4_gemm(got["l2_w"], got["l2_ws"], c, s)
+    assert bf16_linear_ok(got["l2_y"], unrounded, 1e-4 * np.abs(unrounded).max()).all()
     want = oracle.fp8_gemm(got["fp8_w"], got["fp8_ws"], got["fp8_c"], got["fp8_s"])
     truth, esc = oracle.fp8_truth(got["fp8_w"], got["fp8_ws"], got["fp8_c"], got["fp8_s"])
     assert max_rel(got["fp8_y"], want) <= 1e-3
