@@ -1375,7 +1375,7 @@ __global__ __launch_bounds__(512, 1) void apus_gemm_lds_kernel(ApusGemmArgs args
         if (ii < LA) {
             const int lr = 8 * ii + (lane >> 3), p = lane & 7;
             const int row = ent.a0 + (m0 + lr < M ? m0 + lr : M - 1);
-            const int sw = ((lr & 15) ^ ((lr & 15) >> 3)) & 7;
+            const int sw = apus_row_swz(lr);
             src[u] = args.acodes + (size_t)row * K + (p ^ sw) * 16;
             dst[u] = ii * 1024;
             qs[u] = 128;
@@ -1408,7 +1408,7 @@ __global__ __launch_bounds__(512, 1) void apus_gemm_lds_kernel(ApusGemmArgs args
     for (int i = 0; i < 4; ++i) acc[i] = apus_v4f{0.f, 0.f, 0.f, 0.f};
     struct Frag { apus_v8i a, b[4]; int sa; };
     const int arow = wm * 16 + r;
-    const int sw = (r ^ (r >> 3)) & 7;
+    const int sw = apus_row_swz(r);
     auto read_frag = [&](Frag &f, int q) {
         const uint8_t *stg = lds + (q % NST) * STB;
 #pragma unroll
@@ -1514,7 +1514,7 @@ __global__ __launch_bounds__(256) void apus_gemm_narrow_kernel(ApusGemmArgs args
         for (int hh = 0; hh < 2; ++hh) {
             const int lr = 8 * hh + (lane >> 3);
             const int rw = ent.a0 + (16 * t + lr < M ? 16 * t + lr : M - 1);
-            const int sw = (lr ^ (lr >> 3)) & 7;
+            const int sw = apus_row_swz(lr);
             lp[2 * t + hh] = args.acodes + (size_t)rw * K + ((lane & 7) ^ sw) * 16;
         }
     }
@@ -1553,7 +1553,7 @@ __global__ __launch_bounds__(256) void apus_gemm_narrow_kernel(ApusGemmArgs args
     apus_v4f acc[TM];
 #pragma unroll
     for (int t = 0; t < TM; ++t) acc[t] = apus_v4f{0.f, 0.f, 0.f, 0.f};
-    const int sw = (r ^ (r >> 3)) & 7;
+    const int sw = apus_row_swz(r);
 #pragma unroll
     for (int i = 0; i < NG; ++i) {
         Grp &cur = ring[i % PD];
@@ -2056,7 +2056,7 @@ __global__ __launch_bounds__(512, 2) void apus_gemm_prefill_lds_kernel(ApusGemmA
      * lane -> row 8 wave + lane / 8, LDS slot lane % 8 holding 16-byte chunk
      * (lane % 8) ^ swizzle(row)) and weight tile `wave` */
     const int alr = 8 * wave + (lane >> 3);
-    const int asw = ((alr & 15) ^ ((alr & 15) >> 3)) & 7;
+    const int asw = apus_row_swz(alr);
     const uint8_t *asrc = args.acodes + (size_t)arow_of(alr) * K + ((lane & 7) ^ asw) * 16;
     const uint8_t *bsrc = ent.w + ((size_t)((n0 >> 4) + wave) * NQ) * 1024 + lane * 16;
     auto issue = [&](int q, int slot) {
@@ -2090,7 +2090,7 @@ __global__ __launch_bounds__(512, 2) void apus_gemm_prefill_lds_kernel(ApusGemmA
     }
     const bool live = wm * 16 < rows;                          /* wave-uniform */
     const int arow = wm * 16 + r;
-    const int sw = (r ^ (r >> 3)) & 7;
+    const int sw = apus_row_swz(r);
     struct Frag { apus_v8i a; apus_v4u b[4]; int sa; unsigned sb[4]; };
     auto read_frag = [&](Frag &f, int q) {
         const uint8_t *stg = lds + (q % NST) * STB;
