@@ -604,10 +604,105 @@ __global__ __launch_bounds__(256) void apus_wgemv_kernel(const void *__restrict_
     }
 }
 
+/* One x row against BF16 weights with K = 512 NS (the LM head at dim 4096;
+ * c/model.h:585-647 apus_head_gemv, c/attn.h:600-666 apus_bf16_linear):
+ * x is staged once per workgroup in LDS (fp32, BF16-rounded first with flag
+ * 1), so each wave reads it from there for its NR rows instead of from L2
+ * (the general kernel reads the 16 KB row once per 4 weight rows: half as
+ * many bytes again as the weights, through L2). Lane l takes elements
+ * 8 l .. 8 l + 7 of each 512-step (one 16-byte load per row, streamed, a
+ * ring PD steps deep); x sits in LDS as [step][half][lane][4] so its two
+ * 16-byte reads per step are contiguous over the lanes. Lane partials meet
+ * in a fixed xor-shuffle tree, as in apus_wgemv_kernel (within FP32
+ * summation error of the CPU's sequential sums, not bitwise). */
+template <int NS, int NR, int PD>
+__global__ __launch_bounds__(256) void apus_head_kernel(const uint16_t *__restrict__ w,
+                                                        const float *__restrict__ x,
+                                                        float *__restrict__ out, int O, int flags) {
+    constexpr int K = NS * 512;
+    __shared__ __align__(16) float hx[K];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int o0 = (blockIdx.x * 4 + wave) * NR;
+    /* x first (L2 hits), then the weight ring */
+    float4 xv[K / 1024];
+#pragma unroll
+    for (int j = 0; j < K / 1024; ++j) xv[j] = apus_gld<float4>(x + (size_t)(threadIdx.x + 256 * j) * 4);
+    /* 32-bit byte offsets from the (uniform) weight base: one VGPR a row
+     * (O K 2 < 4 GiB is checked by the launcher) */
+    const uint8_t *wb = reinterpret_cast<const uint8_t *>(w);
+    unsigned wo[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) wo[r] = (unsigned)min(o0 + r, O - 1) * (unsigned)(K * 2) + (unsigned)lane * 16u;
+    apus_v4u ring[PD][NR];
+#pragma unroll
+    for (int u = 0; u < PD; ++u)
+#pragma unroll
+        for (int r = 0; r < NR; ++r) ring[u][r] = apus_ld16_stream(wb + (wo[r] + u * 1024u));
+#pragma unroll
+    for (int j = 0; j < K / 1024; ++j) {
+        float4 v = xv[j];
+        if (flags & 1) {
+            v.x = apus_bf16_rne(v.x); v.y = apus_bf16_rne(v.y);
+            v.z = apus_bf16_rne(v.z); v.w = apus_bf16_rne(v.w);
+        }
+        const int e = (threadIdx.x + 256 * j) * 4;          /* element of x */
+        const int st = e >> 9, l = (e & 511) >> 3, h = (e >> 2) & 1;
+        *reinterpret_cast<float4 *>(&hx[((st * 2 + h) * 64 + l) * 4]) = v;
+    }
+    apus_lds_barrier();
+    float acc[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+        const float4 a = *reinterpret_cast<const float4 *>(&hx[((st * 2) * 64 + lane) * 4]);
+        const float4 b = *reinterpret_cast<const float4 *>(&hx[((st * 2 + 1) * 64 + lane) * 4]);
+        const float xe[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        apus_v4u (&cur)[NR] = ring[st % PD];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const unsigned q[4] = {cur[r].x, cur[r].y, cur[r].z, cur[r].w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                acc[r] = __builtin_fmaf(__uint_as_float(q[i] << 16), xe[2 * i], acc[r]);
+                acc[r] = __builtin_fmaf(__uint_as_float(q[i] & 0xffff0000u), xe[2 * i + 1], acc[r]);
+            }
+        }
+        /* the step's FMAs stay here (sunk to the reduction, they kept every
+         * step's weights live) */
+#pragma unroll
+        for (int r = 0; r < NR; ++r) asm volatile("" : "+v"(acc[r]));
+        if (st + PD < NS) {
+#pragma unroll
+            for (int r = 0; r < NR; ++r) cur[r] = apus_ld16_stream(wb + (wo[r] + (st + PD) * 1024u));
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        float v = acc[r];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+        if (lane == 0 && o0 + r < O) out[o0 + r] = (flags & 2) ? apus_bf16_rne(v) : v;
+    }
+}
+
 hipError_t apus_launch_wgemv(const void *w, const float *x, float *out, int M, int K, int O,
                              int flags, hipStream_t st) {
     if (M <= 0 || O <= 0) return hipSuccess;
     if (K <= 0 || K % 8) return hipErrorInvalidValue;
+    /* one x row, BF16 weights, K 2048 / 4096 / 8192: x staged in LDS, 4
+     * rows a wave, a ring 4 steps deep (LM head [129280, 4096]: 154-158
+     * against 176 us for the general kernel; 8 rows a wave or rings of 3, 6,
+     * 8 steps 157-161 us) */
+    if (M == 1 && (flags & 4) && (K == 2048 || K == 4096 || K == 8192) && (size_t)O * K * 2 < (1ull << 32)) {
+        constexpr int NR = 4, PD = 4;
+        const dim3 grid((O + 4 * NR - 1) / (4 * NR));
+        const uint16_t *wh = (const uint16_t *)w;
+        if (K == 2048)      hipLaunchKernelGGL((apus_head_kernel<4, NR, PD>), grid, dim3(256), 0, st, wh, x, out, O, flags);
+        else if (K == 4096) hipLaunchKernelGGL((apus_head_kernel<8, NR, PD>), grid, dim3(256), 0, st, wh, x, out, O, flags);
+        else                hipLaunchKernelGGL((apus_head_kernel<16, NR, PD>), grid, dim3(256), 0, st, wh, x, out, O, flags);
+        return hipGetLastError();
+    }
     const unsigned gx = (O + 4 * APUS_WG_NR - 1) / (4 * APUS_WG_NR);
     const dim3 block(256);
     if (M == 1) {       /* decode (the LM head): accumulators for one x row */

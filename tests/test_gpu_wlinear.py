@@ -40,14 +40,17 @@ def _check(got, oracle, w, x, flags):
 
 
 @pytest.mark.parametrize("M,K,O,flags", [(1, 4096, 256, 0), (3, 4096, 1000, 3), (1, 4096, 1024, 6),
-                                         (8, 1000, 77, 0), (20, 512, 64, 3), (2, 8, 5, 4)])
+                                         (8, 1000, 77, 0), (20, 512, 64, 3), (2, 8, 5, 4),
+                                         (1, 4096, 333, 7), (1, 2048, 70, 5), (1, 8192, 129, 6),
+                                         (1, 1024, 40, 4)])
 def test_f32_linear_hook(hip, oracle, rng, M, K, O, flags):
     w, x = _data(rng, M, K, O, flags & 4)
     got = hip.f32_linear(w, x, flags)
     _check(got, oracle, w, x, flags)
 
 
-@pytest.mark.parametrize("bf16w,O,K", [(True, 4999, 4096), (False, 300, 2048)])
+@pytest.mark.parametrize("bf16w,O,K", [(True, 4999, 4096), (False, 300, 2048), (True, 1027, 2048),
+                                       (True, 515, 8192)])
 def test_head_gemv_hook(hip, oracle, rng, bf16w, O, K):
     w, x = _data(rng, 1, K, O, bf16w)
     got = hip.head_gemv(w, x[0])
