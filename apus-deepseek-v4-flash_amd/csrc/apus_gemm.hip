@@ -464,8 +464,16 @@ __device__ __forceinline__ void apus_stage_quant(const ApusGemmArgs &a, const Ap
     if (sub == 0) lsc[r.row * NQ + r.q] = (uint8_t)e;
 }
 
+/* the K-quarter-order instance at K = 2048 (the routed few-row w2) held to 4
+ * waves per SIMD: 126 VGPRs, no spills (unconstrained 126 + 16 AGPRs, 3
+ * waves); config 2 443-445 -> 434-441 us, the 64-token sublayer 456-461 ->
+ * 446-454 us (same box, alternating) */
+#ifndef APUS_DEC_FOLD_WPE
+#define APUS_DEC_FOLD_WPE 4
+#endif
 template <int WF, int R, int NS, int PD, int KS, int ASRC, bool FOLD>
-__global__ __launch_bounds__(APUS_DEC_NT) void apus_gemm_decode_kernel(ApusGemmArgs args) {
+__global__ __launch_bounds__(APUS_DEC_NT)
+__attribute__((amdgpu_waves_per_eu(FOLD && NS == 4 ? APUS_DEC_FOLD_WPE : 1))) void apus_gemm_decode_kernel(ApusGemmArgs args) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int last_ticket;
     constexpr int K = NS * 512, NQ = NS * 4, K16 = K / 16, LDK = K + 32;
