@@ -80,3 +80,24 @@ def test_f32_linear_rejects_ragged_k(hip, rng):
     rc = L.apus_hip_f32_linear(w.ctypes.data, x.ctypes.data_as(hip.f32p),
                                out.ctypes.data_as(hip.f32p), 1, 12, 4, 0)
     assert rc != 0
+
+
+def test_head_gemv_full_size(hip, oracle):
+    """The LM head at the model's shape, BF16 [129280, 4096] (1.06 GB):
+    every output row against the oracle would take the CPU minutes, so the
+    first and last 256 rows (the last workgroup covers a partial 16-row
+    block: 129280 = 16 * 8080) and 1024 seeded rows in between are checked,
+    each output row depending on its own weight row only."""
+    O, K = 129280, 4096
+    rng = np.random.default_rng(17)
+    # BF16 bits of N(0, 1/K) weights, generated in blocks to bound host memory
+    w = np.empty((O, K), np.uint16)
+    for r0 in range(0, O, 16384):
+        r1 = min(O, r0 + 16384)
+        blk = (rng.standard_normal((r1 - r0, K), dtype=np.float32) / np.float32(64.0))
+        w[r0:r1] = (blk.view(np.uint32) >> 16).astype(np.uint16)
+    x = (rng.standard_normal(K) * 2).astype(np.float32)
+    got = hip.head_gemv(w, x)
+    rows = np.unique(np.concatenate([np.arange(256), np.arange(O - 256, O),
+                                     rng.choice(O, 1024, replace=False)]))
+    _check(got[None, rows], oracle, w[rows], x[None, :], 4)
